@@ -1,0 +1,167 @@
+/*
+ * seedplane_hip.h - C ABI of the MI355X (gfx950) Qwen2 decode / speculative-verify library.
+ *
+ * The library is a plain C ABI over hand-written HIP kernels: no torch types cross it.  Pointers named *_dev are
+ * device pointers (e.g. a torch tensor's data_ptr()); every other pointer is host memory owned by the caller.
+ * Every entry point returns an int status (SP_OK == 0).  On failure, sp_engine_last_error() (engine calls) or
+ * sp_last_error() (calls without an engine) returns a message that stays valid until the next failing call.
+ *
+ * Threading: one engine is driven by one host thread on one HIP stream; calls on one engine are not thread-safe,
+ * matching the single-threaded reference engines (seedplane/qwen_engine.py:32, native/vulkan_decode/qwen_vk.cpp:92).
+ *
+ * Each declaration names the reference interface it replaces (paths relative to the reference repository).
+ */
+#ifndef SEEDPLANE_HIP_H
+#define SEEDPLANE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status codes */
+enum {
+    SP_OK = 0,
+    SP_EINVAL = 1,      /* bad argument (maps to ValueError in Python)          */
+    SP_ENOMEM = 2,      /* device allocation failed                              */
+    SP_EHIP = 3,        /* a HIP runtime call failed (maps to RuntimeError)      */
+    SP_ESTATE = 4,      /* call out of order, e.g. forward before weights loaded */
+    SP_ECAPACITY = 5    /* KV slots / token count exceeded (ValueError)          */
+};
+
+/* ---------------------------------------------------------------- weight formats (canonical host layouts)
+ * SP_FMT_F16: fp16 row-major [rows][cols].
+ * SP_FMT_Q8 : int8 codes row-major [rows][cols] + fp16 scales [rows][cols/32]; w = code * scale (blocks of 32
+ *             along K, symmetric).
+ * SP_FMT_Q4 : uint8 packed codes [rows][cols/2] (byte j: k=2j in the low nibble, k=2j+1 in the high nibble,
+ *             codes 0..15) + fp16 scales [rows][cols/32] + fp16 zeros [rows][cols/32];
+ *             w = (code - zero) * scale (groups of 32 along K).
+ * SP_FMT_F32: fp32 row-major; accepted for norms and biases only. */
+enum { SP_FMT_F32 = 0, SP_FMT_F16 = 1, SP_FMT_Q8 = 2, SP_FMT_Q4 = 3 };
+
+/* ---------------------------------------------------------------- tensor kinds for sp_engine_load
+ * The fused matrices follow the reference's inference packing (seedplane/qwen_engine.py:64-80):
+ * QKV = cat(q_proj, k_proj, v_proj) rows, QKV_BIAS = cat of the biases, GATE_UP = cat(gate_proj, up_proj) rows. */
+enum {
+    SP_T_EMBED = 0,       /* [vocab][hidden]                                     */
+    SP_T_HEAD = 1,        /* [vocab][hidden]; omit when the head is tied         */
+    SP_T_FINAL_NORM = 2,  /* fp32 [hidden]                                       */
+    SP_T_IN_NORM = 3,     /* fp32 [hidden], per layer                            */
+    SP_T_POST_NORM = 4,   /* fp32 [hidden], per layer                            */
+    SP_T_QKV = 5,         /* [(heads + 2*kv_heads)*head_dim][hidden], per layer  */
+    SP_T_QKV_BIAS = 6,    /* fp32 [(heads + 2*kv_heads)*head_dim], per layer     */
+    SP_T_O = 7,           /* [hidden][heads*head_dim], per layer                 */
+    SP_T_GATE_UP = 8,     /* [2*intermediate][hidden], per layer                 */
+    SP_T_DOWN = 9         /* [hidden][intermediate], per layer                   */
+};
+
+/* ---------------------------------------------------------------- forward flags */
+enum {
+    SP_F_LOGITS = 1,      /* run the final norm + LM head and produce fp32 logits for every column   */
+    SP_F_ARGMAX = 2,      /* also produce the greedy id per column (first index on ties)             */
+    SP_F_GRAPH = 4        /* capture the step into a hipGraph on first use and replay it afterwards  */
+};
+
+typedef struct sp_model_desc {
+    int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate, vocab;
+    int32_t weight_format;   /* SP_FMT_F16 / SP_FMT_Q8 / SP_FMT_Q4 for every projection, embed and head      */
+    int32_t tied_head;       /* 1: the LM head is the embedding matrix (seedplane/qwen_engine.py:142)        */
+    int32_t max_tokens;      /* most columns (batch rows + tree nodes) one sp_engine_forward call may carry  */
+    float rms_eps;
+    float reserved0;
+    const float *inv_freq;   /* head_dim/2 RoPE inverse frequencies, fp32, computed as qwen_engine.py:52     */
+} sp_model_desc;
+
+/* One column of a forward call: a token, the KV cache (sequence) it belongs to and what it attends to.
+ * Visible keys = ring positions [ctx_lo, ctx_hi] (slot = position mod n_slots) followed by the tree block:
+ * slots (tree_base + j) mod n_slots for j < tree_count whose bit j is set in tree_mask.  The token's own K/V is
+ * written to `slot` before attention, so a plain decode column has ctx_hi == pos and slot == pos mod n_slots.
+ * This is the (slot range, positions) contract of the reference attention (native/vulkan_decode/shaders/
+ * attn_part.comp:18, rope_kv.comp:16,25) generalised with an ancestor mask for tree verification. */
+typedef struct sp_token {
+    int32_t token;
+    int32_t seq;
+    int32_t pos;          /* RoPE position (qwen_engine.py:99-103, 115)  */
+    int32_t slot;         /* KV slot this column writes                  */
+    int32_t ctx_lo, ctx_hi;
+    int32_t tree_base, tree_count;
+    uint64_t tree_mask;
+} sp_token;
+
+typedef struct sp_engine sp_engine;
+
+/* Replaces Qwen2Engine.__init__ (seedplane/qwen_engine.py:35-63) and Engine::init's shape checks
+ * (native/vulkan_decode/qwen_vk.cpp:283-308).  Shapes are general: any head_dim in {64, 128}, hidden and
+ * intermediate multiples of 128, any vocab. */
+int sp_engine_create(const sp_model_desc *desc, sp_engine **out);
+void sp_engine_destroy(sp_engine *e);
+const char *sp_engine_last_error(const sp_engine *e);
+/* Last error of a call that has no engine (create, sp_op_*), per host thread. */
+const char *sp_last_error(void);
+
+/* Use `hip_stream` (a hipStream_t, e.g. torch.cuda.current_stream().cuda_stream) for every later call. */
+int sp_engine_set_stream(sp_engine *e, void *hip_stream);
+
+/* Replaces the weight upload of Engine::init (qwen_vk.cpp:311-322) and the fused packing of Qwen2Engine.__init__
+ * (qwen_engine.py:64-80).  Host buffers in the canonical layout of `fmt`; the library re-tiles them for the
+ * kernels and copies them to HBM.  `layer` is ignored for the global kinds. */
+int sp_engine_load(sp_engine *e, int32_t kind, int32_t layer, int32_t fmt, int32_t rows, int32_t cols,
+                   const void *data, const void *scales, const void *zeros);
+
+/* Replaces KVCache.allocate / Qwen2Engine.new_cache (qwen_engine.py:25-29, 82-85) and the window buffers of
+ * Engine::init (qwen_vk.cpp:314-316).  Allocates fp16 K and V for `n_seq` sequences x `n_slots` ring slots for
+ * every layer (layout [layer][seq][kv_head][slot][head_dim]).  Re-reserving frees the previous cache. */
+int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots);
+
+/* Replaces Qwen2Engine.forward (qwen_engine.py:105-144) and the recorded one-token / K/V-batch command buffers
+ * (qwen_vk.cpp:374-437).  Runs `n` columns (any mix of sequences) through every layer.  Without SP_F_LOGITS the
+ * call is K/V-only: the last layer stops after writing its K/V (qwen_vk.cpp:426).  logits_dev, when not NULL,
+ * receives fp32 [n][vocab]; argmax_host, when not NULL (requires SP_F_ARGMAX), receives the greedy ids and the call
+ * waits for the stream. */
+int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t flags, float *logits_dev,
+                      int32_t *argmax_host);
+
+/* Device pointer to the engine's fp32 logits buffer [max_tokens][vocab] holding the last SP_F_LOGITS call. */
+int sp_engine_logits(sp_engine *e, float **logits_dev);
+
+/* Replaces the KV rollback by `cache.length = ...` (experiments/hive_scaling/benchmark_speculative.py:119,127) and
+ * the slot copies of copy_slots (qwen_vk.cpp:441-451): for every layer copies K/V of slot src[i] to dst[i] of
+ * sequence `seq`, in order i = 0..n-1 (tree compaction after acceptance). */
+int sp_engine_kv_move(sp_engine *e, int32_t seq, int32_t n, const int32_t *src_slots, const int32_t *dst_slots);
+
+/* Wait for all work queued by the engine. */
+int sp_engine_sync(sp_engine *e);
+
+/* Bytes of HBM the engine holds for weights / KV (for roofline accounting). */
+int sp_engine_bytes(const sp_engine *e, uint64_t *weight_bytes, uint64_t *kv_bytes);
+
+/* ---------------------------------------------------------------- standalone operators */
+
+/* Replaces the greedy branch of Qwen2Engine.sample (qwen_engine.py:147-148) and argmax.comp: two-pass
+ * wavefront argmax over each row of logits_dev [rows][cols] (fp32), first index on ties, into out_dev (int32).
+ * workspace_dev must hold sp_op_argmax_workspace(rows, cols) bytes. */
+size_t sp_op_argmax_workspace(int32_t rows, int32_t cols);
+int sp_op_argmax(const float *logits_dev, int32_t rows, int32_t cols, int32_t *out_dev, void *workspace_dev,
+                 void *hip_stream);
+
+/* A packed projection matrix in HBM, for kernel-level tests and roofline measurement of the GEMV alone.
+ * Replaces the per-matrix path of F.linear (qwen_engine.py:121,136,138-139,143) and gemv.comp. */
+typedef struct sp_weight sp_weight;
+int sp_weight_create(int32_t fmt, int32_t rows, int32_t cols, const void *data, const void *scales,
+                     const void *zeros, sp_weight **out);
+void sp_weight_destroy(sp_weight *w);
+/* HBM bytes of the packed codes + scales + zeros. */
+uint64_t sp_weight_bytes(const sp_weight *w);
+/* y_dev[m][r] = sum_k W[r][k] * x_dev[m][k] for m < m_cols (x fp16 [m_cols][cols], y fp32 [m_cols][rows]).
+ * workspace_dev must hold sp_op_gemv_workspace(w, m_cols) bytes (split-K partials and arrival counters; it must
+ * be zero-filled once before first use and is left zeroed by every call). */
+size_t sp_op_gemv_workspace(const sp_weight *w, int32_t m_cols);
+int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_dev, void *workspace_dev,
+               void *hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SEEDPLANE_HIP_H */

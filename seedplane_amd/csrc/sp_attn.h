@@ -1,0 +1,265 @@
+// Decode-side kernels around the GEMVs: embedding gather, RMSNorm, RoPE + KV-cache write, split-K GQA attention
+// (windowed ring slots + tree ancestor mask), split-K combine, two-pass argmax, KV slot moves.
+#pragma once
+#include "sp_device.h"
+#include "../../include/seedplane_hip.h"
+
+// ---------------------------------------------------------------------------------------------------------------
+// Element (row, k) of a packed matrix (layout written by sp_pack.h), dequantised in fp32 exactly as the canonical
+// definition: Q8 code*scale, Q4 (code - zero)*scale, F16 the value itself.
+template <int FMT>
+__device__ __forceinline__ float packed_elem(const uint8_t *w, const f16 *sz, int nkt, int row, int k) {
+    const int rg = row >> 4, r = row & 15;
+    if constexpr (FMT == 1) {
+        const int kt = k >> 5, lk = k & 31, g = lk >> 3, i = lk & 7;
+        const f16 *t = (const f16 *)(w + ((size_t)rg * nkt + kt) * TILE_BYTES);
+        return (float)t[(g * 16 + r) * 8 + i];
+    } else if constexpr (FMT == 2) {
+        const int kt = k >> 6, lk = k & 63, blk = lk >> 5, kk = lk & 31, g = kk >> 3, i = kk & 7;
+        const size_t tile = (size_t)rg * nkt + kt;
+        const int8_t c = (int8_t)w[tile * TILE_BYTES + (g * 16 + r) * 16 + blk * 8 + i];
+        return (float)c * (float)sz[tile * 32 + r * 2 + blk];
+    } else {
+        const int kt = k >> 7, lk = k & 127, s = lk >> 5, kk = lk & 31, g = kk >> 3, i = kk & 7;
+        const size_t tile = (size_t)rg * nkt + kt;
+        const uint32_t d = *(const uint32_t *)(w + tile * TILE_BYTES + (g * 16 + r) * 16 + s * 4);
+        const int pos = (i >> 1) + 4 * (i & 1);
+        const float code = (float)((d >> (4 * pos)) & 15u);
+        const float scale = (float)sz[tile * 128 + (r * 4 + s) * 2], zero = (float)sz[tile * 128 + (r * 4 + s) * 2 + 1];
+        return __fmul_rn(code - zero, scale);
+    }
+}
+
+// x[b][k] = E[token_b][k] (fp32).  Replaces F.embedding (qwen_engine.py:117) / embed.comp.
+template <int FMT>
+__global__ void __launch_bounds__(256) k_embed(const uint8_t *w, const f16 *sz, int nkt, const sp_token *toks,
+                                               int H, float *x, int ldx) {
+    const int b = blockIdx.x, tok = toks[b].token;
+    for (int k = threadIdx.x; k < H; k += blockDim.x) x[(size_t)b * ldx + k] = packed_elem<FMT>(w, sz, nkt, tok, k);
+}
+
+// out[b][k] = fp16(x * rsqrt(mean(x^2) + eps) * w).  Replaces Qwen2Engine._norm (qwen_engine.py:90-92): the weight
+// multiply happens in fp32 before the cast.
+__global__ void __launch_bounds__(256) k_rmsnorm(const float *x, int ldx, const float *w, int H, float eps, f16 *out,
+                                                 int ldo) {
+    __shared__ float red[16];
+    const int b = blockIdx.x;
+    const float *xr = x + (size_t)b * ldx;
+    float ss = 0.f;
+    for (int k = threadIdx.x; k < H; k += blockDim.x) { const float v = xr[k]; ss += v * v; }
+    ss = block_sum(ss, red);
+    const float rs = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int k = threadIdx.x; k < H; k += blockDim.x) out[(size_t)b * ldo + k] = (f16)((xr[k] * rs) * w[k]);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+struct RopeArgs {
+    const float *qkv;       // [n][Nqkv] fp32 (bias already added)
+    int Nqkv, NH, NKV, HD;
+    const float *inv_freq;  // [HD/2]
+    const sp_token *toks;
+    float *q;               // [n][NH*HD] fp32, rotated
+    f16 *kc, *vc;           // this layer's K/V: [seq][kvh][slot][HD]
+    int n_slots;
+};
+// Non-interleaved half rotation x*cos + rotate_half(x)*sin with phase = float(pos) * inv_freq (qwen_engine.py:94-103,
+// rope_kv.comp:1-32); K and V of every column are written to their slot.
+__global__ void __launch_bounds__(256) k_rope_kv(RopeArgs a) {
+    const int b = blockIdx.x;
+    const sp_token t = a.toks[b];
+    const int half = a.HD >> 1;
+    const float *src = a.qkv + (size_t)b * a.Nqkv;
+    const float fpos = (float)t.pos;
+    for (int idx = threadIdx.x; idx < (a.NH + a.NKV) * half; idx += blockDim.x) {
+        const int head = idx / half, i = idx - head * half;
+        const float ph = fpos * a.inv_freq[i];
+        const float c = cosf(ph), s = sinf(ph);
+        const float *v = src + head * a.HD;
+        const float x1 = v[i], x2 = v[i + half];
+        const float o1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(-x2, s));
+        const float o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+        if (head < a.NH) {
+            float *q = a.q + (size_t)b * a.NH * a.HD + head * a.HD;
+            q[i] = o1; q[i + half] = o2;
+        } else {
+            const int kvh = head - a.NH;
+            f16 *k = a.kc + (((size_t)t.seq * a.NKV + kvh) * a.n_slots + t.slot) * a.HD;
+            k[i] = (f16)o1; k[i + half] = (f16)o2;
+        }
+    }
+    const float *vsrc = src + (a.NH + a.NKV) * a.HD;
+    for (int idx = threadIdx.x; idx < a.NKV * a.HD; idx += blockDim.x) {
+        const int kvh = idx / a.HD, d = idx - kvh * a.HD;
+        a.vc[(((size_t)t.seq * a.NKV + kvh) * a.n_slots + t.slot) * a.HD + d] = (f16)vsrc[idx];
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Split-K GQA attention.  One block per (chunk of CH visible keys, kv head, column); the G query heads of the kv
+// head share the K/V chunk staged in LDS.  Visible keys of a column: ring positions [ctx_lo, ctx_hi] then the tree
+// block (slots tree_base + j, bit j of tree_mask).  Each block records {m, l, acc[HD]} per query head; k_attn_combine
+// merges them with exp(m - M) weights.  Replaces the SDPA call with its causal/slot mask (qwen_engine.py:126-135)
+// and attn_part.comp / attn_combine.comp.
+constexpr int ATT_CH = 64;
+struct AttnArgs {
+    const float *q;        // [n][NH*HD]
+    const f16 *kc, *vc;    // this layer
+    const sp_token *toks;
+    int NH, NKV, HD, n_slots, nchunk;   // nchunk = grid.x (max over columns)
+    float scale;
+    float *part;           // [n][NH][nchunk][HD + 2]
+};
+
+__device__ __forceinline__ int att_visible(const sp_token &t, int &nlin) {
+    nlin = t.ctx_hi >= t.ctx_lo ? t.ctx_hi - t.ctx_lo + 1 : 0;
+    return nlin + t.tree_count;
+}
+
+template <int HD, int G>
+__global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
+    constexpr int KP = HD + 8;                       // padded K row (halves) to spread LDS banks
+    __shared__ float q_s[G][HD];
+    __shared__ __align__(16) f16 k_s[ATT_CH][KP];
+    __shared__ __align__(16) f16 v_s[ATT_CH][HD];
+    __shared__ float p_s[G][ATT_CH];
+    __shared__ float ml_s[G][2];
+    __shared__ int ok_s[ATT_CH];
+
+    const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const sp_token t = a.toks[b];
+    int nlin;
+    const int nvis = att_visible(t, nlin);
+    const int v0 = c * ATT_CH;
+    if (v0 >= nvis) return;
+    const int cnt = min(ATT_CH, nvis - v0);
+    const int tid = threadIdx.x;
+
+    for (int i = tid; i < G * HD; i += 256)
+        q_s[i / HD][i % HD] = a.q[(size_t)b * a.NH * HD + (kvh * G) * HD + i] * a.scale;
+
+    const size_t head_base = ((size_t)t.seq * a.NKV + kvh) * a.n_slots;
+    constexpr int CPR = HD / 8;                     // 16-byte chunks per row
+    for (int i = tid; i < cnt * CPR; i += 256) {
+        const int j = i / CPR, ch = i - j * CPR;
+        const int vis = v0 + j;
+        int slot, ok = 1;
+        if (vis < nlin) {
+            slot = (t.ctx_lo + vis) % a.n_slots;
+        } else {
+            const int tj = vis - nlin;
+            slot = (t.tree_base + tj) % a.n_slots;
+            ok = (int)((t.tree_mask >> tj) & 1ull);
+        }
+        if (ch == 0) ok_s[j] = ok;
+        const size_t off = (head_base + slot) * HD + ch * 8;
+        *(f16x8 *)&k_s[j][ch * 8] = *(const f16x8 *)(a.kc + off);
+        *(f16x8 *)&v_s[j][ch * 8] = *(const f16x8 *)(a.vc + off);
+    }
+    __syncthreads();
+
+    // scores
+    for (int p = tid; p < G * cnt; p += 256) {
+        const int h = p / cnt, j = p - h * cnt;
+        float s = -INFINITY;
+        if (ok_s[j]) {
+            float acc = 0.f;
+#pragma unroll 8
+            for (int d = 0; d < HD; d += 8) {
+                const f16x8 kv = *(const f16x8 *)&k_s[j][d];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc += q_s[h][d + e] * (float)kv[e];
+            }
+            s = acc;
+        }
+        p_s[h][j] = s;
+    }
+    __syncthreads();
+
+    // per-head max / exp / sum: one wave per head
+    const int lane = tid & 63, wv = tid >> 6;
+    for (int h = wv; h < G; h += 4) {
+        const float s = lane < cnt ? p_s[h][lane] : -INFINITY;
+        const float m = wave_max(s);
+        const float e = (m == -INFINITY || s == -INFINITY) ? 0.f : expf(s - m);
+        const float l = wave_sum(e);
+        if (lane < cnt) p_s[h][lane] = e;
+        if (lane == 0) { ml_s[h][0] = m; ml_s[h][1] = l; }
+    }
+    __syncthreads();
+
+    float *out = a.part + (((size_t)b * a.NH + kvh * G) * a.nchunk + c) * (HD + 2);
+    const size_t hstride = (size_t)a.nchunk * (HD + 2);
+    for (int o = tid; o < G * HD; o += 256) {
+        const int h = o / HD, d = o - h * HD;
+        float acc = 0.f;
+        for (int j = 0; j < cnt; ++j) acc += p_s[h][j] * (float)v_s[j][d];
+        out[h * hstride + 2 + d] = acc;
+    }
+    if (tid < G) { out[tid * hstride] = ml_s[tid][0]; out[tid * hstride + 1] = ml_s[tid][1]; }
+}
+
+// out[b][h*HD + d] (fp16) = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}
+__global__ void __launch_bounds__(128) k_attn_combine(const float *part, const sp_token *toks, int NH, int HD,
+                                                      int nchunk, f16 *out, int ldo) {
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    int nlin;
+    const int nvis = att_visible(toks[b], nlin);
+    const int nc = (nvis + ATT_CH - 1) / ATT_CH;
+    const float *p = part + ((size_t)b * NH + h) * nchunk * (HD + 2);
+    float M = -INFINITY;
+    for (int c = 0; c < nc; ++c) if (p[c * (HD + 2) + 1] > 0.f) M = fmaxf(M, p[c * (HD + 2)]);
+    float L = 0.f, acc = 0.f;
+    for (int c = 0; c < nc; ++c) {
+        const float *pc = p + c * (HD + 2);
+        if (!(pc[1] > 0.f)) continue;
+        const float wgt = expf(pc[0] - M);
+        L += pc[1] * wgt;
+        if (d < HD) acc += pc[2 + d] * wgt;
+    }
+    if (d < HD) out[(size_t)b * ldo + h * HD + d] = (f16)(acc / L);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Two-pass argmax, first index on ties (qwen_engine.py:148 torch.argmax; sampler.hpp:98-99; argmax.comp:2,17).
+constexpr int ARGMAX_BLOCKS = 64;
+__global__ void __launch_bounds__(256) k_argmax_part(const float *x, int cols, int ld, float *pv, int *pi) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int row = blockIdx.y, blk = blockIdx.x;
+    const int per = (cols + ARGMAX_BLOCKS - 1) / ARGMAX_BLOCKS;
+    const int lo = blk * per, hi = min(cols, lo + per);
+    float bv = -INFINITY; int bi = 0x7fffffff;
+    const float *xr = x + (size_t)row * ld;
+    for (int i = lo + threadIdx.x; i < hi; i += 256) argmax_merge(bv, bi, xr[i], i);
+    wave_argmax(bv, bi);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    if (lane == 0) { sv[wv] = bv; si[wv] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w2 = 1; w2 < 4; ++w2) argmax_merge(bv, bi, sv[w2], si[w2]);
+        pv[row * ARGMAX_BLOCKS + blk] = bv; pi[row * ARGMAX_BLOCKS + blk] = bi;
+    }
+}
+__global__ void __launch_bounds__(64) k_argmax_final(const float *pv, const int *pi, int *out) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    float bv = pv[row * ARGMAX_BLOCKS + lane]; int bi = pi[row * ARGMAX_BLOCKS + lane];
+    wave_argmax(bv, bi);
+    if (lane == 0) out[row] = bi == 0x7fffffff ? 0 : bi;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// K/V slot moves of one sequence, applied in order (one block per layer x kv head).
+__global__ void __launch_bounds__(128) k_kv_move(f16 *const *kl, f16 *const *vl, int seq, int NKV, int n_slots, int HD,
+                                                 const int *src, const int *dst, int n) {
+    const int layer = blockIdx.x / NKV, kvh = blockIdx.x % NKV;
+    f16 *k = kl[layer], *v = vl[layer];
+    const size_t base = ((size_t)seq * NKV + kvh) * n_slots;
+    for (int i = 0; i < n; ++i) {
+        const size_t so = (base + src[i]) * HD, dO = (base + dst[i]) * HD;
+        f16 tk = 0, tv = 0;
+        if (threadIdx.x < HD) { tk = k[so + threadIdx.x]; tv = v[so + threadIdx.x]; }
+        __syncthreads();
+        if (threadIdx.x < HD) { k[dO + threadIdx.x] = tk; v[dO + threadIdx.x] = tv; }
+        __syncthreads();
+    }
+}

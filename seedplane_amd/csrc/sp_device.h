@@ -1,0 +1,97 @@
+// Device-side building blocks shared by every kernel: vector types, exact code->fp16 unpacking, the gfx950
+// 16x16x32 fp16 MFMA, wavefront reductions.  gfx950 only: wave64, MFMA, LDS.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define SP_WAVE 64
+
+// ----------------------------------------------------------------------------------------------------------------
+// Packed tile geometry (host packer in sp_pack.h writes exactly this; see the layout notes there).
+//   Every format tiles a matrix into 16-row groups x KT columns; one tile is 1024 code bytes, one dwordx4 per lane.
+//   Lane l of a wave owns row (l % 16) and k-subset g = l / 16 of the tile.
+constexpr int TILE_ROWS = 16;
+constexpr int TILE_BYTES = 1024;
+template <int FMT> struct TileGeom;
+// FMT values mirror SP_FMT_*: 1 = F16, 2 = Q8, 3 = Q4.
+template <> struct TileGeom<1> { static constexpr int KT = 32;  static constexpr int STEPS = 1; static constexpr int SZ_BYTES = 0;   };
+template <> struct TileGeom<2> { static constexpr int KT = 64;  static constexpr int STEPS = 2; static constexpr int SZ_BYTES = 64;  };
+template <> struct TileGeom<3> { static constexpr int KT = 128; static constexpr int STEPS = 4; static constexpr int SZ_BYTES = 256; };
+
+// ----------------------------------------------------------------------------------------------------------------
+// Exact unpacking.  int8 code c (two's complement) -> fp16: the byte c^0x80 = c+128 is placed under the exponent
+// byte 0x64, giving the fp16 value 1024 + c + 128 exactly; subtracting 1152 (exact in fp16) leaves c.
+__device__ __forceinline__ f16x2 q8_pair(uint32_t u, uint32_t sel) {
+    // u already xor-ed with 0x80808080; sel picks two bytes of u interleaved with 0x64.
+    uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, sel);
+    return __builtin_bit_cast(f16x2, h) - (f16x2){(f16)1152.0f, (f16)1152.0f};
+}
+// 8 int8 codes (two dwords, k order) -> 8 fp16 in k order.
+__device__ __forceinline__ f16x8 q8_unpack8(uint32_t d0, uint32_t d1) {
+    d0 ^= 0x80808080u; d1 ^= 0x80808080u;
+    f16x2 a = q8_pair(d0, 0x04010400u), b = q8_pair(d0, 0x04030402u);
+    f16x2 c = q8_pair(d1, 0x04010400u), d = q8_pair(d1, 0x04030402u);
+    return (f16x8){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+// 8 uint4 codes of one dword -> 8 fp16 in k order.  The packer stores k-order codes c0..c7 at nibble positions
+// 0,4,1,5,2,6,3,7 so that (v >> 4j) & 0x000F000F yields the pair (c_{2j}, c_{2j+1}) in the two fp16 halves; OR-ing
+// 0x6400 gives 1024 + c exactly, and subtracting 1024 leaves c.
+__device__ __forceinline__ f16x2 q4_pair(uint32_t v, int j) {
+    uint32_t h = ((v >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+    return __builtin_bit_cast(f16x2, h) - (f16x2){(f16)1024.0f, (f16)1024.0f};
+}
+__device__ __forceinline__ f16x8 q4_unpack8(uint32_t v) {
+    f16x2 a = q4_pair(v, 0), b = q4_pair(v, 1), c = q4_pair(v, 2), d = q4_pair(v, 3);
+    return (f16x8){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// D(16x16, fp32) += A(16x32 fp16) * B(32x16 fp16).  Lane l: A row (l%16) k-subset (l/16); B column (l%16)
+// k-subset (l/16); D column (l%16), rows 4*(l/16) + r in register r.
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// ----------------------------------------------------------------------------------------------------------------
+// Wavefront reductions (wave64, butterfly over all lanes).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SP_WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, SP_WAVE));
+    return v;
+}
+// (value, index) max with the smallest index winning ties.
+__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+}
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float v2 = __shfl_xor(v, o, SP_WAVE); int i2 = __shfl_xor(i, o, SP_WAVE);
+        argmax_merge(v, i, v2, i2);
+    }
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024); `red` holds >= 16 floats of LDS.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int j = 0; j < nw; ++j) t += red[j];
+    return t;
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }

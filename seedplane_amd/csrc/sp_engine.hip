@@ -1,0 +1,647 @@
+// libseedplane_hip: C ABI (include/seedplane_hip.h) over the gfx950 decode / verify kernels.
+//
+// The engine owns every device buffer: packed weights, the fp16 KV ring of every layer, the activation buffers
+// for up to max_tokens columns, split-K / attention / argmax scratch.  One forward call = one stream-ordered
+// sequence of kernels (optionally captured once into a hipGraph per (columns, flags) and replayed).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/seedplane_hip.h"
+#include "sp_attn.h"
+#include "sp_gemv.h"
+#include "sp_pack.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+struct Fail {
+    int code;
+    std::string msg;
+};
+
+#define HIPCHK(expr)                                                                                     \
+    do {                                                                                                 \
+        hipError_t _e = (expr);                                                                          \
+        if (_e != hipSuccess)                                                                            \
+            throw Fail{SP_EHIP, std::string(#expr) + ": " + hipGetErrorString(_e)};                      \
+    } while (0)
+
+inline void require(bool ok, int code, const std::string &msg) {
+    if (!ok) throw Fail{code, msg};
+}
+
+template <class T>
+T *dev_alloc(size_t count, uint64_t *acct = nullptr) {
+    void *p = nullptr;
+    if (count == 0) count = 1;
+    hipError_t e = hipMalloc(&p, count * sizeof(T));
+    if (e != hipSuccess) throw Fail{SP_ENOMEM, "hipMalloc of " + std::to_string(count * sizeof(T)) + " bytes failed: " + hipGetErrorString(e)};
+    if (acct) *acct += count * sizeof(T);
+    return (T *)p;
+}
+inline void dev_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+// ------------------------------------------------------------------------------------------- packed matrix on HBM
+struct DevMat {
+    int fmt = 0, rows = 0, cols = 0, rows_pad = 0, nkt = 0;
+    bool paired = false;
+    uint8_t *w = nullptr;
+    f16 *sz = nullptr;
+    uint64_t bytes = 0;
+    void release() { dev_free(w); dev_free(sz); w = nullptr; sz = nullptr; bytes = 0; }
+};
+
+DevMat upload_matrix(int fmt, int rows, int cols, const void *data, const void *scales, const void *zeros, bool paired) {
+    sp::Packed p;
+    try {
+        p = sp::pack_matrix(fmt, rows, cols, data, scales, zeros, paired);
+    } catch (const std::invalid_argument &ex) {
+        throw Fail{SP_EINVAL, ex.what()};
+    }
+    DevMat m;
+    m.fmt = fmt; m.rows = rows; m.cols = cols; m.rows_pad = p.rows_pad; m.nkt = p.nkt; m.paired = paired;
+    m.w = dev_alloc<uint8_t>(p.codes.size());
+    HIPCHK(hipMemcpy(m.w, p.codes.data(), p.codes.size(), hipMemcpyHostToDevice));
+    m.bytes = p.codes.size();
+    if (!p.sz.empty()) {
+        m.sz = dev_alloc<f16>(p.sz.size());
+        HIPCHK(hipMemcpy(m.sz, p.sz.data(), p.sz.size() * 2, hipMemcpyHostToDevice));
+        m.bytes += p.sz.size() * 2;
+    }
+    return m;
+}
+
+// ------------------------------------------------------------------------------------------- GEMV planning/launch
+constexpr int GEMV_NW = 4;
+constexpr int GEMV_MAX_MT = 4;
+
+struct GemvPlan {
+    int units, ksplit, rg;
+};
+
+GemvPlan plan_gemv(const DevMat &m) {
+    GemvPlan p;
+    p.rg = m.paired ? 2 : 1;
+    p.units = m.rows_pad / 16 / p.rg;
+    p.ksplit = 1;
+    const int target_blocks = 1024;
+    if (p.units < target_blocks) {
+        const int by_work = std::max(1, m.nkt / (GEMV_NW * 2));
+        const int by_fill = (target_blocks + p.units - 1) / p.units;
+        p.ksplit = std::max(1, std::min(by_work, by_fill));
+    }
+    return p;
+}
+
+size_t gemv_partial_floats(const DevMat &m, int mt) {
+    GemvPlan p = plan_gemv(m);
+    if (p.ksplit == 1) return 0;
+    return (size_t)p.ksplit * p.units * p.rg * mt * 64 * 4;
+}
+
+template <int FMT>
+void launch_gemv_fmt(int mt, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+    switch (mt) {
+        case 1: hipLaunchKernelGGL((k_gemv<FMT, 1>), grid, block, smem, st, a); break;
+        case 2: hipLaunchKernelGGL((k_gemv<FMT, 2>), grid, block, smem, st, a); break;
+        case 3: hipLaunchKernelGGL((k_gemv<FMT, 3>), grid, block, smem, st, a); break;
+        default: hipLaunchKernelGGL((k_gemv<FMT, 4>), grid, block, smem, st, a); break;
+    }
+}
+
+void launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, float *out_f32, f16 *out_f16, int ldo,
+                 const float *bias, float *partial, uint32_t *counters, hipStream_t st) {
+    require(mcols >= 1 && mcols <= 16 * GEMV_MAX_MT, SP_EINVAL, "gemv columns out of range");
+    require((epi == EPI_SILU) == m.paired, SP_EINVAL, "gemv epilogue does not match the matrix packing");
+    GemvPlan p = plan_gemv(m);
+    const int mt = (mcols + 15) / 16;
+    GemvArgs a;
+    a.w = m.w; a.sz = m.sz; a.nkt = m.nkt; a.units = p.units;
+    a.n_real = m.paired ? m.rows / 2 : m.rows;
+    a.x = x; a.ldx = ldx; a.m = mcols;
+    a.out_f32 = out_f32; a.out_f16 = out_f16; a.ldo = ldo; a.bias = bias;
+    a.partial = partial; a.counters = counters; a.ksplit = p.ksplit; a.epi = epi;
+    dim3 grid(p.units, p.ksplit), block(64 * GEMV_NW);
+    const size_t smem = (size_t)GEMV_NW * p.rg * mt * 64 * 16;
+    switch (m.fmt) {
+        case 1: launch_gemv_fmt<1>(mt, grid, block, smem, st, a); break;
+        case 2: launch_gemv_fmt<2>(mt, grid, block, smem, st, a); break;
+        default: launch_gemv_fmt<3>(mt, grid, block, smem, st, a); break;
+    }
+}
+
+// ------------------------------------------------------------------------------------------- attention dispatch
+template <int HD>
+void launch_attn_hd(int G, dim3 grid, hipStream_t st, const AttnArgs &a) {
+    switch (G) {
+        case 1: hipLaunchKernelGGL((k_attn_part<HD, 1>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((k_attn_part<HD, 2>), grid, dim3(256), 0, st, a); break;
+        case 3: hipLaunchKernelGGL((k_attn_part<HD, 3>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((k_attn_part<HD, 4>), grid, dim3(256), 0, st, a); break;
+        case 5: hipLaunchKernelGGL((k_attn_part<HD, 5>), grid, dim3(256), 0, st, a); break;
+        case 6: hipLaunchKernelGGL((k_attn_part<HD, 6>), grid, dim3(256), 0, st, a); break;
+        case 7: hipLaunchKernelGGL((k_attn_part<HD, 7>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_attn_part<HD, 8>), grid, dim3(256), 0, st, a); break;
+    }
+}
+
+template <int FMT>
+void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x, hipStream_t st) {
+    hipLaunchKernelGGL((k_embed<FMT>), dim3(n), dim3(256), 0, st, m.w, m.sz, m.nkt, toks, H, x, H);
+}
+
+}  // namespace
+
+// ============================================================================================== engine
+struct sp_engine {
+    sp_model_desc d{};
+    std::string err;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    int device = 0;
+
+    struct Layer {
+        DevMat qkv, o, gate_up, down;
+        float *qkv_b = nullptr, *in_norm = nullptr, *post_norm = nullptr;
+    };
+    std::vector<Layer> layers;
+    DevMat embed, head;
+    float *final_norm = nullptr, *inv_freq = nullptr;
+    uint64_t weight_bytes = 0, kv_bytes = 0;
+
+    // activations
+    int Nqkv = 0, maxT = 0, max_nchunk = 0;
+    float *x = nullptr, *qkv = nullptr, *q = nullptr, *logits = nullptr, *attn_part = nullptr;
+    f16 *xn = nullptr, *attn = nullptr, *act = nullptr;
+    float *gpart = nullptr;
+    uint32_t *gcnt = nullptr;
+    size_t gpart_floats = 0;
+    int gcnt_len = 0;
+    float *am_v = nullptr;
+    int *am_i = nullptr, *am_out = nullptr;
+    sp_token *dtoks = nullptr;
+
+    // KV ring
+    int n_seq = 0, n_slots = 0;
+    std::vector<f16 *> kc, vc;
+    f16 **d_kl = nullptr, **d_vl = nullptr;
+    int *d_move = nullptr;
+
+    std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+
+    void free_all();
+    void alloc_activations();
+    void ensure_scratch();
+    void step(int n, int flags, int nchunk);
+    int nchunk_for(int n, const sp_token *t, bool graph) const;
+};
+
+void sp_engine::free_all() {
+    for (auto &kv : graphs) (void)hipGraphExecDestroy(kv.second);
+    graphs.clear();
+    for (auto &l : layers) {
+        l.qkv.release(); l.o.release(); l.gate_up.release(); l.down.release();
+        dev_free(l.qkv_b); dev_free(l.in_norm); dev_free(l.post_norm);
+    }
+    layers.clear();
+    embed.release(); head.release();
+    dev_free(final_norm); dev_free(inv_freq);
+    for (void *p : {(void *)x, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)xn, (void *)attn,
+                    (void *)act, (void *)gpart, (void *)gcnt, (void *)am_v, (void *)am_i, (void *)am_out,
+                    (void *)dtoks, (void *)d_kl, (void *)d_vl, (void *)d_move})
+        dev_free(p);
+    for (auto p : kc) dev_free(p);
+    for (auto p : vc) dev_free(p);
+    kc.clear(); vc.clear();
+    if (own_stream && stream) (void)hipStreamDestroy(stream);
+    stream = nullptr;
+}
+
+void sp_engine::alloc_activations() {
+    const int H = d.hidden, I = d.intermediate, V = d.vocab;
+    Nqkv = (d.n_heads + 2 * d.n_kv_heads) * d.head_dim;
+    maxT = d.max_tokens;
+    const int kmax = std::max(std::max(H, I), d.n_heads * d.head_dim);
+    x = dev_alloc<float>((size_t)maxT * H);
+    xn = dev_alloc<f16>((size_t)maxT * kmax);
+    qkv = dev_alloc<float>((size_t)maxT * Nqkv);
+    q = dev_alloc<float>((size_t)maxT * d.n_heads * d.head_dim);
+    attn = dev_alloc<f16>((size_t)maxT * d.n_heads * d.head_dim);
+    act = dev_alloc<f16>((size_t)maxT * I);
+    logits = dev_alloc<float>((size_t)maxT * V);
+    am_v = dev_alloc<float>((size_t)maxT * ARGMAX_BLOCKS);
+    am_i = dev_alloc<int>((size_t)maxT * ARGMAX_BLOCKS);
+    am_out = dev_alloc<int>(maxT);
+    dtoks = dev_alloc<sp_token>(maxT);
+    d_move = dev_alloc<int>(2 * 64);
+    HIPCHK(hipMemset(xn, 0, (size_t)maxT * kmax * sizeof(f16)));
+    HIPCHK(hipMemset(attn, 0, (size_t)maxT * d.n_heads * d.head_dim * sizeof(f16)));
+    HIPCHK(hipMemset(act, 0, (size_t)maxT * I * sizeof(f16)));
+}
+
+// split-K scratch sized for the loaded matrices at the largest column count
+void sp_engine::ensure_scratch() {
+    const int mt = (maxT + 15) / 16;
+    size_t need = 0;
+    int units = 0;
+    auto visit = [&](const DevMat &m) {
+        if (!m.w) return;
+        need = std::max(need, gemv_partial_floats(m, mt));
+        units = std::max(units, plan_gemv(m).units);
+    };
+    for (auto &l : layers) { visit(l.qkv); visit(l.o); visit(l.gate_up); visit(l.down); }
+    visit(embed); visit(head);
+    if (need > gpart_floats) {
+        dev_free(gpart);
+        gpart = dev_alloc<float>(need);
+        gpart_floats = need;
+    }
+    if (units > gcnt_len) {
+        dev_free(gcnt);
+        gcnt = dev_alloc<uint32_t>(units);
+        HIPCHK(hipMemset(gcnt, 0, units * sizeof(uint32_t)));
+        gcnt_len = units;
+    }
+}
+
+int sp_engine::nchunk_for(int n, const sp_token *t, bool graph) const {
+    if (graph) return (n_slots + 64 + ATT_CH - 1) / ATT_CH;
+    int mx = 1;
+    for (int i = 0; i < n; ++i) {
+        const int nlin = t[i].ctx_hi >= t[i].ctx_lo ? t[i].ctx_hi - t[i].ctx_lo + 1 : 0;
+        mx = std::max(mx, nlin + t[i].tree_count);
+    }
+    return (mx + ATT_CH - 1) / ATT_CH;
+}
+
+void sp_engine::step(int n, int flags, int nchunk) {
+    const int H = d.hidden, I = d.intermediate, NH = d.n_heads, NKV = d.n_kv_heads, HD = d.head_dim;
+    hipStream_t st = stream;
+    switch (embed.fmt) {
+        case 1: launch_embed<1>(embed, dtoks, n, H, x, st); break;
+        case 2: launch_embed<2>(embed, dtoks, n, H, x, st); break;
+        default: launch_embed<3>(embed, dtoks, n, H, x, st); break;
+    }
+    const bool logits_on = flags & SP_F_LOGITS;
+    for (int l = 0; l < d.n_layers; ++l) {
+        Layer &ly = layers[l];
+        hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, ly.in_norm, H, d.rms_eps, xn, H);
+        launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, gpart, gcnt, st);
+        RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots};
+        hipLaunchKernelGGL(k_rope_kv, dim3(n), dim3(256), 0, st, ra);
+        if (l + 1 == d.n_layers && !logits_on) break;   // K/V-only: the last layer only needs its K/V
+        AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
+        const int G = NH / NKV;
+        dim3 agrid(nchunk, NKV, n);
+        if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
+        else launch_attn_hd<128>(G, agrid, st, aa);
+        hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dtoks, NH, HD, nchunk, attn, NH * HD);
+        launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, gpart, gcnt, st);
+        hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, ly.post_norm, H, d.rms_eps, xn, H);
+        launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, gpart, gcnt, st);
+        launch_gemv(ly.down, EPI_RESID, act, I, n, x, nullptr, H, nullptr, gpart, gcnt, st);
+    }
+    if (logits_on) {
+        hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, final_norm, H, d.rms_eps, xn, H);
+        const DevMat &hm = d.tied_head ? embed : head;
+        launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, gpart, gcnt, st);
+        if (flags & SP_F_ARGMAX) {
+            hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, n), dim3(256), 0, st, logits, d.vocab, d.vocab, am_v, am_i);
+            hipLaunchKernelGGL(k_argmax_final, dim3(n), dim3(64), 0, st, am_v, am_i, am_out);
+        }
+    }
+    HIPCHK(hipGetLastError());
+}
+
+// ============================================================================================== C ABI
+namespace {
+int fail_engine(sp_engine *e, const Fail &f) {
+    if (e) e->err = f.msg;
+    g_err = f.msg;
+    return f.code;
+}
+template <class F>
+int guarded(sp_engine *e, F &&fn) {
+    try {
+        fn();
+        return SP_OK;
+    } catch (const Fail &f) {
+        return fail_engine(e, f);
+    } catch (const std::exception &ex) {
+        return fail_engine(e, Fail{SP_EHIP, ex.what()});
+    }
+}
+}  // namespace
+
+extern "C" {
+
+const char *sp_last_error(void) { return g_err.c_str(); }
+const char *sp_engine_last_error(const sp_engine *e) { return e ? e->err.c_str() : g_err.c_str(); }
+
+int sp_engine_create(const sp_model_desc *desc, sp_engine **out) {
+    if (!out) { g_err = "out is NULL"; return SP_EINVAL; }
+    *out = nullptr;
+    sp_engine *e = new sp_engine();
+    int rc = guarded(nullptr, [&] {
+        require(desc != nullptr, SP_EINVAL, "desc is NULL");
+        const sp_model_desc &d = *desc;
+        require(d.n_layers > 0 && d.hidden > 0 && d.n_heads > 0 && d.n_kv_heads > 0 && d.vocab > 0 && d.intermediate > 0,
+                SP_EINVAL, "model dimensions must be positive");
+        require(d.n_heads % d.n_kv_heads == 0 && d.n_heads / d.n_kv_heads <= 8, SP_EINVAL,
+                "n_heads must be a multiple of n_kv_heads with at most 8 query heads per kv head");
+        require(d.head_dim == 64 || d.head_dim == 128, SP_EINVAL, "head_dim must be 64 or 128");
+        require(d.weight_format == SP_FMT_F16 || d.weight_format == SP_FMT_Q8 || d.weight_format == SP_FMT_Q4, SP_EINVAL,
+                "weight_format must be SP_FMT_F16, SP_FMT_Q8 or SP_FMT_Q4");
+        require(d.max_tokens >= 1 && d.max_tokens <= 16 * GEMV_MAX_MT, SP_EINVAL, "max_tokens must be in [1, 64]");
+        require(d.hidden % 128 == 0 && d.intermediate % 128 == 0 && (d.n_heads * d.head_dim) % 128 == 0, SP_EINVAL,
+                "hidden, intermediate and heads*head_dim must be multiples of 128");
+        require(d.inv_freq != nullptr, SP_EINVAL, "inv_freq is NULL");
+        e->d = d;
+        e->d.inv_freq = nullptr;
+        HIPCHK(hipGetDevice(&e->device));
+        HIPCHK(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+        e->own_stream = true;
+        e->layers.resize(d.n_layers);
+        e->inv_freq = dev_alloc<float>(d.head_dim / 2);
+        HIPCHK(hipMemcpy(e->inv_freq, d.inv_freq, d.head_dim / 2 * sizeof(float), hipMemcpyHostToDevice));
+        e->alloc_activations();
+    });
+    if (rc != SP_OK) { e->free_all(); delete e; return rc; }
+    *out = e;
+    return SP_OK;
+}
+
+void sp_engine_destroy(sp_engine *e) {
+    if (!e) return;
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    e->free_all();
+    delete e;
+}
+
+int sp_engine_set_stream(sp_engine *e, void *s) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        HIPCHK(hipStreamSynchronize(e->stream));
+        if (e->own_stream) HIPCHK(hipStreamDestroy(e->stream));
+        for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
+        e->graphs.clear();
+        e->stream = (hipStream_t)s;
+        e->own_stream = false;
+    });
+}
+
+int sp_engine_load(sp_engine *e, int32_t kind, int32_t layer, int32_t fmt, int32_t rows, int32_t cols, const void *data,
+                   const void *scales, const void *zeros) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        const sp_model_desc &d = e->d;
+        const int Nqkv = (d.n_heads + 2 * d.n_kv_heads) * d.head_dim;
+        auto vec = [&](float *&dst, int n) {
+            require(fmt == SP_FMT_F32 && rows == 1 && cols == n, SP_EINVAL, "vector tensor must be fp32 [1][n] with the model's width");
+            require(data != nullptr, SP_EINVAL, "data is NULL");
+            dev_free(dst);
+            dst = dev_alloc<float>(n, &e->weight_bytes);
+            HIPCHK(hipMemcpy(dst, data, n * sizeof(float), hipMemcpyHostToDevice));
+        };
+        auto mat = [&](DevMat &dst, int want_rows, int want_cols, bool paired) {
+            require(fmt == d.weight_format, SP_EINVAL, "matrix format differs from the model's weight_format");
+            require(rows == want_rows && cols == want_cols, SP_EINVAL, "matrix shape does not match the model description");
+            e->weight_bytes -= dst.bytes;
+            dst.release();
+            dst = upload_matrix(fmt, rows, cols, data, scales, zeros, paired);
+            e->weight_bytes += dst.bytes;
+        };
+        const bool per_layer = kind >= SP_T_IN_NORM;
+        if (per_layer) require(layer >= 0 && layer < d.n_layers, SP_EINVAL, "layer out of range");
+        switch (kind) {
+            case SP_T_EMBED: mat(e->embed, d.vocab, d.hidden, false); break;
+            case SP_T_HEAD: require(!d.tied_head, SP_EINVAL, "the model has a tied head"); mat(e->head, d.vocab, d.hidden, false); break;
+            case SP_T_FINAL_NORM: vec(e->final_norm, d.hidden); break;
+            case SP_T_IN_NORM: vec(e->layers[layer].in_norm, d.hidden); break;
+            case SP_T_POST_NORM: vec(e->layers[layer].post_norm, d.hidden); break;
+            case SP_T_QKV: mat(e->layers[layer].qkv, Nqkv, d.hidden, false); break;
+            case SP_T_QKV_BIAS: vec(e->layers[layer].qkv_b, Nqkv); break;
+            case SP_T_O: mat(e->layers[layer].o, d.hidden, d.n_heads * d.head_dim, false); break;
+            case SP_T_GATE_UP: mat(e->layers[layer].gate_up, 2 * d.intermediate, d.hidden, true); break;
+            case SP_T_DOWN: mat(e->layers[layer].down, d.hidden, d.intermediate, false); break;
+            default: throw Fail{SP_EINVAL, "unknown tensor kind"};
+        }
+        for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
+        e->graphs.clear();
+    });
+}
+
+int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        require(n_seq >= 1 && n_slots >= 1, SP_EINVAL, "n_seq and n_slots must be positive");
+        HIPCHK(hipStreamSynchronize(e->stream));
+        for (auto p : e->kc) dev_free(p);
+        for (auto p : e->vc) dev_free(p);
+        e->kc.assign(e->d.n_layers, nullptr);
+        e->vc.assign(e->d.n_layers, nullptr);
+        e->kv_bytes = 0;
+        e->n_seq = 0; e->n_slots = 0;
+        dev_free(e->attn_part); e->attn_part = nullptr;
+        const size_t per = (size_t)n_seq * e->d.n_kv_heads * n_slots * e->d.head_dim;
+        for (int l = 0; l < e->d.n_layers; ++l) {
+            e->kc[l] = dev_alloc<f16>(per, &e->kv_bytes);
+            e->vc[l] = dev_alloc<f16>(per, &e->kv_bytes);
+            HIPCHK(hipMemset(e->kc[l], 0, per * sizeof(f16)));
+            HIPCHK(hipMemset(e->vc[l], 0, per * sizeof(f16)));
+        }
+        if (!e->d_kl) e->d_kl = dev_alloc<f16 *>(e->d.n_layers);
+        if (!e->d_vl) e->d_vl = dev_alloc<f16 *>(e->d.n_layers);
+        HIPCHK(hipMemcpy(e->d_kl, e->kc.data(), e->d.n_layers * sizeof(f16 *), hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(e->d_vl, e->vc.data(), e->d.n_layers * sizeof(f16 *), hipMemcpyHostToDevice));
+        e->n_seq = n_seq; e->n_slots = n_slots;
+        e->max_nchunk = (n_slots + 64 + ATT_CH - 1) / ATT_CH;
+        e->attn_part = dev_alloc<float>((size_t)e->maxT * e->d.n_heads * e->max_nchunk * (e->d.head_dim + 2));
+        for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
+        e->graphs.clear();
+    });
+}
+
+int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t flags, float *logits_dev, int32_t *argmax_host) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        const sp_model_desc &d = e->d;
+        require(n >= 1 && n <= e->maxT, SP_ECAPACITY, "column count must be in [1, max_tokens]");
+        require(toks != nullptr, SP_EINVAL, "toks is NULL");
+        require(e->n_seq > 0, SP_ESTATE, "KV cache not reserved");
+        require(e->embed.w && e->final_norm && (d.tied_head || e->head.w), SP_ESTATE, "embedding / head / final norm not loaded");
+        for (auto &l : e->layers)
+            require(l.qkv.w && l.o.w && l.gate_up.w && l.down.w && l.qkv_b && l.in_norm && l.post_norm, SP_ESTATE,
+                    "a layer's weights are not loaded");
+        require(!(argmax_host && !(flags & SP_F_ARGMAX)), SP_EINVAL, "argmax_host needs SP_F_ARGMAX");
+        require(!((flags & SP_F_ARGMAX) && !(flags & SP_F_LOGITS)), SP_EINVAL, "SP_F_ARGMAX needs SP_F_LOGITS");
+        for (int i = 0; i < n; ++i) {
+            const sp_token &t = toks[i];
+            require(t.token >= 0 && t.token < d.vocab, SP_EINVAL, "token id out of range");
+            require(t.seq >= 0 && t.seq < e->n_seq, SP_EINVAL, "sequence index out of range");
+            require(t.slot >= 0 && t.slot < e->n_slots, SP_EINVAL, "slot out of range");
+            require(t.pos >= 0, SP_EINVAL, "position must be non-negative");
+            require(t.ctx_lo >= 0, SP_EINVAL, "ctx_lo must be non-negative");
+            const int nlin = t.ctx_hi >= t.ctx_lo ? t.ctx_hi - t.ctx_lo + 1 : 0;
+            require(nlin <= e->n_slots, SP_ECAPACITY, "visible range exceeds the KV slots");
+            require(t.tree_count >= 0 && t.tree_count <= 64, SP_EINVAL, "tree_count must be in [0, 64]");
+            require(t.tree_count == 0 || (t.tree_base >= 0 && t.tree_base < e->n_slots), SP_EINVAL, "tree_base out of range");
+            require(nlin + t.tree_count >= 1, SP_EINVAL, "a column must see at least one key");
+        }
+        HIPCHK(hipMemcpyAsync(e->dtoks, toks, n * sizeof(sp_token), hipMemcpyHostToDevice, e->stream));
+        const bool use_graph = flags & SP_F_GRAPH;
+        const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX);
+        if (use_graph) {
+            auto key = std::make_pair(n, sflags);
+            auto it = e->graphs.find(key);
+            if (it == e->graphs.end()) {
+                e->ensure_scratch();
+                hipGraph_t g;
+                HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+                try {
+                    e->step(n, sflags, e->nchunk_for(n, toks, true));
+                } catch (...) {
+                    hipGraph_t dummy;
+                    (void)hipStreamEndCapture(e->stream, &dummy);
+                    throw;
+                }
+                HIPCHK(hipStreamEndCapture(e->stream, &g));
+                hipGraphExec_t ge;
+                HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+                (void)hipGraphDestroy(g);
+                it = e->graphs.emplace(key, ge).first;
+            }
+            HIPCHK(hipGraphLaunch(it->second, e->stream));
+        } else {
+            e->ensure_scratch();
+            e->step(n, sflags, e->nchunk_for(n, toks, false));
+        }
+        if (logits_dev && (flags & SP_F_LOGITS))
+            HIPCHK(hipMemcpyAsync(logits_dev, e->logits, (size_t)n * d.vocab * sizeof(float), hipMemcpyDeviceToDevice, e->stream));
+        if (argmax_host) {
+            HIPCHK(hipMemcpyAsync(argmax_host, e->am_out, n * sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
+            HIPCHK(hipStreamSynchronize(e->stream));
+        }
+    });
+}
+
+int sp_engine_logits(sp_engine *e, float **logits_dev) {
+    if (!e || !logits_dev) { g_err = "NULL argument"; return SP_EINVAL; }
+    *logits_dev = e->logits;
+    return SP_OK;
+}
+
+int sp_engine_kv_move(sp_engine *e, int32_t seq, int32_t n, const int32_t *src, const int32_t *dst) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        require(e->n_seq > 0, SP_ESTATE, "KV cache not reserved");
+        require(seq >= 0 && seq < e->n_seq, SP_EINVAL, "sequence index out of range");
+        require(n >= 0 && n <= 64, SP_EINVAL, "at most 64 slot moves per call");
+        if (n == 0) return;
+        require(src && dst, SP_EINVAL, "slot arrays are NULL");
+        std::vector<int> buf(2 * n);
+        for (int i = 0; i < n; ++i) {
+            require(src[i] >= 0 && src[i] < e->n_slots && dst[i] >= 0 && dst[i] < e->n_slots, SP_EINVAL, "slot out of range");
+            buf[i] = src[i]; buf[n + i] = dst[i];
+        }
+        HIPCHK(hipMemcpyAsync(e->d_move, buf.data(), 2 * n * sizeof(int), hipMemcpyHostToDevice, e->stream));
+        hipLaunchKernelGGL(k_kv_move, dim3(e->d.n_layers * e->d.n_kv_heads), dim3(128), 0, e->stream, e->d_kl, e->d_vl, seq,
+                           e->d.n_kv_heads, e->n_slots, e->d.head_dim, e->d_move, e->d_move + n, n);
+        HIPCHK(hipGetLastError());
+        HIPCHK(hipStreamSynchronize(e->stream));
+    });
+}
+
+int sp_engine_sync(sp_engine *e) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] { HIPCHK(hipStreamSynchronize(e->stream)); });
+}
+
+int sp_engine_bytes(const sp_engine *e, uint64_t *wb, uint64_t *kb) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    if (wb) *wb = e->weight_bytes;
+    if (kb) *kb = e->kv_bytes;
+    return SP_OK;
+}
+
+// ---------------------------------------------------------------------------------------------- standalone ops
+size_t sp_op_argmax_workspace(int32_t rows, int32_t cols) {
+    (void)cols;
+    return rows <= 0 ? 0 : (size_t)rows * ARGMAX_BLOCKS * (sizeof(float) + sizeof(int));
+}
+
+int sp_op_argmax(const float *logits_dev, int32_t rows, int32_t cols, int32_t *out_dev, void *ws, void *stream) {
+    return guarded(nullptr, [&] {
+        require(logits_dev && out_dev && ws, SP_EINVAL, "NULL pointer");
+        require(rows >= 1 && rows <= 65535 && cols >= 1, SP_EINVAL, "rows must be in [1, 65535] and cols positive");
+        float *pv = (float *)ws;
+        int *pi = (int *)(pv + (size_t)rows * ARGMAX_BLOCKS);
+        hipStream_t st = (hipStream_t)stream;
+        hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, rows), dim3(256), 0, st, logits_dev, cols, cols, pv, pi);
+        hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pv, pi, out_dev);
+        HIPCHK(hipGetLastError());
+    });
+}
+
+}  // extern "C"
+
+struct sp_weight {
+    DevMat m;
+};
+
+extern "C" {
+
+int sp_weight_create(int32_t fmt, int32_t rows, int32_t cols, const void *data, const void *scales, const void *zeros,
+                     sp_weight **out) {
+    if (!out) { g_err = "out is NULL"; return SP_EINVAL; }
+    *out = nullptr;
+    sp_weight *w = new sp_weight();
+    int rc = guarded(nullptr, [&] {
+        require(fmt == SP_FMT_F16 || fmt == SP_FMT_Q8 || fmt == SP_FMT_Q4, SP_EINVAL, "fmt must be F16, Q8 or Q4");
+        w->m = upload_matrix(fmt, rows, cols, data, scales, zeros, false);
+    });
+    if (rc != SP_OK) { delete w; return rc; }
+    *out = w;
+    return SP_OK;
+}
+
+void sp_weight_destroy(sp_weight *w) {
+    if (!w) return;
+    w->m.release();
+    delete w;
+}
+
+uint64_t sp_weight_bytes(const sp_weight *w) { return w ? w->m.bytes : 0; }
+
+size_t sp_op_gemv_workspace(const sp_weight *w, int32_t m_cols) {
+    if (!w || m_cols < 1) return 0;
+    const int mt = (m_cols + 15) / 16;
+    GemvPlan p = plan_gemv(w->m);
+    return gemv_partial_floats(w->m, mt) * sizeof(float) + (size_t)p.units * sizeof(uint32_t) + 256;
+}
+
+int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_dev, void *ws, void *stream) {
+    return guarded(nullptr, [&] {
+        require(w && x_dev && y_dev && ws, SP_EINVAL, "NULL pointer");
+        require(m_cols >= 1 && m_cols <= 16 * GEMV_MAX_MT, SP_EINVAL, "m_cols must be in [1, 64]");
+        const int mt = (m_cols + 15) / 16;
+        const size_t pf = gemv_partial_floats(w->m, mt);
+        float *partial = (float *)ws;
+        uint32_t *counters = (uint32_t *)((char *)ws + ((pf * sizeof(float) + 255) / 256) * 256);
+        launch_gemv(w->m, EPI_STORE, (const f16 *)x_dev, w->m.cols, m_cols, y_dev, nullptr, w->m.rows, nullptr, partial,
+                    counters, (hipStream_t)stream);
+        HIPCHK(hipGetLastError());
+    });
+}
+
+}  // extern "C"

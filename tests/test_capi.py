@@ -1,0 +1,90 @@
+"""The C ABI library: it loads, exports every function include/seedplane_hip.h declares with the signatures the
+ctypes binding uses, and the struct layouts agree between C and ctypes.  No compute call needs a GPU here."""
+import ctypes
+import re
+import subprocess
+import tempfile
+from pathlib import Path
+
+import pytest
+
+from seedplane_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / 'include' / 'seedplane_hip.h'
+
+
+def declared_functions():
+    text = re.sub(r'/\*.*?\*/', '', HEADER.read_text(), flags=re.S)
+    return set(re.findall(r'\b(sp_\w+)\s*\(', text))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 19
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    assert names == set(_lib.SIGNATURES), 'ctypes signatures and header out of sync'
+
+
+def test_struct_layout_matches_c():
+    src = r'''
+    #include <stdio.h>
+    #include <stddef.h>
+    #include "seedplane_hip.h"
+    int main(void) {
+        printf("%zu %zu %zu %zu %zu\n", sizeof(sp_token), offsetof(sp_token, tree_mask), sizeof(sp_model_desc),
+               offsetof(sp_model_desc, rms_eps), offsetof(sp_model_desc, inv_freq));
+        return 0;
+    }'''
+    with tempfile.TemporaryDirectory() as d:
+        c = Path(d) / 'layout.c'
+        c.write_text(src)
+        exe = Path(d) / 'layout'
+        subprocess.run(['gcc', '-std=c99', '-I', str(HEADER.parent), str(c), '-o', str(exe)], check=True)
+        out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    got = list(map(int, out))
+    assert got == [ctypes.sizeof(_lib.Token), _lib.Token.tree_mask.offset, ctypes.sizeof(_lib.ModelDesc),
+                   _lib.ModelDesc.rms_eps.offset, _lib.ModelDesc.inv_freq.offset]
+
+
+def test_workspace_queries_are_pure_host_functions():
+    lib = _lib.load()
+    assert lib.sp_op_argmax_workspace(0, 10) == 0
+    assert lib.sp_op_argmax_workspace(3, 151936) == 3 * 64 * 8
+    assert lib.sp_op_gemv_workspace(None, 1) == 0
+
+
+def test_null_arguments_are_rejected_with_einval():
+    lib = _lib.load()
+    assert lib.sp_engine_create(None, None) == _lib.SP_EINVAL
+    assert lib.sp_engine_forward(None, 1, None, 0, None, None) == _lib.SP_EINVAL
+    assert b'NULL' in lib.sp_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(_lib.SP_EINVAL)
+
+
+def test_engine_create_without_gpu_fails_cleanly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip('a GPU is present')
+    import numpy as np
+    lib = _lib.load()
+    inv = np.ones(32, np.float32)
+    d = _lib.ModelDesc(2, 128, 2, 1, 64, 256, 50, _lib.SP_FMT_F16, 1, 8, 1e-6, 0.0,
+                       inv.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    h = ctypes.c_void_p()
+    rc = lib.sp_engine_create(ctypes.byref(d), ctypes.byref(h))
+    assert rc == _lib.SP_EHIP and not h.value
+    assert b'device' in lib.sp_last_error()
+
+
+def test_engine_rejects_unsupported_shapes_before_touching_the_gpu():
+    import numpy as np
+    lib = _lib.load()
+    inv = np.ones(48, np.float32)
+    d = _lib.ModelDesc(2, 96 * 4, 4, 1, 96, 256, 50, _lib.SP_FMT_F16, 1, 8, 1e-6, 0.0,
+                       inv.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    h = ctypes.c_void_p()
+    assert lib.sp_engine_create(ctypes.byref(d), ctypes.byref(h)) == _lib.SP_EINVAL
+    assert b'head_dim' in lib.sp_last_error()
