@@ -134,6 +134,13 @@ int sp_engine_kv_move(sp_engine *e, int32_t seq, int32_t n, const int32_t *src_s
 /* Wait for all work queued by the engine. */
 int sp_engine_sync(sp_engine *e);
 
+/* Measurement hook (no counterpart in the reference): launch the engine's own GEMV for matrix `kind` of `layer`
+ * (same packing, split and epilogue as the decode step) `iters` times over n_cols columns on the engine's stream,
+ * timed with HIP events.  Returns the average launch duration in microseconds and the packed bytes one launch
+ * reads.  Clobbers the activation buffers (not the KV cache); call between forward passes only. */
+int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_cols, int32_t iters, float *avg_us,
+                        uint64_t *bytes);
+
 /* Bytes of HBM the engine holds for weights / KV (for roofline accounting). */
 int sp_engine_bytes(const sp_engine *e, uint64_t *weight_bytes, uint64_t *kv_bytes);
 
@@ -154,6 +161,11 @@ int sp_weight_create(int32_t fmt, int32_t rows, int32_t cols, const void *data, 
 void sp_weight_destroy(sp_weight *w);
 /* HBM bytes of the packed codes + scales + zeros. */
 uint64_t sp_weight_bytes(const sp_weight *w);
+/* Host-only: the tiled layout sp_weight_create uploads, written into caller buffers (for inspection and for
+ * callers that cache packed weights).  With out_codes/out_side NULL only the sizes are returned.  pair_halves
+ * selects the SwiGLU row-group interleave used for SP_T_GATE_UP. */
+int sp_pack_matrix(int32_t fmt, int32_t rows, int32_t cols, const void *data, const void *scales, const void *zeros,
+                   int32_t pair_halves, void *out_codes, uint64_t *codes_bytes, void *out_side, uint64_t *side_bytes);
 /* y_dev[m][r] = sum_k W[r][k] * x_dev[m][k] for m < m_cols (x fp16 [m_cols][cols], y fp32 [m_cols][rows]).
  * workspace_dev must hold sp_op_gemv_workspace(w, m_cols) bytes (split-K partials and arrival counters; it must
  * be zero-filled once before first use and is left zeroed by every call). */

@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <string>
 #include <utility>
@@ -109,14 +110,19 @@ size_t gemv_partial_floats(const DevMat &m, int mt) {
     return (size_t)p.ksplit * p.units * p.rg * mt * 64 * 4;
 }
 
-template <int FMT>
-void launch_gemv_fmt(int mt, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+template <int FMT, int RG>
+void launch_gemv_rg(int mt, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
     switch (mt) {
-        case 1: hipLaunchKernelGGL((k_gemv<FMT, 1>), grid, block, smem, st, a); break;
-        case 2: hipLaunchKernelGGL((k_gemv<FMT, 2>), grid, block, smem, st, a); break;
-        case 3: hipLaunchKernelGGL((k_gemv<FMT, 3>), grid, block, smem, st, a); break;
-        default: hipLaunchKernelGGL((k_gemv<FMT, 4>), grid, block, smem, st, a); break;
+        case 1: hipLaunchKernelGGL((k_gemv<FMT, 1, RG>), grid, block, smem, st, a); break;
+        case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, RG>), grid, block, smem, st, a); break;
+        case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, RG>), grid, block, smem, st, a); break;
+        default: hipLaunchKernelGGL((k_gemv<FMT, 4, RG>), grid, block, smem, st, a); break;
     }
+}
+template <int FMT>
+void launch_gemv_fmt(int mt, bool paired, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+    if (paired) launch_gemv_rg<FMT, 2>(mt, grid, block, smem, st, a);
+    else launch_gemv_rg<FMT, 1>(mt, grid, block, smem, st, a);
 }
 
 void launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, float *out_f32, f16 *out_f16, int ldo,
@@ -134,9 +140,9 @@ void launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, flo
     dim3 grid(p.units, p.ksplit), block(64 * GEMV_NW);
     const size_t smem = (size_t)GEMV_NW * p.rg * mt * 64 * 16;
     switch (m.fmt) {
-        case 1: launch_gemv_fmt<1>(mt, grid, block, smem, st, a); break;
-        case 2: launch_gemv_fmt<2>(mt, grid, block, smem, st, a); break;
-        default: launch_gemv_fmt<3>(mt, grid, block, smem, st, a); break;
+        case 1: launch_gemv_fmt<1>(mt, m.paired, grid, block, smem, st, a); break;
+        case 2: launch_gemv_fmt<2>(mt, m.paired, grid, block, smem, st, a); break;
+        default: launch_gemv_fmt<3>(mt, m.paired, grid, block, smem, st, a); break;
     }
 }
 
@@ -167,6 +173,7 @@ struct sp_engine {
     sp_model_desc d{};
     std::string err;
     hipStream_t stream = nullptr;
+    hipStream_t capture_stream = nullptr;   // private: graphs are recorded here and launched on `stream`
     bool own_stream = false;
     int device = 0;
 
@@ -224,7 +231,9 @@ void sp_engine::free_all() {
     for (auto p : vc) dev_free(p);
     kc.clear(); vc.clear();
     if (own_stream && stream) (void)hipStreamDestroy(stream);
+    if (capture_stream) (void)hipStreamDestroy(capture_stream);
     stream = nullptr;
+    capture_stream = nullptr;
 }
 
 void sp_engine::alloc_activations() {
@@ -370,6 +379,7 @@ int sp_engine_create(const sp_model_desc *desc, sp_engine **out) {
         e->d.inv_freq = nullptr;
         HIPCHK(hipGetDevice(&e->device));
         HIPCHK(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+        HIPCHK(hipStreamCreateWithFlags(&e->capture_stream, hipStreamNonBlocking));
         e->own_stream = true;
         e->layers.resize(d.n_layers);
         e->inv_freq = dev_alloc<float>(d.head_dim / 2);
@@ -506,16 +516,22 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 e->ensure_scratch();
+                // record on the private stream (the caller's may be the null stream, which cannot capture)
                 hipGraph_t g;
+                hipStream_t run_stream = e->stream;
+                e->stream = e->capture_stream;
                 HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
                 try {
                     e->step(n, sflags, e->nchunk_for(n, toks, true));
                 } catch (...) {
                     hipGraph_t dummy;
                     (void)hipStreamEndCapture(e->stream, &dummy);
+                    e->stream = run_stream;
                     throw;
                 }
-                HIPCHK(hipStreamEndCapture(e->stream, &g));
+                hipError_t ce = hipStreamEndCapture(e->stream, &g);
+                e->stream = run_stream;
+                HIPCHK(ce);
                 hipGraphExec_t ge;
                 HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
                 (void)hipGraphDestroy(g);
@@ -565,6 +581,57 @@ int sp_engine_kv_move(sp_engine *e, int32_t seq, int32_t n, const int32_t *src, 
 int sp_engine_sync(sp_engine *e) {
     if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
     return guarded(e, [&] { HIPCHK(hipStreamSynchronize(e->stream)); });
+}
+
+int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_cols, int32_t iters, float *avg_us,
+                        uint64_t *bytes) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        const sp_model_desc &d = e->d;
+        require(avg_us && bytes, SP_EINVAL, "NULL output");
+        require(n_cols >= 1 && n_cols <= e->maxT && iters >= 1, SP_EINVAL, "n_cols must be in [1, max_tokens], iters >= 1");
+        const bool per_layer = kind == SP_T_QKV || kind == SP_T_O || kind == SP_T_GATE_UP || kind == SP_T_DOWN;
+        require(!per_layer || (layer >= 0 && layer < d.n_layers), SP_EINVAL, "layer out of range");
+        e->ensure_scratch();
+        const int H = d.hidden, I = d.intermediate, NHD = d.n_heads * d.head_dim;
+        hipStream_t st = e->stream;
+        std::function<void()> launch;
+        const DevMat *m = nullptr;
+        switch (kind) {
+            case SP_T_QKV: m = &e->layers[layer].qkv;
+                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->qkv, nullptr, e->Nqkv, e->layers[layer].qkv_b, e->gpart, e->gcnt, st); };
+                break;
+            case SP_T_O: m = &e->layers[layer].o;
+                launch = [&] { launch_gemv(*m, EPI_RESID, e->attn, NHD, n_cols, e->x, nullptr, H, nullptr, e->gpart, e->gcnt, st); };
+                break;
+            case SP_T_GATE_UP: m = &e->layers[layer].gate_up;
+                launch = [&] { launch_gemv(*m, EPI_SILU, e->xn, H, n_cols, nullptr, e->act, I, nullptr, e->gpart, e->gcnt, st); };
+                break;
+            case SP_T_DOWN: m = &e->layers[layer].down;
+                launch = [&] { launch_gemv(*m, EPI_RESID, e->act, I, n_cols, e->x, nullptr, H, nullptr, e->gpart, e->gcnt, st); };
+                break;
+            case SP_T_HEAD: case SP_T_EMBED: m = d.tied_head || kind == SP_T_EMBED ? &e->embed : &e->head;
+                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->logits, nullptr, d.vocab, nullptr, e->gpart, e->gcnt, st); };
+                break;
+            default: throw Fail{SP_EINVAL, "kind must name a matrix"};
+        }
+        require(m->w != nullptr, SP_ESTATE, "matrix not loaded");
+        hipEvent_t a, b;
+        HIPCHK(hipEventCreate(&a));
+        HIPCHK(hipEventCreate(&b));
+        launch();                       // warm-up
+        HIPCHK(hipEventRecord(a, st));
+        for (int i = 0; i < iters; ++i) launch();
+        HIPCHK(hipEventRecord(b, st));
+        HIPCHK(hipEventSynchronize(b));
+        float ms = 0.f;
+        HIPCHK(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        HIPCHK(hipGetLastError());
+        *avg_us = ms * 1000.f / iters;
+        *bytes = m->bytes;
+    });
 }
 
 int sp_engine_bytes(const sp_engine *e, uint64_t *wb, uint64_t *kb) {
@@ -622,6 +689,23 @@ void sp_weight_destroy(sp_weight *w) {
 }
 
 uint64_t sp_weight_bytes(const sp_weight *w) { return w ? w->m.bytes : 0; }
+
+int sp_pack_matrix(int32_t fmt, int32_t rows, int32_t cols, const void *data, const void *scales, const void *zeros,
+                   int32_t pair_halves, void *out_codes, uint64_t *codes_bytes, void *out_side, uint64_t *side_bytes) {
+    return guarded(nullptr, [&] {
+        require(codes_bytes && side_bytes, SP_EINVAL, "size outputs are NULL");
+        sp::Packed p;
+        try {
+            p = sp::pack_matrix(fmt, rows, cols, data, scales, zeros, pair_halves != 0);
+        } catch (const std::invalid_argument &ex) {
+            throw Fail{SP_EINVAL, ex.what()};
+        }
+        *codes_bytes = p.codes.size();
+        *side_bytes = p.sz.size() * 2;
+        if (out_codes) std::memcpy(out_codes, p.codes.data(), p.codes.size());
+        if (out_side && !p.sz.empty()) std::memcpy(out_side, p.sz.data(), p.sz.size() * 2);
+    });
+}
 
 size_t sp_op_gemv_workspace(const sp_weight *w, int32_t m_cols) {
     if (!w || m_cols < 1) return 0;

@@ -49,7 +49,7 @@ __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
     }
 }
 
-template <int FMT, int MT>
+template <int FMT, int MT, int RG>
 __global__ void __launch_bounds__(512) k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     constexpr int KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
@@ -57,12 +57,11 @@ __global__ void __launch_bounds__(512) k_gemv(GemvArgs a) {
     const int unit = blockIdx.x, split = blockIdx.y;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int RG = a.epi == EPI_SILU ? 2 : 1;
     const int kt0 = (int)((long)split * a.nkt / a.ksplit), kt1 = (int)((long)(split + 1) * a.nkt / a.ksplit);
 
-    f32x4 acc[2][MT];
+    f32x4 acc[RG][MT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RG; ++i)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[i][mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
@@ -70,17 +69,26 @@ __global__ void __launch_bounds__(512) k_gemv(GemvArgs a) {
     const f16x8 ones8 = (f16x8){1, 1, 1, 1, 1, 1, 1, 1};
 
     for (int kt = kt0 + wv; kt < kt1; kt += NW) {
-        // ---- loads: codes (1 KiB per row group), scales, activation fragments
-        u32x4 wt[2];
-        uint32_t sc8[2] = {0u, 0u};
-        u32x4 sc4[2];
+        // ---- loads: codes (1 KiB per row group), per-step scale (and zero), activation fragments
+        u32x4 wt[RG];
+        float scale[RG][ST], zero[RG][ST];
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
-            if (rg < RG) {
-                const size_t tile = (size_t)(unit * RG + rg) * a.nkt + kt;
-                wt[rg] = __builtin_nontemporal_load((const u32x4 *)(a.w + tile * TILE_BYTES) + lane);
-                if constexpr (FMT == 2) sc8[rg] = *((const uint32_t *)(a.sz + tile * 32) + r);
-                if constexpr (FMT == 3) sc4[rg] = *((const u32x4 *)(a.sz + tile * 128) + r);
+        for (int rg = 0; rg < RG; ++rg) {
+            const size_t tile = (size_t)(unit * RG + rg) * a.nkt + kt;
+            wt[rg] = __builtin_nontemporal_load((const u32x4 *)(a.w + tile * TILE_BYTES) + lane);
+            if constexpr (FMT == 2) {
+                const uint32_t d = *((const uint32_t *)(a.sz + tile * 32) + r);
+                scale[rg][0] = (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
+                scale[rg][1] = (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
+            }
+            if constexpr (FMT == 3) {
+                const uint32_t *p = (const uint32_t *)(a.sz + tile * 128) + 4 * r;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const uint32_t d = p[s];
+                    scale[rg][s] = (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
+                    zero[rg][s] = (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
+                }
             }
         }
         f16x8 xa[MT][ST];
@@ -100,27 +108,22 @@ __global__ void __launch_bounds__(512) k_gemv(GemvArgs a) {
                 for (int mt = 0; mt < MT; ++mt) xs[mt] = mfma16(xa[mt][s], ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
             }
 #pragma unroll
-            for (int rg = 0; rg < 2; ++rg) {
-                if (rg >= RG) continue;
+            for (int rg = 0; rg < RG; ++rg) {
                 const f16x8 b = unpack_step<FMT>(wt[rg], s);
                 if constexpr (FMT == 1) {
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) acc[rg][mt] = mfma16(xa[mt][s], b, acc[rg][mt]);
                 } else if constexpr (FMT == 2) {
-                    const f16x2 sp = __builtin_bit_cast(f16x2, sc8[rg]);
-                    const float scale = (float)sp[s];
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) {
                         const f32x4 d = mfma16(xa[mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
-                        acc[rg][mt] += scale * d;
+                        acc[rg][mt] += scale[rg][s] * d;
                     }
                 } else {
-                    const f16x2 szp = __builtin_bit_cast(f16x2, sc4[rg][s]);
-                    const float scale = (float)szp[0], zero = (float)szp[1];
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) {
                         const f32x4 d = mfma16(xa[mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
-                        acc[rg][mt] += scale * (d - zero * xs[mt]);
+                        acc[rg][mt] += scale[rg][s] * (d - zero[rg][s] * xs[mt]);
                     }
                 }
             }
@@ -131,17 +134,15 @@ __global__ void __launch_bounds__(512) k_gemv(GemvArgs a) {
     f32x4 *red = (f32x4 *)smem_raw;   // [NW][RG*MT][64]
     if (NW > 1) {
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg)
+        for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                if (rg < RG) red[(wv * RG * MT + rg * MT + mt) * 64 + lane] = acc[rg][mt];
+            for (int mt = 0; mt < MT; ++mt) red[(wv * RG * MT + rg * MT + mt) * 64 + lane] = acc[rg][mt];
         __syncthreads();
         if (wv != 0) return;
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg)
+        for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                if (rg >= RG) continue;
                 f32x4 t = red[(rg * MT + mt) * 64 + lane];
                 for (int w2 = 1; w2 < NW; ++w2) t += red[(w2 * RG * MT + rg * MT + mt) * 64 + lane];
                 acc[rg][mt] = t;
@@ -153,10 +154,9 @@ __global__ void __launch_bounds__(512) k_gemv(GemvArgs a) {
         f32x4 *part = (f32x4 *)a.partial;
         const size_t stride = (size_t)RG * MT * 64;
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg)
+        for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                if (rg < RG) part[((size_t)split * a.units + unit) * stride + (rg * MT + mt) * 64 + lane] = acc[rg][mt];
+            for (int mt = 0; mt < MT; ++mt) part[((size_t)split * a.units + unit) * stride + (rg * MT + mt) * 64 + lane] = acc[rg][mt];
         __threadfence();
         uint32_t prev = 0;
         if (lane == 0) prev = atomicAdd(&a.counters[unit], 1u);
@@ -164,10 +164,9 @@ __global__ void __launch_bounds__(512) k_gemv(GemvArgs a) {
         if (prev != (uint32_t)(a.ksplit - 1)) return;
         __threadfence();
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg)
+        for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                if (rg >= RG) continue;
                 f32x4 t = (f32x4){0.f, 0.f, 0.f, 0.f};
                 for (int s2 = 0; s2 < a.ksplit; ++s2)
                     t += __builtin_nontemporal_load(&part[((size_t)s2 * a.units + unit) * stride + (rg * MT + mt) * 64 + lane]);
@@ -190,8 +189,8 @@ __global__ void __launch_bounds__(512) k_gemv(GemvArgs a) {
                 a.out_f32[(size_t)m * a.ldo + n] = v;
             } else if (a.epi == EPI_RESID) {
                 a.out_f32[(size_t)m * a.ldo + n] += acc[0][mt][j];
-            } else {
-                const float gt = acc[0][mt][j], up = acc[1][mt][j];
+            } else if constexpr (RG == 2) {
+                const float gt = acc[0][mt][j], up = acc[RG - 1][mt][j];
                 a.out_f16[(size_t)m * a.ldo + n] = (f16)(silu_f(gt) * up);
             }
         }

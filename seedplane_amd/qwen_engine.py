@@ -187,6 +187,14 @@ class Qwen2Engine:
         _lib.check(self.lib.sp_engine_bytes(self.h, ctypes.byref(wb), ctypes.byref(kb)), self.h)
         return wb.value, kb.value
 
+    def time_gemv(self, kind, layer=0, n_cols=1, iters=100):
+        """Average duration (us) and packed bytes of one launch of this engine's GEMV for matrix `kind`
+        (an SP_T_* constant), timed with HIP events on the engine's stream.  Clobbers activation buffers."""
+        us, nb = ctypes.c_float(), ctypes.c_uint64()
+        _lib.check(self.lib.sp_engine_time_gemv(self.h, kind, layer, n_cols, iters, ctypes.byref(us), ctypes.byref(nb)),
+                   self.h)
+        return us.value, nb.value
+
     # ------------------------------------------------------------------------------------------ KV pool
     def reserve(self, n_seq, n_slots):
         """(Re)allocate the HBM KV pool for n_seq sequences x n_slots ring slots; invalidates existing caches."""
