@@ -167,8 +167,8 @@ uint64_t sp_weight_bytes(const sp_weight *w);
 int sp_pack_matrix(int32_t fmt, int32_t rows, int32_t cols, const void *data, const void *scales, const void *zeros,
                    int32_t pair_halves, void *out_codes, uint64_t *codes_bytes, void *out_side, uint64_t *side_bytes);
 /* y_dev[m][r] = sum_k W[r][k] * x_dev[m][k] for m < m_cols (x fp16 [m_cols][cols], y fp32 [m_cols][rows]).
- * workspace_dev must hold sp_op_gemv_workspace(w, m_cols) bytes (split-K partials and arrival counters; it must
- * be zero-filled once before first use and is left zeroed by every call). */
+ * The kernel needs no scratch: sp_op_gemv_workspace returns 0 and workspace_dev may be NULL (kept so callers
+ * need not change if a later kernel needs one). */
 size_t sp_op_gemv_workspace(const sp_weight *w, int32_t m_cols);
 int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_dev, void *workspace_dev,
                void *hip_stream);

@@ -39,17 +39,28 @@ __global__ void __launch_bounds__(256) k_embed(const uint8_t *w, const f16 *sz, 
 }
 
 // out[b][k] = fp16(x * rsqrt(mean(x^2) + eps) * w).  Replaces Qwen2Engine._norm (qwen_engine.py:90-92): the weight
-// multiply happens in fp32 before the cast.
+// multiply happens in fp32 before the cast.  One block per column, x read once into registers (H <= 16 * 256).
+constexpr int NORM_PER_THREAD = 16;
 __global__ void __launch_bounds__(256) k_rmsnorm(const float *x, int ldx, const float *w, int H, float eps, f16 *out,
                                                  int ldo) {
     __shared__ float red[16];
     const int b = blockIdx.x;
     const float *xr = x + (size_t)b * ldx;
+    float v[NORM_PER_THREAD];
     float ss = 0.f;
-    for (int k = threadIdx.x; k < H; k += blockDim.x) { const float v = xr[k]; ss += v * v; }
+#pragma unroll
+    for (int i = 0; i < NORM_PER_THREAD; ++i) {
+        const int k = threadIdx.x + i * 256;
+        v[i] = k < H ? xr[k] : 0.f;
+        ss += v[i] * v[i];
+    }
     ss = block_sum(ss, red);
     const float rs = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int k = threadIdx.x; k < H; k += blockDim.x) out[(size_t)b * ldo + k] = (f16)((xr[k] * rs) * w[k]);
+#pragma unroll
+    for (int i = 0; i < NORM_PER_THREAD; ++i) {
+        const int k = threadIdx.x + i * 256;
+        if (k < H) out[(size_t)b * ldo + k] = (f16)((v[i] * rs) * w[k]);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -115,14 +126,17 @@ __device__ __forceinline__ int att_visible(const sp_token &t, int &nlin) {
     return nlin + t.tree_count;
 }
 
+constexpr int ATT_MAX_CHUNKS = 512;
+
+// One block per (chunk of ATT_CH visible keys, kv head, column); wave h handles query head kvh*G + h: lane j scores
+// key j of the chunk, the wave takes max / exp / sum over its 64 lanes, then lanes own output dims for P.V.
 template <int HD, int G>
-__global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
+__global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
     constexpr int KP = HD + 8;                       // padded K row (halves) to spread LDS banks
     __shared__ float q_s[G][HD];
     __shared__ __align__(16) f16 k_s[ATT_CH][KP];
     __shared__ __align__(16) f16 v_s[ATT_CH][HD];
-    __shared__ float p_s[G][ATT_CH];
-    __shared__ float ml_s[G][2];
+    __shared__ float e_s[G][ATT_CH];
     __shared__ int ok_s[ATT_CH];
 
     const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -132,14 +146,14 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     const int v0 = c * ATT_CH;
     if (v0 >= nvis) return;
     const int cnt = min(ATT_CH, nvis - v0);
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
+    constexpr int NT = 64 * G;
 
-    for (int i = tid; i < G * HD; i += 256)
+    for (int i = tid; i < G * HD; i += NT)
         q_s[i / HD][i % HD] = a.q[(size_t)b * a.NH * HD + (kvh * G) * HD + i] * a.scale;
-
     const size_t head_base = ((size_t)t.seq * a.NKV + kvh) * a.n_slots;
     constexpr int CPR = HD / 8;                     // 16-byte chunks per row
-    for (int i = tid; i < cnt * CPR; i += 256) {
+    for (int i = tid; i < cnt * CPR; i += NT) {
         const int j = i / CPR, ch = i - j * CPR;
         const int vis = v0 + j;
         int slot, ok = 1;
@@ -157,66 +171,75 @@ __global__ void __launch_bounds__(256) k_attn_part(AttnArgs a) {
     }
     __syncthreads();
 
-    // scores
-    for (int p = tid; p < G * cnt; p += 256) {
-        const int h = p / cnt, j = p - h * cnt;
-        float s = -INFINITY;
-        if (ok_s[j]) {
-            float acc = 0.f;
-#pragma unroll 8
-            for (int d = 0; d < HD; d += 8) {
-                const f16x8 kv = *(const f16x8 *)&k_s[j][d];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc += q_s[h][d + e] * (float)kv[e];
-            }
-            s = acc;
-        }
-        p_s[h][j] = s;
-    }
-    __syncthreads();
-
-    // per-head max / exp / sum: one wave per head
-    const int lane = tid & 63, wv = tid >> 6;
-    for (int h = wv; h < G; h += 4) {
-        const float s = lane < cnt ? p_s[h][lane] : -INFINITY;
-        const float m = wave_max(s);
-        const float e = (m == -INFINITY || s == -INFINITY) ? 0.f : expf(s - m);
-        const float l = wave_sum(e);
-        if (lane < cnt) p_s[h][lane] = e;
-        if (lane == 0) { ml_s[h][0] = m; ml_s[h][1] = l; }
-    }
-    __syncthreads();
-
-    float *out = a.part + (((size_t)b * a.NH + kvh * G) * a.nchunk + c) * (HD + 2);
-    const size_t hstride = (size_t)a.nchunk * (HD + 2);
-    for (int o = tid; o < G * HD; o += 256) {
-        const int h = o / HD, d = o - h * HD;
+    float sc = -INFINITY;
+    if (lane < cnt && ok_s[lane]) {
         float acc = 0.f;
-        for (int j = 0; j < cnt; ++j) acc += p_s[h][j] * (float)v_s[j][d];
-        out[h * hstride + 2 + d] = acc;
+#pragma unroll 4
+        for (int d = 0; d < HD; d += 8) {
+            const f16x8 kv = *(const f16x8 *)&k_s[lane][d];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += q_s[h][d + e] * (float)kv[e];
+        }
+        sc = acc;
     }
-    if (tid < G) { out[tid * hstride] = ml_s[tid][0]; out[tid * hstride + 1] = ml_s[tid][1]; }
+    const float m = wave_max(sc);
+    const float ex = (sc == -INFINITY) ? 0.f : expf(sc - m);
+    const float l = wave_sum(ex);
+    e_s[h][lane] = ex;
+    __syncthreads();
+
+    float *out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + c) * (HD + 2);
+    constexpr int DPL = HD / 64;                    // output dims per lane
+    float o[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[i] = 0.f;
+    for (int j = 0; j < cnt; ++j) {
+        const float p = e_s[h][j];
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) o[i] += p * (float)v_s[j][lane + 64 * i];
+    }
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) out[2 + lane + 64 * i] = o[i];
+    if (lane == 0) { out[0] = m; out[1] = l; }
 }
 
-// out[b][h*HD + d] (fp16) = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}
+// out[b][h*HD + d] (fp16) = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}; one block (HD threads) per
+// (head, column), chunk statistics loaded in parallel.
 __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const sp_token *toks, int NH, int HD,
                                                       int nchunk, f16 *out, int ldo) {
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    __shared__ float w_s[ATT_MAX_CHUNKS];
+    __shared__ float red[16];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
     int nlin;
     const int nvis = att_visible(toks[b], nlin);
     const int nc = (nvis + ATT_CH - 1) / ATT_CH;
     const float *p = part + ((size_t)b * NH + h) * nchunk * (HD + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) if (p[c * (HD + 2) + 1] > 0.f) M = fmaxf(M, p[c * (HD + 2)]);
-    float L = 0.f, acc = 0.f;
-    for (int c = 0; c < nc; ++c) {
-        const float *pc = p + c * (HD + 2);
-        if (!(pc[1] > 0.f)) continue;
-        const float wgt = expf(pc[0] - M);
-        L += pc[1] * wgt;
-        if (d < HD) acc += pc[2 + d] * wgt;
+    float mloc = -INFINITY;
+    for (int c = tid; c < nc; c += nt) {
+        const float mc = p[(size_t)c * (HD + 2)], lc = p[(size_t)c * (HD + 2) + 1];
+        w_s[c] = lc > 0.f ? mc : -INFINITY;
+        mloc = fmaxf(mloc, w_s[c]);
     }
-    if (d < HD) out[(size_t)b * ldo + h * HD + d] = (f16)(acc / L);
+    // block max
+    mloc = wave_max(mloc);
+    if ((tid & 63) == 0) red[tid >> 6] = mloc;
+    __syncthreads();
+    float M = red[0];
+    for (int i = 1; i < (nt + 63) / 64; ++i) M = fmaxf(M, red[i]);
+    float lsum = 0.f;
+    for (int c = tid; c < nc; c += nt) {
+        const float wc = w_s[c] == -INFINITY ? 0.f : expf(w_s[c] - M);
+        w_s[c] = wc;
+        lsum += wc * p[(size_t)c * (HD + 2) + 1];
+    }
+    __syncthreads();
+    const float L = block_sum(lsum, red + 8);
+    if (tid < HD) {
+        float acc = 0.f;
+#pragma unroll 4
+        for (int c = 0; c < nc; ++c) acc += w_s[c] * p[(size_t)c * (HD + 2) + 2 + tid];
+        out[(size_t)b * ldo + h * HD + tid] = (f16)(acc / L);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------

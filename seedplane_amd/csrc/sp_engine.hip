@@ -83,31 +83,23 @@ DevMat upload_matrix(int fmt, int rows, int cols, const void *data, const void *
 }
 
 // ------------------------------------------------------------------------------------------- GEMV planning/launch
-constexpr int GEMV_NW = 4;
 constexpr int GEMV_MAX_MT = 4;
 
 struct GemvPlan {
-    int units, ksplit, rg;
+    int units, nw, rg;
 };
 
+// One block per unit; waves per block chosen so that each wave owns at least ~2 k-tiles and small matrices still
+// spread over many waves (bs1 GEMVs are latency-bound).
 GemvPlan plan_gemv(const DevMat &m) {
     GemvPlan p;
     p.rg = m.paired ? 2 : 1;
     p.units = m.rows_pad / 16 / p.rg;
-    p.ksplit = 1;
-    const int target_blocks = 1024;
-    if (p.units < target_blocks) {
-        const int by_work = std::max(1, m.nkt / (GEMV_NW * 2));
-        const int by_fill = (target_blocks + p.units - 1) / p.units;
-        p.ksplit = std::max(1, std::min(by_work, by_fill));
-    }
+    int nw = 16;
+    while (nw > 4 && m.nkt < 2 * nw) nw >>= 1;
+    if (p.units >= 4096 && nw > 8) nw = 8;
+    p.nw = nw;
     return p;
-}
-
-size_t gemv_partial_floats(const DevMat &m, int mt) {
-    GemvPlan p = plan_gemv(m);
-    if (p.ksplit == 1) return 0;
-    return (size_t)p.ksplit * p.units * p.rg * mt * 64 * 4;
 }
 
 template <int FMT, int RG>
@@ -126,7 +118,7 @@ void launch_gemv_fmt(int mt, bool paired, dim3 grid, dim3 block, size_t smem, hi
 }
 
 void launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, float *out_f32, f16 *out_f16, int ldo,
-                 const float *bias, float *partial, uint32_t *counters, hipStream_t st) {
+                 const float *bias, hipStream_t st) {
     require(mcols >= 1 && mcols <= 16 * GEMV_MAX_MT, SP_EINVAL, "gemv columns out of range");
     require((epi == EPI_SILU) == m.paired, SP_EINVAL, "gemv epilogue does not match the matrix packing");
     GemvPlan p = plan_gemv(m);
@@ -135,10 +127,9 @@ void launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, flo
     a.w = m.w; a.sz = m.sz; a.nkt = m.nkt; a.units = p.units;
     a.n_real = m.paired ? m.rows / 2 : m.rows;
     a.x = x; a.ldx = ldx; a.m = mcols;
-    a.out_f32 = out_f32; a.out_f16 = out_f16; a.ldo = ldo; a.bias = bias;
-    a.partial = partial; a.counters = counters; a.ksplit = p.ksplit; a.epi = epi;
-    dim3 grid(p.units, p.ksplit), block(64 * GEMV_NW);
-    const size_t smem = (size_t)GEMV_NW * p.rg * mt * 64 * 16;
+    a.out_f32 = out_f32; a.out_f16 = out_f16; a.ldo = ldo; a.bias = bias; a.epi = epi;
+    dim3 grid(p.units), block(64 * p.nw);
+    const size_t smem = (size_t)p.nw * p.rg * mt * 64 * 16;
     switch (m.fmt) {
         case 1: launch_gemv_fmt<1>(mt, m.paired, grid, block, smem, st, a); break;
         case 2: launch_gemv_fmt<2>(mt, m.paired, grid, block, smem, st, a); break;
@@ -150,14 +141,14 @@ void launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, flo
 template <int HD>
 void launch_attn_hd(int G, dim3 grid, hipStream_t st, const AttnArgs &a) {
     switch (G) {
-        case 1: hipLaunchKernelGGL((k_attn_part<HD, 1>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((k_attn_part<HD, 2>), grid, dim3(256), 0, st, a); break;
-        case 3: hipLaunchKernelGGL((k_attn_part<HD, 3>), grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((k_attn_part<HD, 4>), grid, dim3(256), 0, st, a); break;
-        case 5: hipLaunchKernelGGL((k_attn_part<HD, 5>), grid, dim3(256), 0, st, a); break;
-        case 6: hipLaunchKernelGGL((k_attn_part<HD, 6>), grid, dim3(256), 0, st, a); break;
-        case 7: hipLaunchKernelGGL((k_attn_part<HD, 7>), grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL((k_attn_part<HD, 8>), grid, dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((k_attn_part<HD, 1>), grid, dim3(64 * 1), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((k_attn_part<HD, 2>), grid, dim3(64 * 2), 0, st, a); break;
+        case 3: hipLaunchKernelGGL((k_attn_part<HD, 3>), grid, dim3(64 * 3), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((k_attn_part<HD, 4>), grid, dim3(64 * 4), 0, st, a); break;
+        case 5: hipLaunchKernelGGL((k_attn_part<HD, 5>), grid, dim3(64 * 5), 0, st, a); break;
+        case 6: hipLaunchKernelGGL((k_attn_part<HD, 6>), grid, dim3(64 * 6), 0, st, a); break;
+        case 7: hipLaunchKernelGGL((k_attn_part<HD, 7>), grid, dim3(64 * 7), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_attn_part<HD, 8>), grid, dim3(64 * 8), 0, st, a); break;
     }
 }
 
@@ -190,10 +181,6 @@ struct sp_engine {
     int Nqkv = 0, maxT = 0, max_nchunk = 0;
     float *x = nullptr, *qkv = nullptr, *q = nullptr, *logits = nullptr, *attn_part = nullptr;
     f16 *xn = nullptr, *attn = nullptr, *act = nullptr;
-    float *gpart = nullptr;
-    uint32_t *gcnt = nullptr;
-    size_t gpart_floats = 0;
-    int gcnt_len = 0;
     float *am_v = nullptr;
     int *am_i = nullptr, *am_out = nullptr;
     sp_token *dtoks = nullptr;
@@ -208,7 +195,6 @@ struct sp_engine {
 
     void free_all();
     void alloc_activations();
-    void ensure_scratch();
     void step(int n, int flags, int nchunk);
     int nchunk_for(int n, const sp_token *t, bool graph) const;
 };
@@ -224,7 +210,7 @@ void sp_engine::free_all() {
     embed.release(); head.release();
     dev_free(final_norm); dev_free(inv_freq);
     for (void *p : {(void *)x, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)xn, (void *)attn,
-                    (void *)act, (void *)gpart, (void *)gcnt, (void *)am_v, (void *)am_i, (void *)am_out,
+                    (void *)act, (void *)am_v, (void *)am_i, (void *)am_out,
                     (void *)dtoks, (void *)d_kl, (void *)d_vl, (void *)d_move})
         dev_free(p);
     for (auto p : kc) dev_free(p);
@@ -258,31 +244,6 @@ void sp_engine::alloc_activations() {
     HIPCHK(hipMemset(act, 0, (size_t)maxT * I * sizeof(f16)));
 }
 
-// split-K scratch sized for the loaded matrices at the largest column count
-void sp_engine::ensure_scratch() {
-    const int mt = (maxT + 15) / 16;
-    size_t need = 0;
-    int units = 0;
-    auto visit = [&](const DevMat &m) {
-        if (!m.w) return;
-        need = std::max(need, gemv_partial_floats(m, mt));
-        units = std::max(units, plan_gemv(m).units);
-    };
-    for (auto &l : layers) { visit(l.qkv); visit(l.o); visit(l.gate_up); visit(l.down); }
-    visit(embed); visit(head);
-    if (need > gpart_floats) {
-        dev_free(gpart);
-        gpart = dev_alloc<float>(need);
-        gpart_floats = need;
-    }
-    if (units > gcnt_len) {
-        dev_free(gcnt);
-        gcnt = dev_alloc<uint32_t>(units);
-        HIPCHK(hipMemset(gcnt, 0, units * sizeof(uint32_t)));
-        gcnt_len = units;
-    }
-}
-
 int sp_engine::nchunk_for(int n, const sp_token *t, bool graph) const {
     if (graph) return (n_slots + 64 + ATT_CH - 1) / ATT_CH;
     int mx = 1;
@@ -305,7 +266,7 @@ void sp_engine::step(int n, int flags, int nchunk) {
     for (int l = 0; l < d.n_layers; ++l) {
         Layer &ly = layers[l];
         hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, ly.in_norm, H, d.rms_eps, xn, H);
-        launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, gpart, gcnt, st);
+        launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st);
         RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots};
         hipLaunchKernelGGL(k_rope_kv, dim3(n), dim3(256), 0, st, ra);
         if (l + 1 == d.n_layers && !logits_on) break;   // K/V-only: the last layer only needs its K/V
@@ -315,15 +276,15 @@ void sp_engine::step(int n, int flags, int nchunk) {
         if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
         else launch_attn_hd<128>(G, agrid, st, aa);
         hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dtoks, NH, HD, nchunk, attn, NH * HD);
-        launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, gpart, gcnt, st);
+        launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, st);
         hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, ly.post_norm, H, d.rms_eps, xn, H);
-        launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, gpart, gcnt, st);
-        launch_gemv(ly.down, EPI_RESID, act, I, n, x, nullptr, H, nullptr, gpart, gcnt, st);
+        launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, st);
+        launch_gemv(ly.down, EPI_RESID, act, I, n, x, nullptr, H, nullptr, st);
     }
     if (logits_on) {
         hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, final_norm, H, d.rms_eps, xn, H);
         const DevMat &hm = d.tied_head ? embed : head;
-        launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, gpart, gcnt, st);
+        launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, st);
         if (flags & SP_F_ARGMAX) {
             hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, n), dim3(256), 0, st, logits, d.vocab, d.vocab, am_v, am_i);
             hipLaunchKernelGGL(k_argmax_final, dim3(n), dim3(64), 0, st, am_v, am_i, am_out);
@@ -375,6 +336,7 @@ int sp_engine_create(const sp_model_desc *desc, sp_engine **out) {
         require(d.hidden % 128 == 0 && d.intermediate % 128 == 0 && (d.n_heads * d.head_dim) % 128 == 0, SP_EINVAL,
                 "hidden, intermediate and heads*head_dim must be multiples of 128");
         require(d.inv_freq != nullptr, SP_EINVAL, "inv_freq is NULL");
+        require(d.hidden <= NORM_PER_THREAD * 256, SP_EINVAL, "hidden must be <= 4096");
         e->d = d;
         e->d.inv_freq = nullptr;
         HIPCHK(hipGetDevice(&e->device));
@@ -455,6 +417,7 @@ int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots) {
     if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
     return guarded(e, [&] {
         require(n_seq >= 1 && n_slots >= 1, SP_EINVAL, "n_seq and n_slots must be positive");
+        require((n_slots + 64 + ATT_CH - 1) / ATT_CH <= ATT_MAX_CHUNKS, SP_EINVAL, "n_slots too large for the attention combine");
         HIPCHK(hipStreamSynchronize(e->stream));
         for (auto p : e->kc) dev_free(p);
         for (auto p : e->vc) dev_free(p);
@@ -515,7 +478,6 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             auto key = std::make_pair(n, sflags);
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
-                e->ensure_scratch();
                 // record on the private stream (the caller's may be the null stream, which cannot capture)
                 hipGraph_t g;
                 hipStream_t run_stream = e->stream;
@@ -539,7 +501,6 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             }
             HIPCHK(hipGraphLaunch(it->second, e->stream));
         } else {
-            e->ensure_scratch();
             e->step(n, sflags, e->nchunk_for(n, toks, false));
         }
         if (logits_dev && (flags & SP_F_LOGITS))
@@ -592,26 +553,25 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
         require(n_cols >= 1 && n_cols <= e->maxT && iters >= 1, SP_EINVAL, "n_cols must be in [1, max_tokens], iters >= 1");
         const bool per_layer = kind == SP_T_QKV || kind == SP_T_O || kind == SP_T_GATE_UP || kind == SP_T_DOWN;
         require(!per_layer || (layer >= 0 && layer < d.n_layers), SP_EINVAL, "layer out of range");
-        e->ensure_scratch();
         const int H = d.hidden, I = d.intermediate, NHD = d.n_heads * d.head_dim;
         hipStream_t st = e->stream;
         std::function<void()> launch;
         const DevMat *m = nullptr;
         switch (kind) {
             case SP_T_QKV: m = &e->layers[layer].qkv;
-                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->qkv, nullptr, e->Nqkv, e->layers[layer].qkv_b, e->gpart, e->gcnt, st); };
+                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->qkv, nullptr, e->Nqkv, e->layers[layer].qkv_b, st); };
                 break;
             case SP_T_O: m = &e->layers[layer].o;
-                launch = [&] { launch_gemv(*m, EPI_RESID, e->attn, NHD, n_cols, e->x, nullptr, H, nullptr, e->gpart, e->gcnt, st); };
+                launch = [&] { launch_gemv(*m, EPI_RESID, e->attn, NHD, n_cols, e->x, nullptr, H, nullptr, st); };
                 break;
             case SP_T_GATE_UP: m = &e->layers[layer].gate_up;
-                launch = [&] { launch_gemv(*m, EPI_SILU, e->xn, H, n_cols, nullptr, e->act, I, nullptr, e->gpart, e->gcnt, st); };
+                launch = [&] { launch_gemv(*m, EPI_SILU, e->xn, H, n_cols, nullptr, e->act, I, nullptr, st); };
                 break;
             case SP_T_DOWN: m = &e->layers[layer].down;
-                launch = [&] { launch_gemv(*m, EPI_RESID, e->act, I, n_cols, e->x, nullptr, H, nullptr, e->gpart, e->gcnt, st); };
+                launch = [&] { launch_gemv(*m, EPI_RESID, e->act, I, n_cols, e->x, nullptr, H, nullptr, st); };
                 break;
             case SP_T_HEAD: case SP_T_EMBED: m = d.tied_head || kind == SP_T_EMBED ? &e->embed : &e->head;
-                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->logits, nullptr, d.vocab, nullptr, e->gpart, e->gcnt, st); };
+                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->logits, nullptr, d.vocab, nullptr, st); };
                 break;
             default: throw Fail{SP_EINVAL, "kind must name a matrix"};
         }
@@ -708,22 +668,17 @@ int sp_pack_matrix(int32_t fmt, int32_t rows, int32_t cols, const void *data, co
 }
 
 size_t sp_op_gemv_workspace(const sp_weight *w, int32_t m_cols) {
-    if (!w || m_cols < 1) return 0;
-    const int mt = (m_cols + 15) / 16;
-    GemvPlan p = plan_gemv(w->m);
-    return gemv_partial_floats(w->m, mt) * sizeof(float) + (size_t)p.units * sizeof(uint32_t) + 256;
+    (void)w; (void)m_cols;
+    return 0;
 }
 
 int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_dev, void *ws, void *stream) {
+    (void)ws;
     return guarded(nullptr, [&] {
-        require(w && x_dev && y_dev && ws, SP_EINVAL, "NULL pointer");
+        require(w && x_dev && y_dev, SP_EINVAL, "NULL pointer");
         require(m_cols >= 1 && m_cols <= 16 * GEMV_MAX_MT, SP_EINVAL, "m_cols must be in [1, 64]");
-        const int mt = (m_cols + 15) / 16;
-        const size_t pf = gemv_partial_floats(w->m, mt);
-        float *partial = (float *)ws;
-        uint32_t *counters = (uint32_t *)((char *)ws + ((pf * sizeof(float) + 255) / 256) * 256);
-        launch_gemv(w->m, EPI_STORE, (const f16 *)x_dev, w->m.cols, m_cols, y_dev, nullptr, w->m.rows, nullptr, partial,
-                    counters, (hipStream_t)stream);
+        launch_gemv(w->m, EPI_STORE, (const f16 *)x_dev, w->m.cols, m_cols, y_dev, nullptr, w->m.rows, nullptr,
+                    (hipStream_t)stream);
         HIPCHK(hipGetLastError());
     });
 }
