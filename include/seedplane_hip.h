@@ -173,6 +173,32 @@ size_t sp_op_gemv_workspace(const sp_weight *w, int32_t m_cols);
 int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_dev, void *workspace_dev,
                void *hip_stream);
 
+/* ---------------------------------------------------------------- seeded sampling and speculative acceptance
+ * Distributions are softmax(logits / temperature) of fp32 rows, evaluated in float64 with a fixed summation order
+ * (rows cut into 1024 contiguous chunks, each summed in index order, chunk sums added in chunk order), so a CPU
+ * restatement reproduces every draw and decision from the same logits and uniforms. */
+
+/* Replaces the T > 0 branch of Qwen2Engine.sample (qwen_engine.py:149-156, torch.multinomial) and the native
+ * Sampler::draw inverse CDF (native/vulkan_decode/sampler.hpp:93-97) with seeded uniforms: out_dev[s] = the first
+ * index whose cumulative softmax mass of row row_dev[s] exceeds u_dev[s] * total.  All pointers are device memory. */
+int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32_t *row_dev, const double *u_dev,
+                 int32_t n, double temperature, int32_t *out_dev, void *hip_stream);
+
+/* No counterpart in the reference, whose verifier is greedy only (seedplane/speculative.py:55-92; README.md:69):
+ * speculative acceptance over a draft tree with residual resampling.  Node 0 is the root (the last committed
+ * token).  The trials of node i are trials_dev[trial_start[i] .. trial_start[i] + n_trials[i]): the child each
+ * draft branch through node i drew, in branch (draw) order, repeats kept.  p_logits_dev: target logits per node;
+ * q_logits_dev: drafter logits per node (read for nodes with trials).  A trial of child x is accepted iff
+ * u < p(x) / q(x); a rejection replaces p by norm(max(p - q, 0)); with every trial rejected the final token is drawn
+ * from that residual, after an accepted leaf (or max_depth levels) a bonus token is drawn from the target.
+ * Uniforms u_dev[0..n_u) are consumed in that order.  out_dev (int32, max_depth + 4 entries): [0] accepted count k,
+ * [1..k] accepted node ids, [max_depth+1] final token, [max_depth+2] uniforms used, [max_depth+3] 1 for a bonus
+ * draw.  resid_dev: vocab doubles of scratch.  token/trial_start/n_trials are device int32 [n_nodes]. */
+int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld, int32_t n_nodes,
+                      const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
+                      const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,
+                      double temperature, int32_t max_depth, double *resid_dev, int32_t *out_dev, void *hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

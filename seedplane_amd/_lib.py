@@ -59,6 +59,11 @@ SIGNATURES = {
                                ctypes.POINTER(c_uint64), c_void_p, ctypes.POINTER(c_uint64)]),
     'sp_op_gemv_workspace': (c_size_t, [c_void_p, c_int32]),
     'sp_op_gemv': (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
+    'sp_op_sample': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_int32, ctypes.c_double, c_void_p,
+                             c_void_p]),
+    'sp_op_accept_tree': (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                  c_void_p, c_int32, c_void_p, c_int32, ctypes.c_double, c_int32, c_void_p, c_void_p,
+                                  c_void_p]),
 }
 
 _lib = None

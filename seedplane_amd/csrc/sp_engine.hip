@@ -18,6 +18,7 @@
 #include "sp_attn.h"
 #include "sp_gemv.h"
 #include "sp_pack.h"
+#include "sp_sample.h"
 
 namespace {
 
@@ -679,6 +680,56 @@ int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_d
         require(m_cols >= 1 && m_cols <= 16 * GEMV_MAX_MT, SP_EINVAL, "m_cols must be in [1, 64]");
         launch_gemv(w->m, EPI_STORE, (const f16 *)x_dev, w->m.cols, m_cols, y_dev, nullptr, w->m.rows, nullptr,
                     (hipStream_t)stream);
+        HIPCHK(hipGetLastError());
+    });
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32_t *row_dev, const double *u_dev,
+                 int32_t n, double temperature, int32_t *out_dev, void *stream) {
+    return guarded(nullptr, [&] {
+        require(logits_dev && row_dev && u_dev && out_dev, SP_EINVAL, "NULL pointer");
+        require(vocab >= 1 && ld >= vocab && n >= 1 && n <= 65535, SP_EINVAL, "bad sizes");
+        require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
+        hipLaunchKernelGGL(k_sample, dim3(n), dim3(SMP_THREADS), 0, (hipStream_t)stream, logits_dev, vocab, ld, row_dev,
+                           u_dev, 1.0 / temperature, out_dev);
+        HIPCHK(hipGetLastError());
+    });
+}
+
+int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld, int32_t n_nodes,
+                      const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
+                      const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,
+                      double temperature, int32_t max_depth, double *resid_dev, int32_t *out_dev, void *stream) {
+    return guarded(nullptr, [&] {
+        require(p_logits_dev && q_logits_dev && token_dev && trial_start_dev && n_trials_dev && trials_dev && u_dev &&
+                    resid_dev && out_dev, SP_EINVAL, "NULL pointer");
+        require(n_trials_total >= 0 && n_trials_total <= 4096, SP_EINVAL, "n_trials_total must be in [0, 4096]");
+        require(vocab >= 1 && ld >= vocab, SP_EINVAL, "bad vocab / ld");
+        require(n_nodes >= 1 && n_nodes <= 64, SP_EINVAL, "n_nodes must be in [1, 64]");
+        require(max_depth >= 1 && max_depth <= 63, SP_EINVAL, "max_depth must be in [1, 63]");
+        require(n_u >= 1, SP_EINVAL, "need at least one uniform");
+        require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
+        // the walk indexes nodes, trials and logits rows through these arrays: check them on the host first
+        std::vector<int32_t> tok(n_nodes), ts(n_nodes), nt(n_nodes), tr(std::max(n_trials_total, 1));
+        hipStream_t st = (hipStream_t)stream;
+        HIPCHK(hipMemcpyAsync(tok.data(), token_dev, n_nodes * 4, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipMemcpyAsync(ts.data(), trial_start_dev, n_nodes * 4, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipMemcpyAsync(nt.data(), n_trials_dev, n_nodes * 4, hipMemcpyDeviceToHost, st));
+        if (n_trials_total) HIPCHK(hipMemcpyAsync(tr.data(), trials_dev, n_trials_total * 4, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+        for (int i = 0; i < n_nodes; ++i) {
+            require(tok[i] >= 0 && tok[i] < vocab, SP_EINVAL, "node token out of range");
+            require(ts[i] >= 0 && nt[i] >= 0 && ts[i] + nt[i] <= n_trials_total, SP_EINVAL, "trial range out of bounds");
+        }
+        for (int j = 0; j < n_trials_total; ++j)
+            require(tr[j] > 0 && tr[j] < n_nodes, SP_EINVAL, "trial child index out of range");
+        AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token_dev, trial_start_dev, n_trials_dev, trials_dev, u_dev,
+                     n_u, 1.0 / temperature, resid_dev, out_dev, max_depth};
+        hipLaunchKernelGGL(k_accept_tree, dim3(1), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
         HIPCHK(hipGetLastError());
     });
 }

@@ -1,0 +1,137 @@
+"""Speculative verification on the GPU against the oracle: seeded draws and tree acceptance bit-exact given identical
+logits and uniforms (every compared decision is checked to lie outside rounding of its threshold), tree-masked
+logits equal linear causal logits of each root path, greedy tree verification equals the reference verify_greedy,
+and the KV compaction keeps later decoding consistent."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import speculative_ref as sref
+from oracle.qwen_ref import RefQwen2, max_rel, top2_margin
+from seedplane_amd import _lib
+from seedplane_amd.qwen_engine import Qwen2Engine
+from seedplane_amd.speculative import (SpecStats, SpeculativeForest, TreeDrafter, TreeVerifier, flatten, sample_rows,
+                                       speculative_generate, uniforms)
+from seedplane_amd.synth import make_weights, random_prompt
+from tests.conftest import small_cfg
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+MARGIN = 1e-12
+
+
+@pytest.fixture(scope='module')
+def model(gpu_device):
+    cfg, w = make_weights(small_cfg(), 'q8', seed=21)
+    return cfg, w, Qwen2Engine(config=cfg, tensors=w, max_tokens=64), RefQwen2(cfg, w)
+
+
+@pytest.mark.parametrize('V,T', [(50, 0.8), (151936, 0.8), (151936, 1.0), (1000, 0.3)])
+def test_sample_matches_oracle(gpu_device, V, T):
+    print(f'sample V={V} T={T}', flush=True)
+    g = torch.Generator().manual_seed(V)
+    logits = torch.randn(4, V, generator=g) * 3
+    rows = [0, 1, 2, 3, 0, 0, 1]
+    u = sref.uniforms(5, V, len(rows))
+    got = sample_rows(_lib.load(), logits.to(gpu_device), rows, u, T)
+    for s, r in enumerate(rows):
+        tok, margin = sref.draw(sref.softmax_weights(logits[r].numpy(), T), u[s])
+        assert margin > MARGIN
+        assert got[s] == tok, (s, r)
+
+
+def _random_case(rng, V, n_branches=8, depth=4, noise=0.3):
+    branches = [[int(rng.integers(0, min(V, 6))) if rng.random() < 0.5 else int(rng.integers(0, V))
+                 for _ in range(depth)] for _ in range(n_branches)]
+    tree = flatten(int(rng.integers(0, V)), branches)
+    base = rng.normal(size=(tree.size, V)).astype(np.float32) * 2
+    for i in range(1, tree.size):          # make the target like the drafted tokens, so some trials accept
+        base[tree.parent[i], tree.token[i]] += 3.0
+    p = base
+    q = (base + rng.normal(size=base.shape).astype(np.float32) * noise).astype(np.float32)
+    return tree, p, q
+
+
+@pytest.mark.parametrize('V', [64, 151936])
+def test_accept_tree_matches_oracle(model, V):
+    cfg, w, eng, _ = model
+    verifier = TreeVerifier(eng)
+    rng = np.random.default_rng(V)
+    accepted_total = 0
+    for case in range(12 if V < 1000 else 4):
+        print(f'accept V={V} case={case}', flush=True)
+        tree, p, q = _random_case(rng, V)
+        u = sref.uniforms(9, case, 64)
+        dev = eng.device
+        got = verifier.accept(torch.from_numpy(p).to(dev), torch.from_numpy(q).to(dev), tree, u, 0.8)
+        t = dict(token=tree.token, trial_start=tree.trial_start, n_trials=tree.n_trials, trials=tree.trials)
+        path, final, used, bonus, margin = sref.accept_tree(p, q, t, u, 0.8, tree.max_depth)
+        assert margin > MARGIN
+        assert (got[0], got[1], got[2], got[3]) == (path, final, used, bonus)
+        accepted_total += len(path)
+    assert accepted_total > 0       # the cases exercise acceptance, not only rejection
+
+
+def test_tree_pass_equals_linear_paths(model):
+    cfg, w, eng, _ = model
+    prefix = random_prompt(12, cfg['vocab_size'], seed=4)
+    branches = [[3, 4, 5], [3, 4, 9], [3, 7], [11, 12, 13, 14]]
+    verifier = TreeVerifier(eng)
+    cache = eng.new_cache(64)
+    eng.forward(prefix[:-1], cache)
+    tree = flatten(prefix[-1], branches)
+    out = torch.empty((tree.size, cfg['vocab_size']), dtype=torch.float32, device=eng.device)
+    ids = verifier.forward(cache, tree, logits_out=out)
+    assert cache.length == len(prefix) - 1
+    for i in range(tree.size):
+        path, j = [], i
+        while j > 0:
+            path.append(tree.token[j]); j = tree.parent[j]
+        seq = prefix + path[::-1]
+        lin, _ = eng.forward(seq, eng.new_cache(64), all_logits=True)
+        assert max_rel(out[i], lin[-1]) < TOL, i
+        if int(ids[i]) != int(torch.argmax(lin[-1])):
+            assert top2_margin(lin[-1]) <= TOL * float(lin[-1].abs().max())
+
+
+def test_greedy_tree_verification_equals_reference_semantics(model):
+    cfg, w, eng, ref = model
+    prefix = random_prompt(10, cfg['vocab_size'], seed=8)
+    greedy, _ = ref.generate_greedy(prefix, 4)
+    branches = [greedy[:2] + [1, 2], greedy[:4], [greedy[0], 77], [5, 6], greedy[:3]]
+    forest = SpeculativeForest.build(branches)
+
+    def target_logits(seq):                      # reference contract: one position per call, from scratch
+        c = ref.new_cache(len(seq))
+        return ref.forward(list(seq), c)[-1].tolist()
+    exp = sref.verify_greedy(prefix, sref.Forest.build(branches), target_logits)
+    cache = eng.new_cache(64)
+    eng.forward(prefix[:-1], cache)
+    got = TreeVerifier(eng).verify_greedy(cache, prefix, forest)
+    assert (got.emitted, got.accepted_draft_tokens, got.rejected, got.target_steps, got.branch) == exp
+    # the cache now holds everything emitted except the last token: continue greedily and compare with a fresh run
+    seq = prefix + list(got.emitted)
+    assert cache.length == len(seq) - 1
+    cont = []
+    tok = seq[-1]
+    for _ in range(4):
+        tok = int(eng.decode([tok], [cache], graph=False)[0])
+        cont.append(tok)
+    fresh = list(eng.generate(seq, max_new_tokens=4))
+    rows = ref.teacher_forced(seq, cont)
+    for a, b, row in zip(cont, fresh, rows):
+        if a != b:
+            assert top2_margin(row) <= TOL * float(row.abs().max())
+
+
+def test_identical_drafter_accepts_every_draft(model, gpu_device):
+    cfg, w, eng, _ = model
+    drafter = TreeDrafter(Qwen2Engine(config=cfg, tensors=w, max_tokens=64))
+    stats = SpecStats()
+    prompt = random_prompt(9, cfg['vocab_size'], seed=2)
+    out = speculative_generate(eng, drafter, prompt, steps=4, n_branches=4, depth=3, temperature=0.8, seed=1,
+                               stats=stats)
+    # p == q up to fp16-class noise: every first trial accepts (u < ratio ~ 1) except near-ties, so nearly every
+    # step keeps all `depth` drafts plus a bonus
+    assert stats.steps == 4 and len(out) == stats.emitted
+    assert stats.accepted >= 3 * stats.steps - 2
