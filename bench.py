@@ -1,15 +1,21 @@
 #!/usr/bin/env python3
-"""Decode throughput of the MI355X Qwen2 decode step (one GPU).
+"""Decode throughput of the MI355X Qwen2 decode step (one GPU) and the cost of speculative tree verification.
 
-Workload (default): Qwen2-1.5B shape, int8 weights in blocks of 32 along K with one fp16 scale per block (codes
-uniform in [-127, 127], scales |N(0, 0.002)|), fp16 KV in a sliding window of 1024 positions, a 3840-token prompt
-prefilled K/V-only, then greedy decode at batch 1 -- one step = one token through all 28 layers, the LM head and the
-argmax.  Synthetic random-init weights (no checkpoints offline); inputs resident in HBM before the timed region.
+Default workload (the `value`): Qwen2-1.5B shape, int8 weights in blocks of 32 along K with one fp16 scale per
+block (codes uniform in [-127, 127], scales |N(0, 0.002)|), fp16 KV in a sliding window of 1024 positions, a
+3840-token prompt prefilled K/V-only through the engine, then greedy decode at batch 1 -- one step = one token
+through all 28 layers, the LM head and the argmax, run as one captured hipGraph.  Synthetic random-init weights (no
+checkpoints offline); inputs resident in HBM before the timed region.
 
-Printed JSON line: value = batch-1 decode tok/s; `hbm_frac_step` = algorithmic bytes per token (packed weights + the
-KV window read) x tok/s / 8 TB/s; `bs16` = the same model decoding 16 sequences at once; `roofline` = the dominant
-kernel (the SwiGLU gate_up GEMV, the largest launch of the step) timed with HIP events on the engine's stream;
-`cpu_baseline` = the CPU oracle (fp32, dequantised weights) on a bounded sample of the same workload.
+The JSON line also carries:
+  hbm_frac_step  algorithmic bytes per token (packed weights + the KV window read) x tok/s / 8 TB/s
+  bs16           the same model decoding 16 sequences at once (16 x 3840-token prompts)
+  verify         tree verification on the same model over a 2048-position prefix: one pass over 1 + 32 nodes
+                 (8 branches x 4 tokens) plus the acceptance kernel, divided by one decode step at that prefix
+  roofline       the dominant kernel (the SwiGLU gate_up GEMV, the largest launch of the step), HIP-event timed
+  cpu_baseline   the CPU oracle (fp32, dequantised weights) on a bounded sample of the same workload
+Other workloads (--workload): 'c2' 0.5B fp16 16-request burst, 'c5' 7B int4 batch 32 at 8k context, 'spec' the full
+speculative loop with a 0.5B fp16 drafter.
 """
 import argparse
 import json
@@ -22,6 +28,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM = 8.0e12
+PEAK_F16 = 2.5e15
 METRIC = 'decode tok/s (bs1, bs16) + % HBM peak, Qwen2-1.5B shape; verify cost/step'
 
 
@@ -29,24 +36,24 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kv_bytes_per_token(cfg, visible):
+def kv_bytes(cfg, visible):
     HD = cfg['hidden_size'] // cfg['num_attention_heads']
     return cfg['num_hidden_layers'] * cfg['num_key_value_heads'] * HD * 2 * 2 * visible
 
 
-def decode_run(eng, caches, first, steps, graph=True):
+def sync():
     import torch
-    toks = list(first)
     torch.cuda.synchronize()
+
+
+def decode_run(eng, caches, first, steps, graph=True):
+    toks = list(first)
+    sync()
     t0 = time.perf_counter()
     for _ in range(steps):
         toks = [int(t) for t in eng.decode(toks, caches, graph=graph)]
-    torch.cuda.synchronize()
+    sync()
     return time.perf_counter() - t0, toks
-
-
-def prefill_all(eng, caches, prompts):
-    return eng.prefill(prompts, caches)
 
 
 def cpu_baseline(cfg, tensors, window, sample_tokens):
@@ -76,29 +83,65 @@ def cpu_baseline(cfg, tensors, window, sample_tokens):
                       f'dequantised to fp32 (4x the bytes), median of 3 after a warm-up'}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=256)
-    ap.add_argument('--warmup', type=int, default=16)
-    ap.add_argument('--no-bs16', action='store_true')
-    ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--cpu-sample-tokens', type=int, default=6)
-    ap.add_argument('--prompt', type=int, default=3840)
-    ap.add_argument('--window', type=int, default=1024)
-    ap.add_argument('--layers', type=int, default=None, help='(debug) fewer layers; the result is then not the metric')
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(json.dumps({'error': 'this build measures one GPU only: run with --gpus 1 (no multi-GPU path exists)'}))
-        sys.exit(2)
+def verify_cost(eng, cfg, prefix=2048, n_branches=8, depth=4, reps=20):
+    """Tree verification vs one decode step over the same 2048-position prefix (full attention)."""
+    import numpy as np
+    import torch
+    from seedplane_amd.speculative import TreeVerifier, flatten, uniforms
+    from seedplane_amd.synth import random_prompt
+    V = cfg['vocab_size']
+    eng.reserve(1, prefix + 2 * 64 + 64)
+    cache = eng.new_cache(prefix + 2 * 64)
+    eng.fill_cache(cache, prefix, seed=7)
+    rng = np.random.default_rng(0)
+    branches = [list(rng.integers(0, V, depth)) for _ in range(n_branches)]
+    tree = flatten(int(rng.integers(0, V)), branches)
+    verifier = TreeVerifier(eng)
+    p = torch.empty((tree.size, V), dtype=torch.float32, device=eng.device)
+    for _ in range(3):
+        verifier.forward(cache, tree, logits_out=p, graph=True)
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        verifier.forward(cache, tree, logits_out=p, graph=True)
+    sync()
+    t_verify = (time.perf_counter() - t0) / reps
+    q = p + 0.3 * torch.randn_like(p)
+    u = uniforms(3, 0, 64)
+    verifier.accept(p, q, tree, u, 0.8)
+    sync()
+    t0 = time.perf_counter()
+    for i in range(reps):
+        verifier.accept(p, q, tree, uniforms(3, i, 64), 0.8)
+    sync()
+    t_accept = (time.perf_counter() - t0) / reps
+    tok = int(rng.integers(0, V))
+    for _ in range(3):
+        eng.decode([tok], [cache], graph=True)
+        cache.length = prefix
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        eng.decode([tok], [cache], graph=True)
+        cache.length = prefix                    # roll back: every step at the same prefix
+    sync()
+    t_decode = (time.perf_counter() - t0) / reps
+    wbytes, _ = eng.weight_bytes()
+    flops = 2.0 * (wbytes / 1.0625) * tree.size      # ~params x columns (int8 + fp16 scale per 32 = 1.0625 B/param)
+    return {'nodes': tree.size, 'prefix': prefix, 'verify_ms': round(t_verify * 1e3, 4),
+            'accept_ms': round(t_accept * 1e3, 4), 'decode_ms': round(t_decode * 1e3, 4),
+            'verify_over_decode': round((t_verify + t_accept) / t_decode, 3),
+            'verify_pass_over_decode': round(t_verify / t_decode, 3),
+            'verify_tflops': round(flops / t_verify / 1e12, 2),
+            'mfma_frac_f16': round(flops / t_verify / PEAK_F16, 4)}
 
+
+def workload_c3(args, out):
     import torch
     from seedplane_amd import _lib
     from seedplane_amd.presets import preset
     from seedplane_amd.qwen_engine import Qwen2Engine
     from seedplane_amd.synth import make_weights, random_prompt
-
-    torch.cuda.set_device(0)
     over = {} if args.layers is None else {'num_hidden_layers': args.layers}
     cfg = preset('qwen2-1.5b', **over)
     t0 = time.perf_counter()
@@ -109,23 +152,20 @@ def main():
     log(f'engine loaded in {time.perf_counter() - t0:.1f}s')
     wbytes, _ = eng.weight_bytes()
     W = args.window
-
-    # ---------------------------------------------------------------- batch 1
-    eng.reserve(17, eng.slots_for(args.prompt + args.steps + args.warmup + 8, W))
+    cap = args.prompt + args.steps + args.warmup + 8
+    eng.reserve(17, eng.slots_for(cap, W))
     prompt = random_prompt(args.prompt, cfg['vocab_size'], seed=0)
-    cache = eng.new_cache(args.prompt + args.steps + args.warmup + 8, window=W)
+    cache = eng.new_cache(cap, window=W)
     t0 = time.perf_counter()
-    first = prefill_all(eng, [cache], [prompt])
-    torch.cuda.synchronize()
+    first = eng.prefill([prompt], [cache])
+    sync()
     log(f'prefill {args.prompt} tokens in {time.perf_counter() - t0:.2f}s')
     _, toks = decode_run(eng, [cache], first, args.warmup)
     dt, toks = decode_run(eng, [cache], toks, args.steps)
     tok_s = args.steps / dt
-    visible = min(W, cache.length)
-    step_bytes = wbytes + kv_bytes_per_token(cfg, visible)
+    step_bytes = wbytes + kv_bytes(cfg, min(W, cache.length))
     log(f'bs1: {tok_s:.1f} tok/s, {dt / args.steps * 1e3:.3f} ms/token, {step_bytes / 1e9:.3f} GB/token')
 
-    # ---------------------------------------------------------------- dominant kernel roofline
     us, gbytes = eng.time_gemv(_lib.SP_T_GATE_UP, layer=0, n_cols=1, iters=200)
     achieved = gbytes / (us * 1e-6) / 1e9
     roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM / 1e9, 'unit': 'GB/s',
@@ -134,22 +174,26 @@ def main():
                 'bytes_per_launch': gbytes, 'avg_launch_us': round(us, 3)}
     log(f'gate_up GEMV: {us:.2f} us/launch, {achieved:.0f} GB/s')
 
-    # ---------------------------------------------------------------- batch 16
     bs16 = None
     if not args.no_bs16:
-        caches = [eng.new_cache(args.prompt + args.steps + args.warmup + 8, window=W) for _ in range(16)]
+        caches = [eng.new_cache(cap, window=W) for _ in range(16)]
         prompts = [random_prompt(args.prompt, cfg['vocab_size'], seed=100 + i) for i in range(16)]
         t0 = time.perf_counter()
-        first16 = prefill_all(eng, caches, prompts)
-        torch.cuda.synchronize()
+        first16 = eng.prefill(prompts, caches)
+        sync()
         log(f'prefill 16 x {args.prompt} tokens in {time.perf_counter() - t0:.2f}s')
         _, t16 = decode_run(eng, caches, first16, args.warmup)
         steps16 = max(16, args.steps // 2)
         dt16, t16 = decode_run(eng, caches, t16, steps16)
-        step16_bytes = wbytes + 16 * kv_bytes_per_token(cfg, min(W, caches[0].length))
+        b16 = wbytes + 16 * kv_bytes(cfg, min(W, caches[0].length))
         bs16 = {'tok_s': round(16 * steps16 / dt16, 1), 'ms_per_step': round(dt16 / steps16 * 1e3, 4),
-                'hbm_frac_step': round(step16_bytes * steps16 / dt16 / PEAK_HBM, 4), 'steps': steps16}
+                'hbm_frac_step': round(b16 * steps16 / dt16 / PEAK_HBM, 4), 'steps': steps16}
         log(f'bs16: {bs16}')
+
+    verify = None
+    if not args.no_verify:
+        verify = verify_cost(eng, cfg)
+        log(f'verify: {verify}')
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -157,16 +201,128 @@ def main():
         cpu = cpu_baseline(cfg, w, W, args.cpu_sample_tokens)
         log(f'cpu baseline {cpu} in {time.perf_counter() - t0:.1f}s')
 
-    out = {'metric': METRIC, 'value': round(tok_s, 2), 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps,
-           'warmup': args.warmup, 'ms_per_step': round(dt / args.steps * 1e3, 4), 'higher_is_better': True,
-           'scaling': 'weak', 'vs_baseline': None, 'dtype': 'int8 weights, fp16 activations/KV, fp32 accumulate',
-           'data': 'synthetic (random-init int8 weights, uniform random prompt ids)',
-           'config': {'workload': f'Qwen2-1.5B int8 (block 32, fp16 scale) greedy decode, batch 1, window {W}, '
-                                  f'prompt {args.prompt}, {args.steps} timed steps',
-                      'layers': cfg['num_hidden_layers'], 'hidden': cfg['hidden_size'], 'vocab': cfg['vocab_size'],
-                      'window': W, 'prompt': args.prompt},
-           'hbm_frac_step': round(step_bytes * tok_s / PEAK_HBM, 4), 'bytes_per_token': step_bytes,
-           'bs16': bs16, 'roofline': roofline, 'cpu_baseline': cpu}
+    out.update({'metric': METRIC, 'value': round(tok_s, 2), 'unit': 'tok/s', 'steps': args.steps,
+                'warmup': args.warmup, 'ms_per_step': round(dt / args.steps * 1e3, 4), 'higher_is_better': True,
+                'dtype': 'int8 weights, fp16 activations/KV, fp32 accumulate',
+                'data': 'synthetic (random-init int8 weights, uniform random prompt ids)',
+                'config': {'workload': f'Qwen2-1.5B int8 (block 32, fp16 scale) greedy decode, batch 1, window {W}, '
+                                       f'prompt {args.prompt}, {args.steps} timed steps',
+                           'layers': cfg['num_hidden_layers'], 'hidden': cfg['hidden_size'],
+                           'vocab': cfg['vocab_size'], 'window': W, 'prompt': args.prompt},
+                'hbm_frac_step': round(step_bytes * tok_s / PEAK_HBM, 4), 'bytes_per_token': step_bytes,
+                'bs16': bs16, 'verify': verify, 'roofline': roofline, 'cpu_baseline': cpu})
+
+
+def workload_c2(args, out):
+    """0.5B fp16, 16 requests x 32 greedy tokens, prompts 16-128 ids, decoded as one batch (decode-only timing)."""
+    import torch
+    from seedplane_amd.presets import preset
+    from seedplane_amd.qwen_engine import Qwen2Engine
+    from seedplane_amd.synth import make_weights, random_prompt
+    cfg, w = make_weights(preset('qwen2-0.5b'), 'f16', seed=0)
+    eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(16, 129, (16,), generator=g).tolist()
+    prompts = [random_prompt(n, cfg['vocab_size'], seed=200 + i) for i, n in enumerate(lens)]
+    new = 32
+    eng.reserve(16, 512)
+    caches = [eng.new_cache(512) for _ in range(16)]
+    first = eng.prefill(prompts, caches)
+    _, _ = decode_run(eng, caches, first, 0)
+    dt, _ = decode_run(eng, caches, first, new - 1)
+    tok_s = 16 * (new - 1) / dt
+    wbytes, _ = eng.weight_bytes()
+    mean_ctx = sum(c.length for c in caches) / 16
+    step_bytes = wbytes + 16 * kv_bytes(cfg, mean_ctx)
+    out.update({'metric': 'decode tok/s, 16-request burst, Qwen2-0.5B fp16', 'value': round(tok_s, 1),
+                'unit': 'tok/s', 'steps': new - 1, 'warmup': 0, 'ms_per_step': round(dt / (new - 1) * 1e3, 4),
+                'higher_is_better': True, 'dtype': 'fp16 weights/activations/KV, fp32 accumulate',
+                'data': 'synthetic (random-init fp16 weights ~N(0,0.02), uniform random prompts of 16-128 ids)',
+                'config': {'workload': 'Qwen2-0.5B fp16, 16 requests x 32 greedy tokens, ragged prompts, batch 16',
+                           'prompt_lens': lens},
+                'hbm_frac_step': round(step_bytes * (new - 1) / dt / PEAK_HBM, 4)})
+
+
+def workload_c5(args, out):
+    """7B int4 (g32 scale + zero), batch 32 at 8192 positions of full fp16 KV each, 128 decode steps.  The 8192-token
+    contexts are filled with seeded synthetic K/V (the decode step reads the same bytes)."""
+    from seedplane_amd.presets import preset
+    from seedplane_amd.qwen_engine import Qwen2Engine
+    from seedplane_amd.synth import make_weights, random_prompt
+    t0 = time.perf_counter()
+    cfg, w = make_weights(preset('qwen2-7b'), 'q4', seed=0)
+    log(f'7B int4 weights generated in {time.perf_counter() - t0:.1f}s')
+    eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    del w
+    ctx, B, steps = 8192, 32, args.steps if args.steps != 256 else 128
+    eng.reserve(B, ctx + steps + 8)
+    caches = [eng.new_cache(ctx + steps + 8) for _ in range(B)]
+    for i, c in enumerate(caches):
+        eng.fill_cache(c, ctx, seed=i)
+    toks = random_prompt(B, cfg['vocab_size'], seed=5)
+    _, toks = decode_run(eng, caches, toks, 4)
+    dt, _ = decode_run(eng, caches, toks, steps)
+    tok_s = B * steps / dt
+    wbytes, _ = eng.weight_bytes()
+    step_bytes = wbytes + B * kv_bytes(cfg, ctx + steps // 2)
+    out.update({'metric': 'decode tok/s, Qwen2-7B int4 batch 32 at 8k context', 'value': round(tok_s, 1),
+                'unit': 'tok/s', 'steps': steps, 'warmup': 4, 'ms_per_step': round(dt / steps * 1e3, 4),
+                'higher_is_better': True, 'dtype': 'int4 weights (g32 fp16 scale+zero), fp16 activations/KV',
+                'data': 'synthetic (random-init int4 weights; 8192-position contexts filled with seeded K/V)',
+                'config': {'workload': 'Qwen2-7B int4, batch 32, 8192-token full fp16 KV per request, 128 steps'},
+                'hbm_frac_step': round(step_bytes * steps / dt / PEAK_HBM, 4), 'bytes_per_step': step_bytes})
+
+
+def workload_spec(args, out):
+    """Full speculative loop: target 1.5B int8, drafter 0.5B fp16, 8 branches x 4 tokens, T = 0.8, 64 steps."""
+    from seedplane_amd.presets import preset
+    from seedplane_amd.qwen_engine import Qwen2Engine
+    from seedplane_amd.speculative import SpecStats, TreeDrafter, speculative_generate
+    from seedplane_amd.synth import make_weights, random_prompt
+    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
+    target = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    dcfg, dw = make_weights(preset('qwen2-0.5b'), 'f16', seed=1)
+    drafter = TreeDrafter(Qwen2Engine(config=dcfg, tensors=dw, max_tokens=64))
+    prompt = random_prompt(2048, cfg['vocab_size'], seed=9)
+    stats = SpecStats()
+    speculative_generate(target, drafter, prompt, steps=2, seed=0)
+    sync()
+    t0 = time.perf_counter()
+    toks = speculative_generate(target, drafter, prompt, steps=64, seed=1, stats=stats)
+    sync()
+    dt = time.perf_counter() - t0
+    out.update({'metric': 'speculative tree decode tok/s (8x4 drafts, T=0.8)', 'value': round(len(toks) / dt, 2),
+                'unit': 'tok/s', 'steps': 64, 'warmup': 2, 'ms_per_step': round(dt / 64 * 1e3, 3),
+                'higher_is_better': True, 'dtype': 'target int8 / drafter fp16, fp32 logits, fp64 acceptance',
+                'data': 'synthetic random-init target and drafter (acceptance is near zero for unrelated models)',
+                'config': {'workload': 'target Qwen2-1.5B int8, drafter Qwen2-0.5B fp16, 8 branches x 4, '
+                                       '2048-token prompt, 64 steps (prefill included in neither timing)'},
+                'accepted_per_step': round(stats.accepted / stats.steps, 3),
+                'emitted_per_step': round(stats.emitted / stats.steps, 3)})
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=256)
+    ap.add_argument('--warmup', type=int, default=16)
+    ap.add_argument('--workload', default='c3', choices=['c3', 'c2', 'c5', 'spec'])
+    ap.add_argument('--no-bs16', action='store_true')
+    ap.add_argument('--no-verify', action='store_true')
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--cpu-sample-tokens', type=int, default=6)
+    ap.add_argument('--prompt', type=int, default=3840)
+    ap.add_argument('--window', type=int, default=1024)
+    ap.add_argument('--layers', type=int, default=None, help='(debug) fewer layers; the result is then not the metric')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({'error': 'this build measures one GPU only: run with --gpus 1 (no multi-GPU path exists)'}))
+        sys.exit(2)
+    import torch
+    torch.cuda.set_device(0)
+    out = {'metric': METRIC, 'value': None, 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
+           'ms_per_step': None, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None}
+    {'c3': workload_c3, 'c2': workload_c2, 'c5': workload_c5, 'spec': workload_spec}[args.workload](args, out)
     print(json.dumps(out), flush=True)
 
 

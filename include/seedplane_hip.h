@@ -141,6 +141,11 @@ int sp_engine_sync(sp_engine *e);
 int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_cols, int32_t iters, float *avg_us,
                         uint64_t *bytes);
 
+/* Benchmark utility (no counterpart in the reference): fill slots [first_slot, first_slot + n) of sequence `seq`
+ * in every layer's K and V with seeded pseudo-random fp16 values in [-scale, scale], standing in for a long prefill
+ * when only the decode step is measured (the step reads the same bytes whatever the values). */
+int sp_engine_kv_fill(sp_engine *e, int32_t seq, int32_t first_slot, int32_t n, uint64_t seed, float scale);
+
 /* Bytes of HBM the engine holds for weights / KV (for roofline accounting). */
 int sp_engine_bytes(const sp_engine *e, uint64_t *weight_bytes, uint64_t *kv_bytes);
 

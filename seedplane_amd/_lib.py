@@ -48,6 +48,7 @@ SIGNATURES = {
     'sp_engine_kv_move': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     'sp_engine_sync': (c_int, [c_void_p]),
     'sp_engine_bytes': (c_int, [c_void_p, ctypes.POINTER(c_uint64), ctypes.POINTER(c_uint64)]),
+    'sp_engine_kv_fill': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_uint64, c_float]),
     'sp_engine_time_gemv': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(c_float),
                                     ctypes.POINTER(c_uint64)]),
     'sp_op_argmax_workspace': (c_size_t, [c_int32, c_int32]),

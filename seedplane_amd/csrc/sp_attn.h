@@ -205,14 +205,12 @@ __global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
 
 // out[b][h*HD + d] (fp16) = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}; one block (HD threads) per
 // (head, column), chunk statistics loaded in parallel.
-__global__ void __launch_bounds__(128) k_attn_combine(const float *part, const sp_token *toks, int NH, int HD,
+__global__ void __launch_bounds__(128) k_attn_combine(const float *part, const int *col_nchunk, int NH, int HD,
                                                       int nchunk, f16 *out, int ldo) {
     __shared__ float w_s[ATT_MAX_CHUNKS];
     __shared__ float red[16];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
-    int nlin;
-    const int nvis = att_visible(toks[b], nlin);
-    const int nc = (nvis + ATT_CH - 1) / ATT_CH;
+    const int nc = col_nchunk[b];
     const float *p = part + ((size_t)b * NH + h) * nchunk * (HD + 2);
     float mloc = -INFINITY;
     for (int c = tid; c < nc; c += nt) {
@@ -283,6 +281,201 @@ __global__ void __launch_bounds__(128) k_kv_move(f16 *const *kl, f16 *const *vl,
         if (threadIdx.x < HD) { tk = k[so + threadIdx.x]; tv = v[so + threadIdx.x]; }
         __syncthreads();
         if (threadIdx.x < HD) { k[dO + threadIdx.x] = tk; v[dO + threadIdx.x] = tv; }
+        __syncthreads();
+    }
+}
+
+// Seeded fill of K/V slots (benchmark stand-in for a long prefill): value = scale * (2 * hash01 - 1).
+__global__ void __launch_bounds__(256) k_kv_fill(f16 *const *kl, f16 *const *vl, int seq, int NKV, int n_slots, int HD,
+                                                 int first, int n, uint64_t seed, float scale) {
+    const int layer = blockIdx.y;
+    const size_t per_head = (size_t)n * HD;
+    const size_t total = per_head * NKV;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int kvh = (int)(i / per_head);
+        const size_t r = i - (size_t)kvh * per_head;
+        const int slot = first + (int)(r / HD), d = (int)(r % HD);
+        const size_t off = (((size_t)seq * NKV + kvh) * n_slots + slot) * HD + d;
+        uint64_t x = seed ^ (((uint64_t)layer << 40) + off);
+        x += 0x9E3779B97F4A7C15ull;
+        x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+        x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+        x ^= x >> 31;
+        const float u1 = (float)(x & 0xffffff) * (1.0f / 16777216.0f), u2 = (float)((x >> 24) & 0xffffff) * (1.0f / 16777216.0f);
+        kl[layer][off] = (f16)(scale * (2.f * u1 - 1.f));
+        vl[layer][off] = (f16)(scale * (2.f * u2 - 1.f));
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Multi-query attention for groups of columns of one sequence (tree verification, prefill chunks).  The group's
+// visible list is the union ring range [lo, lo + nlin) followed by the shared tree block; one block per (chunk of
+// ATT_CH keys, kv head, group) stages the chunk's K (row-major) and V (transposed) in LDS once, and every
+// (column, query head) row of the group is scored against it on MFMA: S = Q K^T, per-row mask (the column's own
+// ring range and tree-mask bits), chunk-local softmax statistics, O = P V.  Partials use the same layout as
+// k_attn_part, so k_attn_combine merges them (with the group's chunk count per column).
+struct AttnGroup {
+    int first_col, ncols, seq, lo, nlin, tree_base, tree_count, pad;
+};
+
+struct AttnMqArgs {
+    const float *q;        // [n][NH*HD]
+    const f16 *kc, *vc;
+    const sp_token *toks;
+    const AttnGroup *groups;
+    int NH, NKV, HD, n_slots, nchunk;
+    float scale;
+    float *part;
+};
+
+template <int HD, int G>
+__global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
+    constexpr int KP = HD + 8, VP = ATT_CH + 8;
+    constexpr int ST = HD / 32;                      // MFMA k-steps over head dim
+    __shared__ __align__(16) f16 k_s[ATT_CH][KP];
+    __shared__ __align__(16) f16 vt_s[HD][VP];
+    __shared__ __align__(16) f16 p_s[4][16][VP];
+    __shared__ int kpos_s[ATT_CH];                  // ring position of key j, or -(1 + tree index), or INT_MIN
+    __shared__ int clo_s[64], chi_s[64], ctc_s[64];
+    __shared__ unsigned long long cmask_s[64];
+
+    const int c = blockIdx.x, kvh = blockIdx.y;
+    const AttnGroup gr = a.groups[blockIdx.z];
+    const int nvis = gr.nlin + gr.tree_count;
+    const int v0 = c * ATT_CH;
+    if (v0 >= nvis) return;
+    const int cnt = min(ATT_CH, nvis - v0);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int R = gr.ncols * G;
+
+    for (int i = tid; i < gr.ncols; i += 256) {
+        const sp_token t = a.toks[gr.first_col + i];
+        clo_s[i] = t.ctx_lo; chi_s[i] = t.ctx_hi; ctc_s[i] = t.tree_count; cmask_s[i] = t.tree_mask;
+    }
+    const size_t head_base = ((size_t)gr.seq * a.NKV + kvh) * a.n_slots;
+    constexpr int CPR = HD / 8;
+    for (int i = tid; i < ATT_CH * CPR; i += 256) {
+        const int j = i / CPR, ch = i - j * CPR;
+        f16x8 kv = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, vv = kv;
+        if (j < cnt) {
+            const int vis = v0 + j;
+            int slot, kp;
+            if (vis < gr.nlin) { kp = gr.lo + vis; slot = kp % a.n_slots; }
+            else { const int tj = vis - gr.nlin; kp = -(1 + tj); slot = (gr.tree_base + tj) % a.n_slots; }
+            if (ch == 0) kpos_s[j] = kp;
+            const size_t off = (head_base + slot) * HD + ch * 8;
+            kv = *(const f16x8 *)(a.kc + off);
+            vv = *(const f16x8 *)(a.vc + off);
+        } else if (ch == 0) {
+            kpos_s[j] = INT_MIN;
+        }
+        *(f16x8 *)&k_s[j][ch * 8] = kv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt_s[ch * 8 + e][j] = vv[e];
+    }
+    __syncthreads();
+
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int n_tiles = (R + 15) / 16, n_iter = (n_tiles + 3) / 4;
+    for (int it = 0; it < n_iter; ++it) {          // same trip count in every wave: the barriers below are uniform
+        const int rt = it * 4 + wv;
+        const bool active = rt < n_tiles;
+        // ---- Q fragments (A operand): row rt*16 + r16, dims 32s + 8*g4 .. +8
+        f16x8 qa[ST];
+        {
+            const int row = rt * 16 + r16;
+            if (row < R) {
+                const int col = row / G, h = row - col * G;
+                const float *qp = a.q + (size_t)(gr.first_col + col) * a.NH * HD + (kvh * G + h) * HD;
+#pragma unroll
+                for (int s = 0; s < ST; ++s) {
+                    const f32x4 x0 = *(const f32x4 *)(qp + 32 * s + 8 * g4);
+                    const f32x4 x1 = *(const f32x4 *)(qp + 32 * s + 8 * g4 + 4);
+                    qa[s] = (f16x8){(f16)(x0[0] * a.scale), (f16)(x0[1] * a.scale), (f16)(x0[2] * a.scale),
+                                    (f16)(x0[3] * a.scale), (f16)(x1[0] * a.scale), (f16)(x1[1] * a.scale),
+                                    (f16)(x1[2] * a.scale), (f16)(x1[3] * a.scale)};
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < ST; ++s) qa[s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+            }
+        }
+        // ---- S = Q K^T: 4 slot tiles of 16; lane holds S[row 4*g4 + j][slot 16*st + r16]
+        f32x4 sc[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < ST; ++s) {
+                const f16x8 kb = *(const f16x8 *)&k_s[16 * st + r16][32 * s + 8 * g4];
+                acc = mfma16(qa[s], kb, acc);
+            }
+            sc[st] = acc;
+        }
+        // ---- mask, chunk-local max / exp / sum per row
+        float mrow[4], lrow[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = rt * 16 + 4 * g4 + j;
+            const int col = row < R ? row / G : 0;
+            const int lo = clo_s[col], hi = chi_s[col], tc = ctc_s[col];
+            const unsigned long long mk = cmask_s[col];
+            float m = -INFINITY;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int kp = kpos_s[16 * st + r16];
+                bool ok = row < R && kp != INT_MIN;
+                if (ok) ok = kp >= 0 ? (kp >= lo && kp <= hi) : ((-kp - 1) < tc && ((mk >> (-kp - 1)) & 1ull));
+                const float v = ok ? sc[st][j] : -INFINITY;
+                sc[st][j] = v;
+                m = fmaxf(m, v);
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, SP_WAVE));
+            float l = 0.f;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const float e = (m == -INFINITY || sc[st][j] == -INFINITY) ? 0.f : expf(sc[st][j] - m);
+                sc[st][j] = e;
+                l += e;
+            }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, SP_WAVE);
+            mrow[j] = m; lrow[j] = l;
+        }
+        // ---- P (fp16) to LDS in row-major, read back as the A operand
+        if (active) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) p_s[wv][4 * g4 + j][16 * st + r16] = (f16)sc[st][j];
+        }
+        __syncthreads();
+        if (active) {
+        f16x8 pa[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) pa[s2] = *(const f16x8 *)&p_s[wv][r16][32 * s2 + 8 * g4];
+        // ---- O = P V over HD/16 dim tiles; lane holds O[row 4*g4 + j][dim 16*dt + r16]
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) {
+            f32x4 o = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const f16x8 vb = *(const f16x8 *)&vt_s[16 * dt + r16][32 * s2 + 8 * g4];
+                o = mfma16(pa[s2], vb, o);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = rt * 16 + 4 * g4 + j;
+                if (row < R) {
+                    const int col = row / G, h = row - col * G;
+                    float *out = a.part + (((size_t)(gr.first_col + col) * a.NH + kvh * G + h) * a.nchunk + c) * (HD + 2);
+                    out[2 + 16 * dt + r16] = o[j];
+                    if (dt == 0 && r16 == 0) { out[0] = mrow[j]; out[1] = lrow[j]; }
+                }
+            }
+        }
+        }
         __syncthreads();
     }
 }

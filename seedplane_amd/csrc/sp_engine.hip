@@ -10,6 +10,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <tuple>
 #include <string>
 #include <utility>
 #include <vector>
@@ -153,6 +154,20 @@ void launch_attn_hd(int G, dim3 grid, hipStream_t st, const AttnArgs &a) {
     }
 }
 
+template <int HD>
+void launch_attn_mq_hd(int G, dim3 grid, hipStream_t st, const AttnMqArgs &a) {
+    switch (G) {
+        case 1: hipLaunchKernelGGL((k_attn_mq<HD, 1>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((k_attn_mq<HD, 2>), grid, dim3(256), 0, st, a); break;
+        case 3: hipLaunchKernelGGL((k_attn_mq<HD, 3>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((k_attn_mq<HD, 4>), grid, dim3(256), 0, st, a); break;
+        case 5: hipLaunchKernelGGL((k_attn_mq<HD, 5>), grid, dim3(256), 0, st, a); break;
+        case 6: hipLaunchKernelGGL((k_attn_mq<HD, 6>), grid, dim3(256), 0, st, a); break;
+        case 7: hipLaunchKernelGGL((k_attn_mq<HD, 7>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_attn_mq<HD, 8>), grid, dim3(256), 0, st, a); break;
+    }
+}
+
 template <int FMT>
 void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x, hipStream_t st) {
     hipLaunchKernelGGL((k_embed<FMT>), dim3(n), dim3(256), 0, st, m.w, m.sz, m.nkt, toks, H, x, H);
@@ -185,6 +200,8 @@ struct sp_engine {
     float *am_v = nullptr;
     int *am_i = nullptr, *am_out = nullptr;
     sp_token *dtoks = nullptr;
+    AttnGroup *dgroups = nullptr;
+    int *dcolnc = nullptr;
 
     // KV ring
     int n_seq = 0, n_slots = 0;
@@ -192,12 +209,20 @@ struct sp_engine {
     f16 **d_kl = nullptr, **d_vl = nullptr;
     int *d_move = nullptr;
 
-    std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+    std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;
+
+    // attention plan of one forward call: same-sequence column groups (multi-query kernel) or one block row per column
+    struct AttnPlan {
+        bool mq = false;
+        int ngroups = 0, nchunk = 1;
+        std::vector<AttnGroup> groups;
+        std::vector<int> colnc;
+    };
+    AttnPlan plan_attention(int n, const sp_token *t, bool graph) const;
 
     void free_all();
     void alloc_activations();
-    void step(int n, int flags, int nchunk);
-    int nchunk_for(int n, const sp_token *t, bool graph) const;
+    void step(int n, int flags, const AttnPlan &ap);
 };
 
 void sp_engine::free_all() {
@@ -212,7 +237,7 @@ void sp_engine::free_all() {
     dev_free(final_norm); dev_free(inv_freq);
     for (void *p : {(void *)x, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)xn, (void *)attn,
                     (void *)act, (void *)am_v, (void *)am_i, (void *)am_out,
-                    (void *)dtoks, (void *)d_kl, (void *)d_vl, (void *)d_move})
+                    (void *)dtoks, (void *)dgroups, (void *)dcolnc, (void *)d_kl, (void *)d_vl, (void *)d_move})
         dev_free(p);
     for (auto p : kc) dev_free(p);
     for (auto p : vc) dev_free(p);
@@ -239,23 +264,59 @@ void sp_engine::alloc_activations() {
     am_i = dev_alloc<int>((size_t)maxT * ARGMAX_BLOCKS);
     am_out = dev_alloc<int>(maxT);
     dtoks = dev_alloc<sp_token>(maxT);
+    dgroups = dev_alloc<AttnGroup>(maxT);
+    dcolnc = dev_alloc<int>(maxT);
     d_move = dev_alloc<int>(2 * 64);
     HIPCHK(hipMemset(xn, 0, (size_t)maxT * kmax * sizeof(f16)));
     HIPCHK(hipMemset(attn, 0, (size_t)maxT * d.n_heads * d.head_dim * sizeof(f16)));
     HIPCHK(hipMemset(act, 0, (size_t)maxT * I * sizeof(f16)));
 }
 
-int sp_engine::nchunk_for(int n, const sp_token *t, bool graph) const {
-    if (graph) return (n_slots + 64 + ATT_CH - 1) / ATT_CH;
-    int mx = 1;
-    for (int i = 0; i < n; ++i) {
-        const int nlin = t[i].ctx_hi >= t[i].ctx_lo ? t[i].ctx_hi - t[i].ctx_lo + 1 : 0;
-        mx = std::max(mx, nlin + t[i].tree_count);
+sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool graph) const {
+    AttnPlan p;
+    auto nlin_of = [](const sp_token &x) { return x.ctx_hi >= x.ctx_lo ? x.ctx_hi - x.ctx_lo + 1 : 0; };
+    // maximal runs of columns with the same sequence and tree block whose union ring range fits the slots
+    int i = 0;
+    while (i < n) {
+        AttnGroup g{};
+        g.first_col = i; g.seq = t[i].seq; g.tree_base = t[i].tree_base; g.tree_count = t[i].tree_count;
+        int lo = INT32_MAX, hi = -1;
+        int j = i;
+        for (; j < n; ++j) {
+            if (t[j].seq != g.seq || t[j].tree_count != g.tree_count || (g.tree_count && t[j].tree_base != g.tree_base)) break;
+            int l2 = lo, h2 = hi;
+            if (nlin_of(t[j]) > 0) { l2 = std::min(lo, t[j].ctx_lo); h2 = std::max(hi, t[j].ctx_hi); }
+            if (h2 >= l2 && h2 - l2 + 1 > n_slots) break;
+            lo = l2; hi = h2;
+        }
+        g.ncols = j - i;
+        g.lo = hi >= lo ? lo : 0;
+        g.nlin = hi >= lo ? hi - lo + 1 : 0;
+        p.groups.push_back(g);
+        i = j;
     }
-    return (mx + ATT_CH - 1) / ATT_CH;
+    p.ngroups = (int)p.groups.size();
+    for (auto &g : p.groups) p.mq = p.mq || g.ncols > 1;
+    p.colnc.assign(n, 0);
+    int mx = 1;
+    if (p.mq) {
+        for (auto &g : p.groups) {
+            const int nc = (g.nlin + g.tree_count + ATT_CH - 1) / ATT_CH;
+            for (int c = 0; c < g.ncols; ++c) p.colnc[g.first_col + c] = nc;
+            mx = std::max(mx, nc);
+        }
+    } else {
+        for (int c = 0; c < n; ++c) {
+            p.colnc[c] = (nlin_of(t[c]) + t[c].tree_count + ATT_CH - 1) / ATT_CH;
+            mx = std::max(mx, p.colnc[c]);
+        }
+    }
+    p.nchunk = graph ? max_nchunk : mx;
+    return p;
 }
 
-void sp_engine::step(int n, int flags, int nchunk) {
+void sp_engine::step(int n, int flags, const AttnPlan &ap) {
+    const int nchunk = ap.nchunk;
     const int H = d.hidden, I = d.intermediate, NH = d.n_heads, NKV = d.n_kv_heads, HD = d.head_dim;
     hipStream_t st = stream;
     switch (embed.fmt) {
@@ -271,12 +332,19 @@ void sp_engine::step(int n, int flags, int nchunk) {
         RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots};
         hipLaunchKernelGGL(k_rope_kv, dim3(n), dim3(256), 0, st, ra);
         if (l + 1 == d.n_layers && !logits_on) break;   // K/V-only: the last layer only needs its K/V
-        AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
         const int G = NH / NKV;
-        dim3 agrid(nchunk, NKV, n);
-        if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
-        else launch_attn_hd<128>(G, agrid, st, aa);
-        hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dtoks, NH, HD, nchunk, attn, NH * HD);
+        if (ap.mq) {
+            AttnMqArgs am{q, kc[l], vc[l], dtoks, dgroups, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
+            dim3 agrid(nchunk, NKV, ap.ngroups);
+            if (HD == 64) launch_attn_mq_hd<64>(G, agrid, st, am);
+            else launch_attn_mq_hd<128>(G, agrid, st, am);
+        } else {
+            AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
+            dim3 agrid(nchunk, NKV, n);
+            if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
+            else launch_attn_hd<128>(G, agrid, st, aa);
+        }
+        hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn, NH * HD);
         launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, st);
         hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, ly.post_norm, H, d.rms_eps, xn, H);
         launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, st);
@@ -472,11 +540,14 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             require(t.tree_count == 0 || (t.tree_base >= 0 && t.tree_base < e->n_slots), SP_EINVAL, "tree_base out of range");
             require(nlin + t.tree_count >= 1, SP_EINVAL, "a column must see at least one key");
         }
-        HIPCHK(hipMemcpyAsync(e->dtoks, toks, n * sizeof(sp_token), hipMemcpyHostToDevice, e->stream));
         const bool use_graph = flags & SP_F_GRAPH;
         const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX);
+        const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
+        HIPCHK(hipMemcpyAsync(e->dtoks, toks, n * sizeof(sp_token), hipMemcpyHostToDevice, e->stream));
+        HIPCHK(hipMemcpyAsync(e->dgroups, ap.groups.data(), ap.ngroups * sizeof(AttnGroup), hipMemcpyHostToDevice, e->stream));
+        HIPCHK(hipMemcpyAsync(e->dcolnc, ap.colnc.data(), n * sizeof(int), hipMemcpyHostToDevice, e->stream));
         if (use_graph) {
-            auto key = std::make_pair(n, sflags);
+            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups : -1);
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 // record on the private stream (the caller's may be the null stream, which cannot capture)
@@ -485,7 +556,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
                 e->stream = e->capture_stream;
                 HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
                 try {
-                    e->step(n, sflags, e->nchunk_for(n, toks, true));
+                    e->step(n, sflags, ap);
                 } catch (...) {
                     hipGraph_t dummy;
                     (void)hipStreamEndCapture(e->stream, &dummy);
@@ -502,7 +573,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             }
             HIPCHK(hipGraphLaunch(it->second, e->stream));
         } else {
-            e->step(n, sflags, e->nchunk_for(n, toks, false));
+            e->step(n, sflags, ap);
         }
         if (logits_dev && (flags & SP_F_LOGITS))
             HIPCHK(hipMemcpyAsync(logits_dev, e->logits, (size_t)n * d.vocab * sizeof(float), hipMemcpyDeviceToDevice, e->stream));
@@ -592,6 +663,20 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
         HIPCHK(hipGetLastError());
         *avg_us = ms * 1000.f / iters;
         *bytes = m->bytes;
+    });
+}
+
+int sp_engine_kv_fill(sp_engine *e, int32_t seq, int32_t first_slot, int32_t n, uint64_t seed, float scale) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        require(e->n_seq > 0, SP_ESTATE, "KV cache not reserved");
+        require(seq >= 0 && seq < e->n_seq, SP_EINVAL, "sequence index out of range");
+        require(first_slot >= 0 && n >= 0 && first_slot + n <= e->n_slots, SP_EINVAL, "slot range out of bounds");
+        if (n == 0) return;
+        hipLaunchKernelGGL(k_kv_fill, dim3(1024, e->d.n_layers), dim3(256), 0, e->stream, e->d_kl, e->d_vl, seq,
+                           e->d.n_kv_heads, e->n_slots, e->d.head_dim, first_slot, n, (uint64_t)seed, scale);
+        HIPCHK(hipGetLastError());
+        HIPCHK(hipStreamSynchronize(e->stream));
     });
 }
 

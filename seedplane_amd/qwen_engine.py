@@ -195,6 +195,22 @@ class Qwen2Engine:
                    self.h)
         return us.value, nb.value
 
+    def fill_cache(self, cache, n_positions, seed=0, scale=1.0):
+        """Benchmark stand-in for a long prefill: positions [0, n_positions) of `cache` get seeded pseudo-random K/V
+        (the decode step reads the same bytes whatever the values); cache.length = n_positions."""
+        self._check_cache(cache)
+        S = self._pool_slots
+        if cache.window is None and n_positions > cache.capacity:
+            raise ValueError(f'KV cache capacity {cache.capacity} exceeded')
+        n = min(n_positions, S)
+        first = (n_positions - n) % S
+        if first + n <= S:
+            _lib.check(self.lib.sp_engine_kv_fill(self.h, cache.seq, first, n, seed, scale), self.h)
+        else:
+            _lib.check(self.lib.sp_engine_kv_fill(self.h, cache.seq, first, S - first, seed, scale), self.h)
+            _lib.check(self.lib.sp_engine_kv_fill(self.h, cache.seq, 0, n - (S - first), seed + 1, scale), self.h)
+        cache.length = n_positions
+
     # ------------------------------------------------------------------------------------------ KV pool
     def reserve(self, n_seq, n_slots):
         """(Re)allocate the HBM KV pool for n_seq sequences x n_slots ring slots; invalidates existing caches."""
