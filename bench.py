@@ -213,6 +213,18 @@ def workload_c3(args, out):
                 'bs16': bs16, 'verify': verify, 'roofline': roofline, 'cpu_baseline': cpu})
 
 
+def workload_verify(args, out):
+    """Only the tree-verification cost on the 1.5B int8 model (for profiling)."""
+    from seedplane_amd.presets import preset
+    from seedplane_amd.qwen_engine import Qwen2Engine
+    from seedplane_amd.synth import make_weights
+    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
+    eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    v = verify_cost(eng, cfg)
+    out.update({'metric': 'tree verify cost / decode step (1 + 8x4 nodes, 2048 prefix)',
+                'value': v['verify_over_decode'], 'unit': 'ratio', 'higher_is_better': False, 'verify': v})
+
+
 def workload_c2(args, out):
     """0.5B fp16, 16 requests x 32 greedy tokens, prompts 16-128 ids, decoded as one batch (decode-only timing)."""
     import torch
@@ -228,7 +240,6 @@ def workload_c2(args, out):
     eng.reserve(16, 512)
     caches = [eng.new_cache(512) for _ in range(16)]
     first = eng.prefill(prompts, caches)
-    _, _ = decode_run(eng, caches, first, 0)
     dt, _ = decode_run(eng, caches, first, new - 1)
     tok_s = 16 * (new - 1) / dt
     wbytes, _ = eng.weight_bytes()
@@ -306,7 +317,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=256)
     ap.add_argument('--warmup', type=int, default=16)
-    ap.add_argument('--workload', default='c3', choices=['c3', 'c2', 'c5', 'spec'])
+    ap.add_argument('--workload', default='c3', choices=['c3', 'c2', 'c5', 'spec', 'verify'])
     ap.add_argument('--no-bs16', action='store_true')
     ap.add_argument('--no-verify', action='store_true')
     ap.add_argument('--no-cpu-baseline', action='store_true')
@@ -322,7 +333,7 @@ def main():
     torch.cuda.set_device(0)
     out = {'metric': METRIC, 'value': None, 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
            'ms_per_step': None, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None}
-    {'c3': workload_c3, 'c2': workload_c2, 'c5': workload_c5, 'spec': workload_spec}[args.workload](args, out)
+    {'c3': workload_c3, 'c2': workload_c2, 'c5': workload_c5, 'spec': workload_spec, 'verify': workload_verify}[args.workload](args, out)
     print(json.dumps(out), flush=True)
 
 

@@ -198,7 +198,11 @@ int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32
  * from that residual, after an accepted leaf (or max_depth levels) a bonus token is drawn from the target.
  * Uniforms u_dev[0..n_u) are consumed in that order.  out_dev (int32, max_depth + 4 entries): [0] accepted count k,
  * [1..k] accepted node ids, [max_depth+1] final token, [max_depth+2] uniforms used, [max_depth+3] 1 for a bonus
- * draw.  resid_dev: vocab doubles of scratch.  token/trial_start/n_trials are device int32 [n_nodes]. */
+ * draw.  resid_dev is unused (kept for callers of the first signature; may be NULL).  token/trial_start/n_trials
+ * are device int32 [n_nodes].  The residual after j rejections is evaluated as max(p - c_j q, 0) / S_j with c_1 = 1,
+ * c_{j+1} = c_j + S_j (the same distribution as renormalising max(p - q, 0) after each rejection).  Float64 sums
+ * use 64 x 256 contiguous chunks: sequential inside a chunk, over the 256 chunk sums of each group of 256, then
+ * over the 64 group sums.  Synchronous: returns after the walk, SP_EHIP if its cross-block exchange timed out. */
 int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld, int32_t n_nodes,
                       const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
                       const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,

@@ -3,9 +3,13 @@
   * Forest / verify_greedy / ledger: seedplane/speculative.py:12-111 (same decisions, same tie rules).
   * Linear batched verify with rollback: experiments/hive_scaling/benchmark_speculative.py:59-135.
   * Seeded uniforms: SplitMix64 (Steele, Lea, Flood 2014) over a counter, u = (x >> 11) * 2^-53.
-  * Float64 draws and tree acceptance with the product's fixed summation order (1024 contiguous chunks, each summed
-    in index order, chunk sums added in chunk order), so decisions can be compared bit for bit; each function also
-    returns the smallest decision margin so a test can show no comparison was within rounding of its threshold.
+  * Float64 draws (draw: 1024 contiguous chunks, each summed in index order, chunk sums added in chunk order) and
+    tree acceptance (accept_tree / draw3: 64 x 256 chunks, summed chunk, group, total) in the product's fixed
+    orders, so decisions can be compared bit for bit; each function also returns the smallest decision margin so a
+    test can show no comparison was within rounding of its threshold.
+  * Pins: draw / draw3 against brute-force inverse CDFs on exact rational weights and on permuted chunkings;
+    accept_tree through the speculative sampling theorem (Monte Carlo over the uniform-driven walk) and against
+    the analytic one-level law with the iterative residual.
   * exact_first_token_distribution: the acceptance rule's output law computed analytically over every draft outcome
     (speculative sampling theorem: it must equal the target distribution p).
 """
@@ -165,9 +169,72 @@ def draw(w, u):
     return int(pick), margin
 
 
+ACC_NB, ACC_T = 64, 256
+
+
+def chunk_sums3(w):
+    """Acceptance-walk summation order: ACC_NB * ACC_T contiguous chunks of C = ceil(V / (ACC_NB * ACC_T)) entries,
+    each summed in index order; each group of ACC_T chunk sums summed in order; the ACC_NB group sums summed in
+    order.  Returns (chunk sums, group sums, total, C)."""
+    V = len(w)
+    G = ACC_NB * ACC_T
+    C = -(-V // G)
+    padded = np.zeros(G * C)
+    padded[:V] = w
+    tsum = np.cumsum(padded.reshape(G, C), axis=1)[:, -1]
+    bsum = np.cumsum(tsum.reshape(ACC_NB, ACC_T), axis=1)[:, -1]
+    return tsum, bsum, np.cumsum(bsum)[-1], C
+
+
+def _first_exceeding(parts, target):
+    """Index of the first entry whose running sum exceeds target, else the last positive entry (0 if none), the
+    running sum before it, and the smallest |target - running sum| over the compared positive entries."""
+    run, last, run_last, gap = 0.0, 0, 0.0, np.inf
+    for i, v in enumerate(parts):
+        nxt = run + v
+        if v > 0:
+            last, run_last = i, run
+            gap = min(gap, abs(target - nxt))
+        if target < nxt:
+            return i, run, gap
+        run = nxt
+    return last, run_last, gap
+
+
+def draw3(w, u):
+    """Inverse CDF over the acceptance-walk chunk tree (group, chunk, element), with its fallbacks: a level whose
+    running sums never exceed the target (rounding) takes its last positive entry; with no positive weight at all
+    the token is 0.  Returns (token, margin) with margin the smallest relative gap at a compared boundary."""
+    tsum, bsum, total, C = chunk_sums3(w)
+    V = len(w)
+    target = u * total
+    scale = total if total > 0 else 1.0
+    b, Pb, g1 = _first_exceeding(bsum, target)
+    tb = target - Pb
+    t, Pt, g2 = _first_exceeding(tsum[b * ACC_T:(b + 1) * ACC_T], tb)
+    tl = tb - Pt
+    lo = (b * ACC_T + t) * C
+    n = max(0, min(C, V - lo))
+    acc, pick, lastpos, g3 = 0.0, -1, -1, np.inf
+    for i in range(lo, lo + n):
+        if w[i] > 0:
+            lastpos = i
+        acc += w[i]
+        g3 = min(g3, abs(acc - tl))
+        if acc > tl:
+            pick = i
+            break
+    if pick < 0:
+        pick = lastpos if lastpos >= 0 else lo
+    return int(pick), min(g1, g2, g3) / scale
+
+
 def accept_tree(p_logits, q_logits, tree, u, temperature, max_depth):
     """Mirror of the GPU acceptance walk.  tree: dict(token, trial_start, n_trials, trials) lists (the trials of a
-    node are its children in draft-branch order, repeats included).  Returns (accepted node ids, final token,
+    node are its children in draft-branch order, repeats included).  Each trial x is accepted when u < r(x) / q(x),
+    r the current residual: p before any rejection, then max(p - c_j q, 0) / S_j after j rejections, c_1 = 1,
+    c_{j+1} = c_j + S_j, S_j the sum of the numerator (equal to renormalising max(r - q, 0) after every rejection).
+    Float64 with the kernel's single roundings and chunk_sums3 order.  Returns (accepted node ids, final token,
     uniforms used, bonus flag, smallest decision margin)."""
     cur, ui, path = 0, 0, []
     margin = np.inf
@@ -176,36 +243,39 @@ def accept_tree(p_logits, q_logits, tree, u, temperature, max_depth):
         wp = softmax_weights(p_logits[cur], temperature)
         nt = tree['n_trials'][cur]
         if nt == 0 or len(path) >= max_depth:
-            tok, mg = draw(wp, take(ui))
+            tok, mg = draw3(wp, take(ui))
             return path, tok, ui + 1, True, min(margin, mg)
         wq = softmax_weights(q_logits[cur], temperature)
-        Zq = chunk_sums(wq)[1]
-        Zp = chunk_sums(wp)[1]
-        resid = None
-        accepted = -1
+        Zp = chunk_sums3(wp)[2]
+        Zq = chunk_sums3(wq)[2]
+        c, S, J, accepted, w = 0.0, 0.0, 0, -1, None
         t0 = tree['trial_start'][cur]
         for j in range(t0, t0 + nt):
-            c = tree['trials'][j]
-            x = tree['token'][c]
-            px = resid[x] if resid is not None else wp[x] / Zp
+            child = tree['trials'][j]
+            x = tree['token'][child]
+            px = wp[x] / Zp
             qx = wq[x] / Zq
+            if J > 0:
+                dx = px - c * qx
+                px = dx / S if dx > 0.0 else 0.0
             uu = take(ui)
             ui += 1
-            ratio = px / qx
+            with np.errstate(divide='ignore', invalid='ignore'):
+                ratio = np.float64(px) / np.float64(qx)
             margin = min(margin, abs(uu - ratio))
             if uu < ratio:
-                accepted = c
+                accepted = child
                 break
-            pi = resid if resid is not None else wp / Zp
-            d = pi - wq / Zq
-            r = np.where(d > 0.0, d, 0.0)
-            Zr = chunk_sums(r)[1]
-            resid = r / Zr
+            c = 1.0 if J == 0 else c + S
+            J += 1
+            d = wp / Zp - c * (wq / Zq)
+            w = np.where(d > 0.0, d, 0.0)
+            S = chunk_sums3(w)[2]
         if accepted >= 0:
             path.append(accepted)
             cur = accepted
             continue
-        tok, mg = draw(resid, take(ui))
+        tok, mg = draw3(w, take(ui))
         return path, tok, ui + 1, False, min(margin, mg)
 
 

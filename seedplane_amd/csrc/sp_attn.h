@@ -326,6 +326,7 @@ struct AttnMqArgs {
     int NH, NKV, HD, n_slots, nchunk;
     float scale;
     float *part;
+    int splits;            // blocks per (chunk, kv head, group); block s takes row tiles 4s .. 4s+3
 };
 
 template <int HD, int G>
@@ -340,13 +341,15 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     __shared__ unsigned long long cmask_s[64];
 
     const int c = blockIdx.x, kvh = blockIdx.y;
-    const AttnGroup gr = a.groups[blockIdx.z];
+    const int split = blockIdx.z % a.splits;
+    const AttnGroup gr = a.groups[blockIdx.z / a.splits];
     const int nvis = gr.nlin + gr.tree_count;
     const int v0 = c * ATT_CH;
     if (v0 >= nvis) return;
+    const int R = gr.ncols * G;
+    if (split * 64 >= R) return;                    // 4 row tiles of 16 rows per block
     const int cnt = min(ATT_CH, nvis - v0);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int R = gr.ncols * G;
 
     for (int i = tid; i < gr.ncols; i += 256) {
         const sp_token t = a.toks[gr.first_col + i];
@@ -376,9 +379,9 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     __syncthreads();
 
     const int r16 = lane & 15, g4 = lane >> 4;
-    const int n_tiles = (R + 15) / 16, n_iter = (n_tiles + 3) / 4;
-    for (int it = 0; it < n_iter; ++it) {          // same trip count in every wave: the barriers below are uniform
-        const int rt = it * 4 + wv;
+    const int n_tiles = (R + 15) / 16;
+    {                                                // one row tile per wave; the barriers below are uniform
+        const int rt = split * 4 + wv;
         const bool active = rt < n_tiles;
         // ---- Q fragments (A operand): row rt*16 + r16, dims 32s + 8*g4 .. +8
         f16x8 qa[ST];

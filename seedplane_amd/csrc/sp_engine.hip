@@ -93,11 +93,11 @@ struct GemvPlan {
 
 // One block per unit; waves per block chosen so that each wave owns at least ~2 k-tiles and small matrices still
 // spread over many waves (bs1 GEMVs are latency-bound).
-GemvPlan plan_gemv(const DevMat &m) {
+GemvPlan plan_gemv(const DevMat &m, int mt) {
     GemvPlan p;
     p.rg = m.paired ? 2 : 1;
     p.units = m.rows_pad / 16 / p.rg;
-    int nw = 16;
+    int nw = mt == 1 ? 16 : 8;
     while (nw > 4 && m.nkt < 2 * nw) nw >>= 1;
     if (p.units >= 4096 && nw > 8) nw = 8;
     p.nw = nw;
@@ -123,8 +123,8 @@ void launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, flo
                  const float *bias, hipStream_t st) {
     require(mcols >= 1 && mcols <= 16 * GEMV_MAX_MT, SP_EINVAL, "gemv columns out of range");
     require((epi == EPI_SILU) == m.paired, SP_EINVAL, "gemv epilogue does not match the matrix packing");
-    GemvPlan p = plan_gemv(m);
     const int mt = (mcols + 15) / 16;
+    GemvPlan p = plan_gemv(m, mt);
     GemvArgs a;
     a.w = m.w; a.sz = m.sz; a.nkt = m.nkt; a.units = p.units;
     a.n_real = m.paired ? m.rows / 2 : m.rows;
@@ -214,7 +214,7 @@ struct sp_engine {
     // attention plan of one forward call: same-sequence column groups (multi-query kernel) or one block row per column
     struct AttnPlan {
         bool mq = false;
-        int ngroups = 0, nchunk = 1;
+        int ngroups = 0, nchunk = 1, splits = 1;
         std::vector<AttnGroup> groups;
         std::vector<int> colnc;
     };
@@ -296,7 +296,10 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
         i = j;
     }
     p.ngroups = (int)p.groups.size();
-    for (auto &g : p.groups) p.mq = p.mq || g.ncols > 1;
+    int maxcols = 1;
+    for (auto &g : p.groups) { p.mq = p.mq || g.ncols > 1; maxcols = std::max(maxcols, g.ncols); }
+    const int G = d.n_heads / d.n_kv_heads;
+    p.splits = (maxcols * G + 63) / 64;
     p.colnc.assign(n, 0);
     int mx = 1;
     if (p.mq) {
@@ -334,8 +337,9 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
         if (l + 1 == d.n_layers && !logits_on) break;   // K/V-only: the last layer only needs its K/V
         const int G = NH / NKV;
         if (ap.mq) {
-            AttnMqArgs am{q, kc[l], vc[l], dtoks, dgroups, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
-            dim3 agrid(nchunk, NKV, ap.ngroups);
+            AttnMqArgs am{q, kc[l], vc[l], dtoks, dgroups, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD),
+                          attn_part, ap.splits};
+            dim3 agrid(nchunk, NKV, ap.ngroups * ap.splits);
             if (HD == 64) launch_attn_mq_hd<64>(G, agrid, st, am);
             else launch_attn_mq_hd<128>(G, agrid, st, am);
         } else {
@@ -547,7 +551,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         HIPCHK(hipMemcpyAsync(e->dgroups, ap.groups.data(), ap.ngroups * sizeof(AttnGroup), hipMemcpyHostToDevice, e->stream));
         HIPCHK(hipMemcpyAsync(e->dcolnc, ap.colnc.data(), n * sizeof(int), hipMemcpyHostToDevice, e->stream));
         if (use_graph) {
-            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups : -1);
+            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : -1);
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 // record on the private stream (the caller's may be the null stream, which cannot capture)
@@ -789,33 +793,43 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
                       const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
                       const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,
                       double temperature, int32_t max_depth, double *resid_dev, int32_t *out_dev, void *stream) {
+    (void)resid_dev;
     return guarded(nullptr, [&] {
         require(p_logits_dev && q_logits_dev && token_dev && trial_start_dev && n_trials_dev && trials_dev && u_dev &&
-                    resid_dev && out_dev, SP_EINVAL, "NULL pointer");
-        require(n_trials_total >= 0 && n_trials_total <= 4096, SP_EINVAL, "n_trials_total must be in [0, 4096]");
-        require(vocab >= 1 && ld >= vocab, SP_EINVAL, "bad vocab / ld");
+                    out_dev, SP_EINVAL, "NULL pointer");
+        require(n_trials_total >= 0 && n_trials_total <= 1024, SP_EINVAL, "n_trials_total must be in [0, 1024]");
+        require(vocab >= 1 && vocab <= ACC_NB * ACC_T * ACC_PER && ld >= vocab, SP_EINVAL, "bad vocab / ld");
         require(n_nodes >= 1 && n_nodes <= 64, SP_EINVAL, "n_nodes must be in [1, 64]");
         require(max_depth >= 1 && max_depth <= 63, SP_EINVAL, "max_depth must be in [1, 63]");
         require(n_u >= 1, SP_EINVAL, "need at least one uniform");
         require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
-        // the walk indexes nodes, trials and logits rows through these arrays: check them on the host first
-        std::vector<int32_t> tok(n_nodes), ts(n_nodes), nt(n_nodes), tr(std::max(n_trials_total, 1));
+        // the kernel checks every node / trial / token index it follows before using it (err = 2 if one is bad)
         hipStream_t st = (hipStream_t)stream;
-        HIPCHK(hipMemcpyAsync(tok.data(), token_dev, n_nodes * 4, hipMemcpyDeviceToHost, st));
-        HIPCHK(hipMemcpyAsync(ts.data(), trial_start_dev, n_nodes * 4, hipMemcpyDeviceToHost, st));
-        HIPCHK(hipMemcpyAsync(nt.data(), n_trials_dev, n_nodes * 4, hipMemcpyDeviceToHost, st));
-        if (n_trials_total) HIPCHK(hipMemcpyAsync(tr.data(), trials_dev, n_trials_total * 4, hipMemcpyDeviceToHost, st));
-        HIPCHK(hipStreamSynchronize(st));
-        for (int i = 0; i < n_nodes; ++i) {
-            require(tok[i] >= 0 && tok[i] < vocab, SP_EINVAL, "node token out of range");
-            require(ts[i] >= 0 && nt[i] >= 0 && ts[i] + nt[i] <= n_trials_total, SP_EINVAL, "trial range out of bounds");
+        // exchange words + timeout flag, one set per device, zeroed once; tags never repeat within 2^20 launches
+        static std::map<int, std::pair<unsigned long long *, unsigned *>> scratch_of;
+        static unsigned launches = 0;
+        int dev = 0;
+        HIPCHK(hipGetDevice(&dev));
+        auto it = scratch_of.find(dev);
+        if (it == scratch_of.end()) {
+            unsigned long long *xb = dev_alloc<unsigned long long>(4 * ACC_NB * 4);
+            unsigned *er = dev_alloc<unsigned>(1);
+            HIPCHK(hipMemset(xb, 0, 4 * ACC_NB * 4 * sizeof(unsigned long long)));
+            it = scratch_of.emplace(dev, std::make_pair(xb, er)).first;
         }
-        for (int j = 0; j < n_trials_total; ++j)
-            require(tr[j] > 0 && tr[j] < n_nodes, SP_EINVAL, "trial child index out of range");
+        launches = launches % 0xFFFFFu + 1;
+        HIPCHK(hipMemsetAsync(it->second.second, 0, sizeof(unsigned), st));
+        HIPCHK(hipMemsetAsync(out_dev, 0xff, (max_depth + 4) * sizeof(int32_t), st));
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token_dev, trial_start_dev, n_trials_dev, trials_dev, u_dev,
-                     n_u, 1.0 / temperature, resid_dev, out_dev, max_depth};
-        hipLaunchKernelGGL(k_accept_tree, dim3(1), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
-        HIPCHK(hipGetLastError());
+                     n_u, 1.0 / temperature, it->second.first, it->second.second, launches << 12, n_nodes,
+                     n_trials_total, out_dev, max_depth};
+        void *args[] = {&a};
+        HIPCHK(hipLaunchCooperativeKernel((const void *)k_accept_tree, dim3(ACC_NB), dim3(ACC_T), args, 0, st));
+        unsigned err = 0;
+        HIPCHK(hipMemcpyAsync(&err, it->second.second, sizeof(unsigned), hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+        require(err != 2, SP_EINVAL, "malformed tree: node, trial or token index out of range");
+        require(err == 0, SP_EHIP, "acceptance exchange timed out");
     });
 }
 

@@ -47,11 +47,16 @@ __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
     }
 }
 
+// Threads per block: single-column-tile variants use up to 16 waves (128 VGPRs each); wider variants up to 8 waves
+// (256 VGPRs) so the activation fragments of several column tiles stay in registers without spilling.
+template <int MT> struct GemvLimits { static constexpr int MAX_THREADS = MT == 1 ? 1024 : 512; };
+
 template <int FMT, int MT, int RG>
-__global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
+__global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     constexpr int KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
-    constexpr int TB = 4;                          // k-tiles whose loads are in flight together per wave
+    // k-tiles whose loads are in flight together per wave, sized to the register budget
+    constexpr int TB = FMT == 3 ? (MT == 1 ? 2 : 1) : (MT == 1 ? 4 : (MT == 2 ? 2 : 1));
     const int NW = blockDim.x >> 6;
     const int unit = blockIdx.x;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;

@@ -141,9 +141,23 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(const float *logits, int
     if (threadIdx.x == 0) out[s] = tok;
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Tree acceptance on ACC_NB co-resident blocks.  The vocabulary is cut into ACC_NB x ACC_T contiguous chunks of
+// C = ceil(V / (ACC_NB * ACC_T)) entries; thread t of block b owns chunk b * ACC_T + t and keeps its logits' weights
+// in registers.  Sums are taken sequentially inside a chunk, then sequentially over the ACC_T chunk sums of a block
+// (block partial), then sequentially over the ACC_NB block partials.  Block partials are all-gathered through
+// tagged 64-bit words (32-bit payload + 32-bit tag, single-copy atomic; relaxed agent-scope atomics, no fences), so
+// every block holds every partial and takes every accept / reject decision itself.
+//
+// Residual after j >= 1 rejections at a node: r_j = max(p - c_j q, 0) / S_j with c_1 = 1, S_j = sum of the numerator,
+// c_{j+1} = c_j + S_j -- algebraically the same as replacing p by norm(max(p - q, 0)) after each rejection, but each
+// rejection costs one reduction instead of a rewrite of the distribution.  All arithmetic is float64 with explicit
+// single roundings (no contraction): w = exp((l - m) * (1/T)), p_i = w_i / Z, d_i = p_i - c * q_i.
+constexpr int ACC_NB = 64, ACC_T = 256, ACC_PER = 16;
+
 struct AcceptArgs {
     const float *p_logits;   // target logits [nodes][ld]
-    const float *q_logits;   // drafter logits [nodes][ld] (rows of nodes with children)
+    const float *q_logits;   // drafter logits [nodes][ld] (rows of nodes with trials)
     int V, ld;
     const int *token;        // [nodes] token of node i (node 0 = root)
     const int *trial_start;  // [nodes] first entry of node i's trials
@@ -152,75 +166,258 @@ struct AcceptArgs {
     const double *u;         // uniforms, consumed in order
     int n_u;
     double invT;
-    double *resid;           // scratch [V] fp64
-    int *out;                // [0] accepted count k, [1..k] accepted node ids, [max_depth+1] final token,
-                             // [max_depth+2] uniforms consumed, [max_depth+3] 1 if final is a bonus draw
+    unsigned long long *xbuf;   // exchange words [4][ACC_NB][4]
+    unsigned *err;           // set to 1 if an exchange timed out
+    unsigned tag_base;       // distinct per launch (low 12 bits are the exchange counter)
+    int n_nodes, n_trials_total;
+    int *out;                // [0] k, [1..k] accepted node ids, [max_depth+1] final token, [max_depth+2] uniforms used,
+                             // [max_depth+3] bonus flag
     int max_depth;
 };
 
-// The whole acceptance walk in one block (it is sequential by nature; every step is a reduction over V).
-__global__ void __launch_bounds__(SMP_THREADS) k_accept_tree(AcceptArgs a) {
-    __shared__ SmpShared sh;
-    int cur = 0, k = 0, ui = 0;
-    int final_tok = -1, bonus = 0;
-    for (;;) {
-        const int nt = a.n_trials[cur];
-        const float *pl = a.p_logits + (size_t)cur * a.ld;
-        Dist p{0, pl, row_max(pl, a.V, sh), a.invT, nullptr};
-        if (nt == 0 || k >= a.max_depth) {                   // bonus draw from the target at the accepted leaf
-            dist_total(p, a.V, sh);
-            final_tok = dist_draw(p, a.V, ui < a.n_u ? a.u[ui] : 0.5, sh);
-            ++ui; bonus = 1;
-            break;
-        }
-        const float *ql = a.q_logits + (size_t)cur * a.ld;
-        Dist q{0, ql, row_max(ql, a.V, sh), a.invT, nullptr};
-        const double Zq = dist_total(q, a.V, sh);
-        double Zp = dist_total(p, a.V, sh);
-        bool residual = false;      // p is the explicit normalised residual in a.resid
-        int accepted = -1;
-        const int t0 = a.trial_start[cur];
-        for (int j = t0; j < t0 + nt && accepted < 0; ++j) {
-            {
-                const int c = a.trials[j];
-                const int x = a.token[c];
-                const double px = residual ? a.resid[x] : p.w(x) / Zp;
-                const double qx = q.w(x) / Zq;
-                const double uu = ui < a.n_u ? a.u[ui] : 0.5;
-                ++ui;
-                if (uu < px / qx) { accepted = c; break; }
-                // rejection: p <- norm(max(p - q, 0))
-                __syncthreads();
-                for (int i = threadIdx.x; i < a.V; i += blockDim.x) {
-                    const double pi = residual ? a.resid[i] : p.w(i) / Zp;
-                    const double di = pi - q.w(i) / Zq;
-                    a.resid[i] = di > 0.0 ? di : 0.0;
-                }
-                __syncthreads();
-                Dist r{1, nullptr, 0.f, 0.0, a.resid};
-                const double Zr = dist_total(r, a.V, sh);
-                for (int i = threadIdx.x; i < a.V; i += blockDim.x) a.resid[i] = a.resid[i] / Zr;
-                __syncthreads();
-                residual = true;
+struct AccShared {
+    double tsum[ACC_T];      // thread chunk sums
+    double bpart0[ACC_NB], bpart1[ACC_NB];
+    float fred[ACC_T / 64];
+    double tl;
+    int found;
+    int ok;
+};
+
+__device__ __forceinline__ double d_w(float l, float m, double invT) {
+    return exp(__dmul_rn(__dsub_rn((double)l, (double)m), invT));
+}
+
+// All-gather of two doubles per block.  Returns false on timeout (every block then stops).
+__device__ bool acc_exchange(const AcceptArgs &a, unsigned &ex, double v0, double v1, AccShared &sh) {
+    const unsigned tag = a.tag_base | (ex & 0xfffu);
+    unsigned long long *slot = a.xbuf + (size_t)(ex & 3u) * ACC_NB * 4;
+    ++ex;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long b0 = __double_as_longlong(v0), b1 = __double_as_longlong(v1);
+        const unsigned long long t = (unsigned long long)tag << 32;
+        unsigned long long *w = slot + blockIdx.x * 4;
+        __hip_atomic_store(w + 0, t | (b0 & 0xffffffffull), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(w + 1, t | (b0 >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(w + 2, t | (b1 & 0xffffffffull), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(w + 3, t | (b1 >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x == 0) sh.ok = 1;
+    __syncthreads();
+    if (threadIdx.x < ACC_NB) {
+        unsigned long long *w = slot + threadIdx.x * 4;
+        unsigned long long x0, x1, x2, x3;
+        long spins = 0;
+        for (;;) {
+            x0 = __hip_atomic_load(w + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            x1 = __hip_atomic_load(w + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            x2 = __hip_atomic_load(w + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            x3 = __hip_atomic_load(w + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((unsigned)(x0 >> 32) == tag && (unsigned)(x1 >> 32) == tag && (unsigned)(x2 >> 32) == tag &&
+                (unsigned)(x3 >> 32) == tag)
+                break;
+            if (++spins > (1l << 22) || __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                sh.ok = 0;
+                break;
             }
         }
+        sh.bpart0[threadIdx.x] = __longlong_as_double((long long)((x0 & 0xffffffffull) | (x1 << 32)));
+        sh.bpart1[threadIdx.x] = __longlong_as_double((long long)((x2 & 0xffffffffull) | (x3 << 32)));
+    }
+    __syncthreads();
+    return sh.ok != 0;
+}
+
+// Sequential sum of this block's ACC_T thread sums (thread 0), broadcast through LDS.
+__device__ double acc_block_sum(double mine, AccShared &sh) {
+    __syncthreads();
+    sh.tsum[threadIdx.x] = mine;
+    __syncthreads();
+    __shared__ double bs;
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int j = 0; j < ACC_T; ++j) t += sh.tsum[j];
+        bs = t;
+    }
+    __syncthreads();
+    return bs;
+}
+
+__device__ float acc_block_max(float v, AccShared &sh) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = sh.fred[0];
+    for (int j = 1; j < ACC_T / 64; ++j) t = fmaxf(t, sh.fred[j]);
+    return t;
+}
+
+// Inverse-CDF draw over the distributed weights w[] (this thread's chunk; thread chunk sums in sh.tsum, block
+// partials in bp).  Three levels, each "first entry whose running sum exceeds the target, else the last positive
+// entry": block (every block, redundantly), thread (thread 0 of the owning block), element (the owning thread).
+// If no weight is positive at all the token is 0.  Returns the token in the owning block, -1 in the others.
+__device__ int acc_draw(const double *w, int lo, int n, double u, const double *bp, AccShared &sh) {
+    double total = 0.0;
+    for (int b = 0; b < ACC_NB; ++b) total += bp[b];
+    const double target = __dmul_rn(u, total);
+    double P = 0.0, Pown = 0.0, Plast = 0.0;
+    int owner = -1, blast = 0;
+    for (int b = 0; b < ACC_NB; ++b) {
+        const double next = P + bp[b];
+        if (bp[b] > 0.0) { blast = b; Plast = P; }
+        if (target < next) { owner = b; Pown = P; break; }
+        P = next;
+    }
+    if (owner < 0) { owner = blast; Pown = Plast; }
+    if ((int)blockIdx.x != owner) return -1;
+    const double tb = __dsub_rn(target, Pown);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double q = 0.0, qsel = 0.0, qlast = 0.0;
+        int tsel = -1, tlast = 0;
+        for (int t = 0; t < ACC_T; ++t) {
+            const double next = q + sh.tsum[t];
+            if (sh.tsum[t] > 0.0) { tlast = t; qlast = q; }
+            if (tb < next) { tsel = t; qsel = q; break; }
+            q = next;
+        }
+        if (tsel < 0) { tsel = tlast; qsel = qlast; }
+        sh.found = tsel;
+        sh.tl = __dsub_rn(tb, qsel);
+    }
+    __syncthreads();
+    const int tsel = sh.found;
+    __syncthreads();
+    if ((int)threadIdx.x == tsel) {
+        const double tl = sh.tl;
+        double acc = 0.0;
+        int pick = -1, lastpos = -1;
+        for (int i = 0; i < ACC_PER; ++i) {
+            if (i < n) {
+                if (w[i] > 0.0) lastpos = lo + i;
+                acc += w[i];
+                if (acc > tl) { pick = lo + i; break; }
+            }
+        }
+        if (pick < 0) pick = lastpos >= 0 ? lastpos : lo;
+        sh.found = pick;
+    }
+    __syncthreads();
+    return sh.found;
+}
+
+// Stops every block identically (the condition depends only on the inputs) and reports a malformed tree.
+__device__ __forceinline__ bool acc_bad(const AcceptArgs &a) {
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(a.err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return false;
+}
+
+__global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
+    __shared__ AccShared sh;
+    const int C = (a.V + ACC_NB * ACC_T - 1) / (ACC_NB * ACC_T);
+    const int lo = (blockIdx.x * ACC_T + threadIdx.x) * C;
+    const int n = max(0, min(C, a.V - lo));
+    double wp[ACC_PER], wq[ACC_PER], w[ACC_PER];
+    unsigned ex = 0;
+    int cur = 0, k = 0, ui = 0, final_tok = -1, bonus = 0;
+    bool alive = true;
+    for (;;) {
+        const float *pl = a.p_logits + (size_t)cur * a.ld;
+        const int nt = a.n_trials[cur];
+        const int t0 = a.trial_start[cur];
+        if (nt < 0 || t0 < 0 || t0 > a.n_trials_total - nt) { alive = acc_bad(a); break; }
+        for (int j = t0; j < t0 + nt && alive; ++j) {
+            const int child = a.trials[j];
+            if (child <= 0 || child >= a.n_nodes || a.token[child] < 0 || a.token[child] >= a.V) alive = acc_bad(a);
+        }
+        if (!alive) break;
+        const bool draw_bonus = nt == 0 || k >= a.max_depth;
+        const float *ql = a.q_logits + (size_t)cur * a.ld;
+        // ---- global maxima
+        float mp = -INFINITY, mq = -INFINITY;
+        for (int i = 0; i < n; ++i) { mp = fmaxf(mp, pl[lo + i]); if (!draw_bonus) mq = fmaxf(mq, ql[lo + i]); }
+        mp = acc_block_max(mp, sh);
+        mq = acc_block_max(mq, sh);
+        if (!(alive = acc_exchange(a, ex, (double)mp, (double)mq, sh))) break;
+        float Mp = -INFINITY, Mq = -INFINITY;
+        for (int b = 0; b < ACC_NB; ++b) { Mp = fmaxf(Mp, (float)sh.bpart0[b]); Mq = fmaxf(Mq, (float)sh.bpart1[b]); }
+        // ---- weights and normalisers
+        double sp = 0.0, sq = 0.0;
+        for (int i = 0; i < ACC_PER; ++i) {
+            if (i < n) {
+                wp[i] = d_w(pl[lo + i], Mp, a.invT); sp += wp[i];
+                if (!draw_bonus) { wq[i] = d_w(ql[lo + i], Mq, a.invT); sq += wq[i]; }
+            } else { wp[i] = 0.0; wq[i] = 0.0; }
+        }
+        const double bsp = acc_block_sum(sp, sh);
+        const double bsq = acc_block_sum(sq, sh);
+        if (!(alive = acc_exchange(a, ex, bsp, bsq, sh))) break;
+        double Zp = 0.0, Zq = 0.0;
+        for (int b = 0; b < ACC_NB; ++b) { Zp += sh.bpart0[b]; Zq += sh.bpart1[b]; }
+        if (draw_bonus) {
+            // thread chunk sums of wp back into sh.tsum for the draw (block partials of wp are in sh.bpart0)
+            (void)acc_block_sum(sp, sh);
+            final_tok = acc_draw(wp, lo, n, ui < a.n_u ? a.u[ui] : 0.5, sh.bpart0, sh);
+            ++ui;
+            bonus = 1;
+            break;
+        }
+        // ---- trials in draw order
+        int accepted = -1, J = 0;
+        double c = 0.0, S = 0.0;
+        for (int j = t0; j < t0 + nt; ++j) {
+            const int child = a.trials[j];
+            const int x = a.token[child];
+            const double px0 = __ddiv_rn(d_w(pl[x], Mp, a.invT), Zp);
+            const double qx = __ddiv_rn(d_w(ql[x], Mq, a.invT), Zq);
+            double px = px0;
+            if (J > 0) {
+                const double dx = __dsub_rn(px0, __dmul_rn(c, qx));
+                px = dx > 0.0 ? __ddiv_rn(dx, S) : 0.0;
+            }
+            const double uu = ui < a.n_u ? a.u[ui] : 0.5;
+            ++ui;
+            if (uu < __ddiv_rn(px, qx)) { accepted = child; break; }
+            // rejection: next residual numerator max(p - c q, 0) with c = 1 (first) or c + S
+            c = J == 0 ? 1.0 : c + S;
+            ++J;
+            double sr = 0.0;
+            for (int i = 0; i < ACC_PER; ++i) {
+                if (i < n) {
+                    const double d = __dsub_rn(__ddiv_rn(wp[i], Zp), __dmul_rn(c, __ddiv_rn(wq[i], Zq)));
+                    w[i] = d > 0.0 ? d : 0.0;
+                    sr += w[i];
+                } else w[i] = 0.0;
+            }
+            // leaves this residual's thread chunk sums in sh.tsum for a possible final draw
+            const double bsr = acc_block_sum(sr, sh);
+            if (!(alive = acc_exchange(a, ex, bsr, 0.0, sh))) break;
+            S = 0.0;
+            for (int b = 0; b < ACC_NB; ++b) S += sh.bpart0[b];
+        }
+        if (!alive) break;
         if (accepted >= 0) {
-            if (threadIdx.x == 0) a.out[1 + k] = accepted;
+            if (blockIdx.x == 0 && threadIdx.x == 0) a.out[1 + k] = accepted;
             ++k;
             cur = accepted;
             continue;
         }
-        // every child rejected: draw from the residual
-        Dist r{1, nullptr, 0.f, 0.0, a.resid};
-        dist_total(r, a.V, sh);
-        final_tok = dist_draw(r, a.V, ui < a.n_u ? a.u[ui] : 0.5, sh);
+        // every trial rejected: draw from the last residual (weights w, block partials in sh.bpart0)
+        final_tok = acc_draw(w, lo, n, ui < a.n_u ? a.u[ui] : 0.5, sh.bpart0, sh);
         ++ui;
         break;
     }
+    if (!alive) return;
     if (threadIdx.x == 0) {
-        a.out[0] = k;
-        a.out[a.max_depth + 1] = final_tok;
-        a.out[a.max_depth + 2] = ui;
-        a.out[a.max_depth + 3] = bonus;
+        if (blockIdx.x == 0) {          // every block took the same decisions; block 0 reports them
+            a.out[0] = k;
+            a.out[a.max_depth + 2] = ui;
+            a.out[a.max_depth + 3] = bonus;
+        }
+        if (final_tok >= 0) a.out[a.max_depth + 1] = final_tok;   // only the block owning the draw has it
     }
 }

@@ -317,13 +317,12 @@ class TreeVerifier:
         arr = lambda x: torch.tensor(x if len(x) else [0], dtype=torch.int32, device=dev)
         tok, ts, nt, tr = arr(tree.token), arr(tree.trial_start), arr(tree.n_trials), arr(tree.trials)
         ud = torch.tensor(np.asarray(u, dtype=np.float64), device=dev)
-        resid = torch.empty(V, dtype=torch.float64, device=dev)
         out = torch.zeros(md + 4, dtype=torch.int32, device=dev)
         ptr = lambda t: ctypes.c_void_p(t.data_ptr())
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         self._lib.check(self.engine.lib.sp_op_accept_tree(
             ptr(p_logits), ptr(q_logits), V, p_logits.stride(0), tree.size, ptr(tok), ptr(ts), ptr(nt), ptr(tr),
-            len(tree.trials), ptr(ud), len(u), float(temperature), md, ptr(resid), ptr(out), stream))
+            len(tree.trials), ptr(ud), len(u), float(temperature), md, None, ptr(out), stream))
         o = out.cpu().tolist()
         k = o[0]
         return o[1:1 + k], o[md + 1], o[md + 2], bool(o[md + 3])

@@ -175,3 +175,81 @@ def test_oracle_acceptance_walk_samples_the_target_law():
         counts[first] += 1
     tv = 0.5 * np.abs(counts / n - p).sum()
     assert tv < 0.03, tv
+
+
+def _brute_inverse_cdf(w, u):
+    # first index whose exact prefix sum exceeds u * total (Fractions: no rounding anywhere)
+    from fractions import Fraction
+    fw = [Fraction(float(x)) for x in w]
+    target = Fraction(float(u)) * sum(fw)
+    run = Fraction(0)
+    for i, x in enumerate(fw):
+        run += x
+        if run > target:
+            return i
+    return max(i for i, x in enumerate(fw) if x > 0)
+
+
+@pytest.mark.parametrize('V', [1, 5, 300, 20000, 151936])
+def test_draws_equal_brute_force_inverse_cdf(V):
+    rng = np.random.default_rng(V)
+    w = rng.exponential(size=V)
+    w[rng.random(V) < 0.3] = 0.0             # zero weights inside chunks
+    if not (w > 0).any():
+        w[0] = 1.0
+    checked = 0
+    for u in list(rng.random(20 if V < 50000 else 6)) + [0.0, 1.0 - 2.0 ** -53]:
+        exp = _brute_inverse_cdf(w, u)
+        for fn in (ref.draw, ref.draw3):
+            tok, margin = fn(w, u)
+            if margin > 1e-12:
+                assert tok == exp, (fn.__name__, u)
+                checked += 1
+    assert checked > 0
+
+
+def test_draw3_fallbacks():
+    assert ref.draw3(np.zeros(7), 0.3)[0] == 0                       # nothing positive: token 0
+    w = np.zeros(40000); w[12345] = 2.0
+    assert ref.draw3(w, 0.999999)[0] == 12345                        # single positive entry in a late chunk
+    w = np.zeros(300); w[[3, 250]] = 1.0
+    assert ref.draw3(w, 1.0 - 2.0 ** -53)[0] == 250                  # target at the very top: last positive
+
+
+def test_walk_thresholds_follow_the_iterative_residual():
+    # each trial's acceptance threshold in the walk is r_j(x) / q(x) with r_j renormalised max(r_{j-1} - q, 0):
+    # a uniform just below it accepts, just above it rejects (pins the c_j closed form against the definition)
+    rng = np.random.default_rng(5)
+    V = 12
+    for _ in range(6):
+        pl = rng.normal(size=V).astype(np.float32) * 2
+        ql = rng.normal(size=V).astype(np.float32) * 2
+        T = 0.8
+        p = ref.softmax_weights(pl, T); p /= p.sum()
+        q = ref.softmax_weights(ql, T); q /= q.sum()
+        xs = [int(x) for x in rng.choice(V, size=4, replace=True, p=q)]
+        t = flatten(0, [[x] for x in xs])
+        tree = dict(token=t.token, trial_start=t.trial_start, n_trials=t.n_trials, trials=t.trials)
+        P, Q = np.stack([pl] * t.size), np.stack([ql] * t.size)
+        r, ratios = p.copy(), []
+        for x in xs:
+            ratios.append(r[x] / q[x])
+            d = np.maximum(r - q, 0.0)
+            r = d / d.sum()
+        for j, rho in enumerate(ratios):
+            if rho >= 1.0 or rho < 1e-6:
+                continue
+            for factor, accept in ((1 - 1e-9, True), (1 + 1e-9, False)):
+                u = [1.0 - 2.0 ** -53] * j + [rho * factor, 0.5, 0.5]
+                path, final, used, bonus, _ = ref.accept_tree(P, Q, tree, u, T, 1)
+                if accept:
+                    assert path and t.token[path[0]] == xs[j] and used == j + 2 and bonus
+                else:
+                    assert used >= j + 2 and (not path or t.token[path[0]] != xs[j] or xs.count(xs[j]) > 1)
+        # all rejected: the final draw follows the last residual
+        u = [1.0 - 2.0 ** -53] * len(xs) + [0.37]
+        if all(rho < 1.0 - 1e-9 for rho in ratios):
+            path, final, used, bonus, margin = ref.accept_tree(P, Q, tree, u, T, 1)
+            assert not path and not bonus and used == len(xs) + 1
+            if margin > 1e-9:
+                assert final == _brute_inverse_cdf(r, 0.37)
