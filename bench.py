@@ -136,6 +136,53 @@ def verify_cost(eng, cfg, prefix=2048, n_branches=8, depth=4, reps=20):
             'mfma_frac_f16': round(flops / t_verify / PEAK_F16, 4)}
 
 
+TRAFFIC_FILE = ROOT / 'profiles' / 'k_gemv_q8_gate_up_traffic.md'
+
+
+def measured_traffic():
+    """HBM bytes per gate_up launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter
+    scaled by what it reads for a plain copy of known size), or None when that summary is absent."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith('traffic_bytes_per_launch:'):
+                return int(line.split(':')[1])
+    except OSError:
+        pass
+    return None
+
+
+def gemv_roofline(eng):
+    """The dominant kernel: the SwiGLU gate_up GEMV (the largest launch of the step), launched on the engine's stream
+    cycling through all 28 layers (so its weights stream from HBM as in decode), HIP-event timed there."""
+    from seedplane_amd import _lib
+    us, gbytes = eng.time_gemv(_lib.SP_T_GATE_UP, layer=-1, n_cols=1, iters=280)
+    achieved = gbytes / (us * 1e-6) / 1e9
+    log(f'gate_up GEMV: {us:.2f} us/launch, {achieved:.0f} GB/s')
+    return {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM / 1e9, 'unit': 'GB/s',
+            'frac': round(achieved * 1e9 / PEAK_HBM, 4), 'traffic': measured_traffic(),
+            'kernel': 'k_gemv<Q8, 1 m-tile, gate+up pair> (SwiGLU gate_up, 17920x1536 int8 + scales)',
+            'bytes_per_launch': gbytes, 'avg_launch_us': round(us, 3)}
+
+
+def workload_roofline(args, out):
+    """Only the dominant kernel's timing (for counter runs), then a plain 512 MiB copy (torch elementwise multiply
+    by 1.0) whose FETCH_SIZE / WRITE_SIZE give the counters' scale."""
+    import torch
+    from seedplane_amd.presets import preset
+    from seedplane_amd.qwen_engine import Qwen2Engine
+    from seedplane_amd.synth import make_weights
+    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
+    eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    out['roofline'] = gemv_roofline(eng)
+    src = torch.ones(128 << 20, dtype=torch.float32, device='cuda')
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    sync()
+    out.update({'value': out['roofline']['achieved'], 'unit': 'GB/s', 'metric': 'gate_up GEMV HBM GB/s',
+                'copy_bytes_each_way': src.numel() * 4})
+
+
 def workload_c3(args, out):
     import torch
     from seedplane_amd import _lib
@@ -166,13 +213,7 @@ def workload_c3(args, out):
     step_bytes = wbytes + kv_bytes(cfg, min(W, cache.length))
     log(f'bs1: {tok_s:.1f} tok/s, {dt / args.steps * 1e3:.3f} ms/token, {step_bytes / 1e9:.3f} GB/token')
 
-    us, gbytes = eng.time_gemv(_lib.SP_T_GATE_UP, layer=0, n_cols=1, iters=200)
-    achieved = gbytes / (us * 1e-6) / 1e9
-    roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM / 1e9, 'unit': 'GB/s',
-                'frac': round(achieved * 1e9 / PEAK_HBM, 4), 'traffic': None,
-                'kernel': 'k_gemv<Q8, 1 m-tile, gate+up pair> (SwiGLU gate_up, 17920x1536 int8 + scales)',
-                'bytes_per_launch': gbytes, 'avg_launch_us': round(us, 3)}
-    log(f'gate_up GEMV: {us:.2f} us/launch, {achieved:.0f} GB/s')
+    roofline = gemv_roofline(eng)
 
     bs16 = None
     if not args.no_bs16:
@@ -317,7 +358,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=256)
     ap.add_argument('--warmup', type=int, default=16)
-    ap.add_argument('--workload', default='c3', choices=['c3', 'c2', 'c5', 'spec', 'verify'])
+    ap.add_argument('--workload', default='c3', choices=['c3', 'c2', 'c5', 'spec', 'verify', 'roofline'])
     ap.add_argument('--no-bs16', action='store_true')
     ap.add_argument('--no-verify', action='store_true')
     ap.add_argument('--no-cpu-baseline', action='store_true')
@@ -333,7 +374,8 @@ def main():
     torch.cuda.set_device(0)
     out = {'metric': METRIC, 'value': None, 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
            'ms_per_step': None, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None}
-    {'c3': workload_c3, 'c2': workload_c2, 'c5': workload_c5, 'spec': workload_spec, 'verify': workload_verify}[args.workload](args, out)
+    {'c3': workload_c3, 'c2': workload_c2, 'c5': workload_c5, 'spec': workload_spec, 'verify': workload_verify,
+     'roofline': workload_roofline}[args.workload](args, out)
     print(json.dumps(out), flush=True)
 
 

@@ -136,8 +136,9 @@ int sp_engine_sync(sp_engine *e);
 
 /* Measurement hook (no counterpart in the reference): launch the engine's own GEMV for matrix `kind` of `layer`
  * (same packing, split and epilogue as the decode step) `iters` times over n_cols columns on the engine's stream,
- * timed with HIP events.  Returns the average launch duration in microseconds and the packed bytes one launch
- * reads.  Clobbers the activation buffers (not the KV cache); call between forward passes only. */
+ * timed with HIP events.  layer -1 (per-layer kinds) cycles launch i through layer i mod n_layers, so the weights
+ * stream from HBM as in a decode step.  Returns the average launch duration in microseconds and the packed bytes one
+ * launch reads.  Clobbers the activation buffers (not the KV cache); call between forward passes only. */
 int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_cols, int32_t iters, float *avg_us,
                         uint64_t *bytes);
 

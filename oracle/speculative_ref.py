@@ -3,13 +3,13 @@
   * Forest / verify_greedy / ledger: seedplane/speculative.py:12-111 (same decisions, same tie rules).
   * Linear batched verify with rollback: experiments/hive_scaling/benchmark_speculative.py:59-135.
   * Seeded uniforms: SplitMix64 (Steele, Lea, Flood 2014) over a counter, u = (x >> 11) * 2^-53.
-  * Float64 draws (draw: 1024 contiguous chunks, each summed in index order, chunk sums added in chunk order) and
-    tree acceptance (accept_tree / draw3: 64 x 256 chunks, summed chunk, group, total) in the product's fixed
-    orders, so decisions can be compared bit for bit; each function also returns the smallest decision margin so a
-    test can show no comparison was within rounding of its threshold.
-  * Pins: draw / draw3 against brute-force inverse CDFs on exact rational weights and on permuted chunkings;
-    accept_tree through the speculative sampling theorem (Monte Carlo over the uniform-driven walk) and against
-    the analytic one-level law with the iterative residual.
+  * Float64 draws and tree acceptance in the product's fixed summation orders (draw: 1024 contiguous chunks, each
+    summed in index order, chunk sums added in chunk order; accept_tree / draw3: 64 x 256 chunks, summed per chunk,
+    per group of 256 by wave butterflies, then over groups), so decisions can be compared bit for bit; each function
+    also returns the smallest decision margin so a test can show no comparison was within rounding of its threshold.
+  * Pins: draw / draw3 against a brute-force inverse CDF in exact rational arithmetic (zeros, single positive
+    entries, top-of-range targets); accept_tree through the speculative sampling theorem (Monte Carlo over the
+    uniform-driven walk) and through per-trial thresholds recomputed with the iterative residual definition.
   * exact_first_token_distribution: the acceptance rule's output law computed analytically over every draft outcome
     (speculative sampling theorem: it must equal the target distribution p).
 """
@@ -172,17 +172,27 @@ def draw(w, u):
 ACC_NB, ACC_T = 64, 256
 
 
+def _butterfly(v):
+    """Sum of 64 values the way a wave's xor butterfly takes it (lane l adds lane l ^ o, o = 32, 16, ..., 1)."""
+    v = v.copy()
+    lanes = np.arange(64)
+    for o in (32, 16, 8, 4, 2, 1):
+        v = v + v[..., lanes ^ o]
+    return v[..., 0]
+
+
 def chunk_sums3(w):
     """Acceptance-walk summation order: ACC_NB * ACC_T contiguous chunks of C = ceil(V / (ACC_NB * ACC_T)) entries,
-    each summed in index order; each group of ACC_T chunk sums summed in order; the ACC_NB group sums summed in
-    order.  Returns (chunk sums, group sums, total, C)."""
+    each summed in index order; each group of ACC_T chunk sums reduced by a butterfly inside every 64-lane wave,
+    the wave sums added in order; the ACC_NB group sums added in order.  Returns (chunk sums, group sums, total, C)."""
     V = len(w)
     G = ACC_NB * ACC_T
     C = -(-V // G)
     padded = np.zeros(G * C)
     padded[:V] = w
     tsum = np.cumsum(padded.reshape(G, C), axis=1)[:, -1]
-    bsum = np.cumsum(tsum.reshape(ACC_NB, ACC_T), axis=1)[:, -1]
+    wsum = _butterfly(tsum.reshape(ACC_NB, ACC_T // 64, 64))
+    bsum = np.cumsum(wsum, axis=1)[:, -1]
     return tsum, bsum, np.cumsum(bsum)[-1], C
 
 

@@ -628,30 +628,39 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
         require(avg_us && bytes, SP_EINVAL, "NULL output");
         require(n_cols >= 1 && n_cols <= e->maxT && iters >= 1, SP_EINVAL, "n_cols must be in [1, max_tokens], iters >= 1");
         const bool per_layer = kind == SP_T_QKV || kind == SP_T_O || kind == SP_T_GATE_UP || kind == SP_T_DOWN;
-        require(!per_layer || (layer >= 0 && layer < d.n_layers), SP_EINVAL, "layer out of range");
+        require(!per_layer || (layer >= -1 && layer < d.n_layers), SP_EINVAL, "layer out of range");
         const int H = d.hidden, I = d.intermediate, NHD = d.n_heads * d.head_dim;
         hipStream_t st = e->stream;
+        // layer -1: launch i uses layer i mod n_layers, so the matrices stream from HBM as in a decode step
+        // instead of staying cached between launches
+        int cur = layer < 0 ? 0 : layer;
+        auto next_layer = [&] { if (layer < 0) cur = (cur + 1) % d.n_layers; };
         std::function<void()> launch;
         const DevMat *m = nullptr;
         switch (kind) {
-            case SP_T_QKV: m = &e->layers[layer].qkv;
-                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->qkv, nullptr, e->Nqkv, e->layers[layer].qkv_b, st); };
+            case SP_T_QKV: m = &e->layers[cur].qkv;
+                launch = [&] { launch_gemv(e->layers[cur].qkv, EPI_STORE, e->xn, H, n_cols, e->qkv, nullptr, e->Nqkv,
+                                           e->layers[cur].qkv_b, st); next_layer(); };
                 break;
-            case SP_T_O: m = &e->layers[layer].o;
-                launch = [&] { launch_gemv(*m, EPI_RESID, e->attn, NHD, n_cols, e->x, nullptr, H, nullptr, st); };
+            case SP_T_O: m = &e->layers[cur].o;
+                launch = [&] { launch_gemv(e->layers[cur].o, EPI_RESID, e->attn, NHD, n_cols, e->x, nullptr, H, nullptr,
+                                           st); next_layer(); };
                 break;
-            case SP_T_GATE_UP: m = &e->layers[layer].gate_up;
-                launch = [&] { launch_gemv(*m, EPI_SILU, e->xn, H, n_cols, nullptr, e->act, I, nullptr, st); };
+            case SP_T_GATE_UP: m = &e->layers[cur].gate_up;
+                launch = [&] { launch_gemv(e->layers[cur].gate_up, EPI_SILU, e->xn, H, n_cols, nullptr, e->act, I,
+                                           nullptr, st); next_layer(); };
                 break;
-            case SP_T_DOWN: m = &e->layers[layer].down;
-                launch = [&] { launch_gemv(*m, EPI_RESID, e->act, I, n_cols, e->x, nullptr, H, nullptr, st); };
+            case SP_T_DOWN: m = &e->layers[cur].down;
+                launch = [&] { launch_gemv(e->layers[cur].down, EPI_RESID, e->act, I, n_cols, e->x, nullptr, H, nullptr,
+                                           st); next_layer(); };
                 break;
             case SP_T_HEAD: case SP_T_EMBED: m = d.tied_head || kind == SP_T_EMBED ? &e->embed : &e->head;
                 launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->logits, nullptr, d.vocab, nullptr, st); };
                 break;
             default: throw Fail{SP_EINVAL, "kind must name a matrix"};
         }
-        require(m->w != nullptr, SP_ESTATE, "matrix not loaded");
+        // back-to-back launches between one event pair: the command processor overlaps each dispatch with the
+        // previous kernel's tail, so the average is the launch duration seen in a stream of GEMVs
         hipEvent_t a, b;
         HIPCHK(hipEventCreate(&a));
         HIPCHK(hipEventCreate(&b));

@@ -56,7 +56,7 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
     extern __shared__ __align__(16) unsigned char smem_raw[];
     constexpr int KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
     // k-tiles whose loads are in flight together per wave, sized to the register budget
-    constexpr int TB = FMT == 3 ? (MT == 1 ? 2 : 1) : (MT == 1 ? 4 : (MT == 2 ? 2 : 1));
+    constexpr int TB = FMT == 3 ? 2 : 4;
     const int NW = blockDim.x >> 6;
     const int unit = blockIdx.x;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -79,11 +79,13 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
     }
 
     for (int kb = wv; kb < a.nkt; kb += NW * TB) {
-        // ---- issue every load of TB tiles: codes, per-step scale (and zero), activation fragments
+        // ---- issue the weight loads of TB tiles (HBM latency) before anything is consumed; with one column tile
+        // the activation fragments are issued with them, wider variants fetch theirs (L2 hits) per tile below
         u32x4 wt[TB][RG];
         uint32_t sq8[TB][RG];
         u32x4 sq4[TB][RG];
-        f16x8 xa[TB][MT][ST];
+        constexpr int XB = MT == 1 ? TB : 1;       // tiles whose activation fragments are held at once
+        f16x8 xa[XB][MT][ST];
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
             const int kt = kb + t * NW;
@@ -94,12 +96,10 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
                 if constexpr (FMT == 2) sq8[t][rg] = *((const uint32_t *)(sbase[rg] + (size_t)kt * 32) + r);
                 if constexpr (FMT == 3) sq4[t][rg] = *((const u32x4 *)(sbase[rg] + (size_t)kt * 128) + r);
             }
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const int m = mt * 16 + r;
+            if constexpr (MT == 1) {
 #pragma unroll
                 for (int s = 0; s < ST; ++s)
-                    xa[t][mt][s] = m < a.m ? *(const f16x8 *)(a.x + (size_t)m * a.ldx + kt * KT + s * 32 + 8 * g) : zero8;
+                    xa[t][0][s] = r < a.m ? *(const f16x8 *)(a.x + (size_t)r * a.ldx + kt * KT + s * 32 + 8 * g) : zero8;
             }
         }
         // ---- MFMA per quant block
@@ -107,25 +107,35 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
         for (int t = 0; t < TB; ++t) {
             const int kt = kb + t * NW;
             if (kt >= a.nkt) break;
+            const int xt = MT == 1 ? t : 0;
+            if constexpr (MT > 1) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int m = mt * 16 + r;
+#pragma unroll
+                    for (int s = 0; s < ST; ++s)
+                        xa[0][mt][s] = m < a.m ? *(const f16x8 *)(a.x + (size_t)m * a.ldx + kt * KT + s * 32 + 8 * g) : zero8;
+                }
+            }
 #pragma unroll
             for (int s = 0; s < ST; ++s) {
                 f32x4 xs[MT];
                 if constexpr (FMT == 3) {
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) xs[mt] = mfma16(xa[t][mt][s], ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                    for (int mt = 0; mt < MT; ++mt) xs[mt] = mfma16(xa[xt][mt][s], ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
                 }
 #pragma unroll
                 for (int rg = 0; rg < RG; ++rg) {
                     const f16x8 b = unpack_step<FMT>(wt[t][rg], s);
                     if constexpr (FMT == 1) {
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) acc[rg][mt] = mfma16(xa[t][mt][s], b, acc[rg][mt]);
+                        for (int mt = 0; mt < MT; ++mt) acc[rg][mt] = mfma16(xa[xt][mt][s], b, acc[rg][mt]);
                     } else if constexpr (FMT == 2) {
                         const uint32_t d = sq8[t][rg];
                         const float scale = (float)__builtin_bit_cast(f16, (uint16_t)(s == 0 ? (d & 0xffffu) : (d >> 16)));
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt)
-                            acc[rg][mt] += scale * mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+                            acc[rg][mt] += scale * mfma16(xa[xt][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
                     } else {
                         uint32_t d;
                         if (s == 0) d = sq4[t][rg].x; else if (s == 1) d = sq4[t][rg].y; else if (s == 2) d = sq4[t][rg].z; else d = sq4[t][rg].w;
@@ -133,7 +143,7 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
                         const float zero = (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt) {
-                            const f32x4 dd = mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+                            const f32x4 dd = mfma16(xa[xt][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
                             acc[rg][mt] += scale * (dd - zero * xs[mt]);
                         }
                     }

@@ -144,8 +144,8 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(const float *logits, int
 // ---------------------------------------------------------------------------------------------------------------
 // Tree acceptance on ACC_NB co-resident blocks.  The vocabulary is cut into ACC_NB x ACC_T contiguous chunks of
 // C = ceil(V / (ACC_NB * ACC_T)) entries; thread t of block b owns chunk b * ACC_T + t and keeps its logits' weights
-// in registers.  Sums are taken sequentially inside a chunk, then sequentially over the ACC_T chunk sums of a block
-// (block partial), then sequentially over the ACC_NB block partials.  Block partials are all-gathered through
+// in registers.  Sums are taken sequentially inside a chunk, then over the ACC_T chunk sums of a block (butterfly in
+// each wave, wave sums in order: the block partial), then sequentially over the ACC_NB block partials.  Block partials are all-gathered through
 // tagged 64-bit words (32-bit payload + 32-bit tag, single-copy atomic; relaxed agent-scope atomics, no fences), so
 // every block holds every partial and takes every accept / reject decision itself.
 //
@@ -230,19 +230,22 @@ __device__ bool acc_exchange(const AcceptArgs &a, unsigned &ex, double v0, doubl
     return sh.ok != 0;
 }
 
-// Sequential sum of this block's ACC_T thread sums (thread 0), broadcast through LDS.
+// Block sum of the ACC_T thread chunk sums: butterfly inside each wave (lane l adds lane l ^ o for o = 32 .. 1, so
+// every lane holds the same value), then the ACC_T / 64 wave sums in wave order.  Also leaves the thread sums in
+// sh.tsum for a draw.
 __device__ double acc_block_sum(double mine, AccShared &sh) {
+    __shared__ double wsum[ACC_T / 64];
     __syncthreads();
     sh.tsum[threadIdx.x] = mine;
+    double v = mine;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SP_WAVE);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = v;
     __syncthreads();
-    __shared__ double bs;
-    if (threadIdx.x == 0) {
-        double t = 0.0;
-        for (int j = 0; j < ACC_T; ++j) t += sh.tsum[j];
-        bs = t;
-    }
-    __syncthreads();
-    return bs;
+    double t = 0.0;
+#pragma unroll
+    for (int j = 0; j < ACC_T / 64; ++j) t += wsum[j];
+    return t;
 }
 
 __device__ float acc_block_max(float v, AccShared &sh) {

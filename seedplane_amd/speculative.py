@@ -251,6 +251,7 @@ class TreeVerifier:
         self.engine = engine
         self._lib = _lib
         self.torch = torch
+        self._out = {}
 
     def forward(self, cache, tree: FlatTree, logits_out=None, graph=False):
         """One pass over every node: node i is written at cache position cache.length + i, RoPE position
@@ -314,15 +315,28 @@ class TreeVerifier:
         dev = p_logits.device
         V = p_logits.shape[1]
         md = max(1, tree.max_depth)
-        arr = lambda x: torch.tensor(x if len(x) else [0], dtype=torch.int32, device=dev)
-        tok, ts, nt, tr = arr(tree.token), arr(tree.trial_start), arr(tree.n_trials), arr(tree.trials)
-        ud = torch.tensor(np.asarray(u, dtype=np.float64), device=dev)
-        out = torch.zeros(md + 4, dtype=torch.int32, device=dev)
+        # one host->device copy: float64 uniforms first (8-byte aligned), then the int32 tree arrays
+        ints = [tree.token, tree.trial_start, tree.n_trials, tree.trials if len(tree.trials) else [0]]
+        nu = len(u)
+        sizes = [len(x) for x in ints]
+        host = np.empty(nu * 2 + sum(sizes), dtype=np.int32)
+        host[:nu * 2] = np.asarray(u, dtype=np.float64).view(np.int32)
+        off, offs = nu * 2, []
+        for x, n in zip(ints, sizes):
+            host[off:off + n] = x
+            offs.append(off)
+            off += n
+        buf = torch.from_numpy(host).to(dev)
+        out = self._out.get((dev, md))
+        if out is None:
+            out = self._out[(dev, md)] = torch.empty(md + 4, dtype=torch.int32, device=dev)
+        base = buf.data_ptr()
+        at = lambda o: ctypes.c_void_p(base + 4 * o)
         ptr = lambda t: ctypes.c_void_p(t.data_ptr())
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         self._lib.check(self.engine.lib.sp_op_accept_tree(
-            ptr(p_logits), ptr(q_logits), V, p_logits.stride(0), tree.size, ptr(tok), ptr(ts), ptr(nt), ptr(tr),
-            len(tree.trials), ptr(ud), len(u), float(temperature), md, None, ptr(out), stream))
+            ptr(p_logits), ptr(q_logits), V, p_logits.stride(0), tree.size, at(offs[0]), at(offs[1]), at(offs[2]),
+            at(offs[3]), len(tree.trials), at(0), nu, float(temperature), md, None, ptr(out), stream))
         o = out.cpu().tolist()
         k = o[0]
         return o[1:1 + k], o[md + 1], o[md + 2], bool(o[md + 3])

@@ -135,3 +135,34 @@ def test_identical_drafter_accepts_every_draft(model, gpu_device):
     # step keeps all `depth` drafts plus a bonus
     assert stats.steps == 4 and len(out) == stats.emitted
     assert stats.accepted >= 3 * stats.steps - 2
+
+
+def test_linear_verify_with_rollback_matches_fresh_run(model):
+    # benchmark_speculative.py:85-131: one batched pass over the draft, accept by row argmax, roll the cache back
+    # by assigning length, continue with the correction; the cache must then equal a fresh run of the emitted tokens
+    cfg, w, eng, ref = model
+    prefix = random_prompt(11, cfg['vocab_size'], seed=12)
+    greedy, _ = ref.generate_greedy(prefix, 5)
+    for draft in (greedy[:4], greedy[:2] + [7, 8], [9] + greedy[1:4]):
+        cache = eng.new_cache(64)
+        pre, _ = eng.forward(prefix, cache)
+        pre_id = int(torch.argmax(pre[-1]))
+        old = cache.length
+        block, _ = eng.forward(draft, cache, all_logits=True)
+        block_ids = [int(torch.argmax(r)) for r in block]
+        emitted, accepted, keep = sref.linear_verify(draft, pre_id, block_ids)
+        cache.length = old + keep
+        if len(emitted) > keep:                       # a correction token follows the kept drafts
+            nxt, _ = eng.forward([emitted[-1]], cache)
+        else:
+            nxt = block[-1:]
+        fresh, _ = eng.forward(prefix + emitted, eng.new_cache(64))
+        assert cache.length == len(prefix) + len(emitted)
+        assert max_rel(nxt[-1], fresh[-1]) < TOL, draft
+        exp_emitted = []                              # greedy reference semantics of the same rule
+        for i, d in enumerate(draft):
+            exp_emitted.append(greedy[i])
+            if d != greedy[i]:
+                break
+        if all(top2_margin(r) > TOL * float(r.abs().max()) for r in ref.teacher_forced(prefix, greedy[:5])):
+            assert emitted == exp_emitted, (draft, emitted, exp_emitted)

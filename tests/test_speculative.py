@@ -253,3 +253,11 @@ def test_walk_thresholds_follow_the_iterative_residual():
             assert not path and not bonus and used == len(xs) + 1
             if margin > 1e-9:
                 assert final == _brute_inverse_cdf(r, 0.37)
+
+
+def test_first_argmax_is_pythons_max_rule():
+    # speculative.py:68,80 pick max(range(n), key=logits.__getitem__): the first maximal index
+    rng = random.Random(4)
+    for _ in range(500):
+        v = [rng.choice([0.0, 0.5, 1.0, -1.0]) for _ in range(rng.randint(1, 9))]
+        assert ref.first_argmax(v) == max(range(len(v)), key=v.__getitem__)
