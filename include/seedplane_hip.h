@@ -61,7 +61,9 @@ enum {
 enum {
     SP_F_LOGITS = 1,      /* run the final norm + LM head and produce fp32 logits for every column   */
     SP_F_ARGMAX = 2,      /* also produce the greedy id per column (first index on ties)             */
-    SP_F_GRAPH = 4        /* capture the step into a hipGraph on first use and replay it afterwards  */
+    SP_F_GRAPH = 4,       /* capture the step into a hipGraph on first use and replay it afterwards  */
+    SP_F_PERSISTENT = 8   /* one decode column without a tree: run the whole step as one persistent   */
+                          /* cooperative kernel when the model fits it (else the kernel chain runs)  */
 };
 
 typedef struct sp_model_desc {
@@ -122,6 +124,10 @@ int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots);
  * waits for the stream. */
 int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t flags, float *logits_dev,
                       int32_t *argmax_host);
+
+/* Introspection (no counterpart in the reference): which implementation ran the last sp_engine_forward call:
+ * 1 = the persistent single-column kernel (SP_F_PERSISTENT accepted), 0 = the kernel chain, -1 = none yet. */
+int sp_engine_last_path(const sp_engine *e);
 
 /* Device pointer to the engine's fp32 logits buffer [max_tokens][vocab] holding the last SP_F_LOGITS call. */
 int sp_engine_logits(sp_engine *e, float **logits_dev);

@@ -17,6 +17,7 @@
 
 #include "../../include/seedplane_hip.h"
 #include "sp_attn.h"
+#include "sp_decode.h"
 #include "sp_gemv.h"
 #include "sp_pack.h"
 #include "sp_sample.h"
@@ -211,6 +212,23 @@ struct sp_engine {
 
     std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;
 
+    // persistent decode kernel state (built on first use, rebuilt when the KV pool moves)
+    struct Persistent {
+        bool tried = false, ok = false;
+        std::string why;                 // reason it is unavailable
+        mk::LayerW *d_layers = nullptr;
+        mk::u64 *ll = nullptr;
+        unsigned *err = nullptr;
+        size_t words = 0;
+        unsigned launch = 0;
+        int nb = 0;
+        const f16 *kv0 = nullptr;        // layer-0 key cache the table was built for
+        mk::Args args{};
+    } pk;
+    int last_path = -1;
+    bool persistent_setup();
+    bool persistent_step(const sp_token &t, int flags);
+
     // attention plan of one forward call: same-sequence column groups (multi-query kernel) or one block row per column
     struct AttnPlan {
         bool mq = false;
@@ -242,6 +260,8 @@ void sp_engine::free_all() {
     for (auto p : kc) dev_free(p);
     for (auto p : vc) dev_free(p);
     kc.clear(); vc.clear();
+    dev_free(pk.d_layers); dev_free(pk.ll); dev_free(pk.err);
+    pk = Persistent{};
     if (own_stream && stream) (void)hipStreamDestroy(stream);
     if (capture_stream) (void)hipStreamDestroy(capture_stream);
     stream = nullptr;
@@ -316,6 +336,128 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
     }
     p.nchunk = graph ? max_nchunk : mx;
     return p;
+}
+
+// ------------------------------------------------------------------------------------------- persistent decode
+namespace {
+template <int FMT, int HD>
+const void *decode_kernel() { return (const void *)mk::k_decode<FMT, HD>; }
+
+const void *pick_decode_kernel(int fmt, int hd) {
+    if (hd == 64) return fmt == 1 ? decode_kernel<1, 64>() : fmt == 2 ? decode_kernel<2, 64>() : decode_kernel<3, 64>();
+    return fmt == 1 ? decode_kernel<1, 128>() : fmt == 2 ? decode_kernel<2, 128>() : decode_kernel<3, 128>();
+}
+
+mk::Mat mk_mat(const DevMat &m) {
+    mk::Mat r;
+    r.w = m.w; r.sz = m.sz; r.nkt = m.nkt;
+    r.groups = m.rows_pad / 16 / (m.paired ? 2 : 1);
+    r.rows = m.paired ? m.rows / 2 : m.rows;
+    return r;
+}
+
+int kt_of(int fmt) { return fmt == 1 ? 32 : fmt == 2 ? 64 : 128; }
+}  // namespace
+
+// Checks that the model fits the persistent kernel's fixed on-chip buffers and builds its tables.  Returns false
+// (with pk.why) when it does not; the kernel chain is then used.
+bool sp_engine::persistent_setup() {
+    const int H = d.hidden, NH = d.n_heads, NKV = d.n_kv_heads, HD = d.head_dim, I = d.intermediate;
+    const int fmt = embed.fmt, KT = kt_of(fmt);
+    if (pk.tried && pk.ok && pk.kv0 == kc[0]) return true;
+    if (pk.tried && !pk.ok) return false;
+    pk.tried = true;
+    auto no = [&](const char *why) { pk.why = why; pk.ok = false; return false; };
+    if (HD != 64 && HD != 128) return no("head_dim must be 64 or 128");
+    if (NH % NKV || NH / NKV > mk::MAX_G) return no("query group larger than 8");
+    if (H > mk::MAX_H) return no("hidden size above 4096");
+    const DevMat &hm = d.tied_head ? embed : head;
+    std::vector<const DevMat *> mats = {&hm};
+    for (auto &l : layers) { mats.push_back(&l.qkv); mats.push_back(&l.o); mats.push_back(&l.gate_up); mats.push_back(&l.down); }
+    for (auto m : mats) {
+        if (m->fmt != fmt) return no("mixed weight formats");
+        if (m->nkt * KT > mk::MAX_K) return no("a matrix is wider than the on-chip operand buffer");
+    }
+    int dev = 0, ncu = 0;
+    HIPCHK(hipGetDevice(&dev));
+    HIPCHK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    const void *kern = pick_decode_kernel(fmt, HD);
+    int per_cu = 0;
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, mk::NT, 0));
+    if (per_cu < 1) return no("the persistent kernel does not fit on a CU");
+    pk.nb = ncu;
+    const int G = NH / NKV, Nqkv = (NH + 2 * NKV) * HD;
+    const Layer &l0 = layers[0];
+    auto split = [&](const DevMat &m, int limit) {
+        const int groups = m.rows_pad / 16 / (m.paired ? 2 : 1);
+        int sp = std::max(1, pk.nb / std::max(1, groups));
+        sp = std::min(sp, std::max(1, m.nkt / 4));
+        return std::max(1, std::min(sp, limit));
+    };
+    const int S1 = split(l0.qkv, mk::STAGE / ((G + 2) * HD));
+    const int S3 = split(l0.o, mk::STAGE / H);
+    int S5 = split(l0.down, mk::STAGE / H);
+    while (S5 > 1 && ((l0.down.nkt + S5 - 1) / S5) * KT > mk::STAGE) --S5;
+    if (((l0.down.nkt + S5 - 1) / S5 + 1) * KT > mk::STAGE) return no("intermediate slice too large");
+    if (NH * HD > mk::STAGE || S1 * (G + 2) * HD > mk::STAGE) return no("attention operands too large");
+    const int nchunk_max = (n_slots + ATT_CH - 1) / ATT_CH;
+    if (nchunk_max > mk::MAX_CHUNKS || nchunk_max * (HD + 2) > mk::STAGE) return no("KV window too long");
+
+    mk::Args &A = pk.args;
+    A = mk::Args{};
+    A.embed = mk_mat(embed); A.head = mk_mat(hm);
+    A.final_norm = final_norm; A.inv_freq = inv_freq;
+    A.L = d.n_layers; A.H = H; A.NH = NH; A.NKV = NKV; A.I = I; A.V = d.vocab; A.n_slots = n_slots;
+    A.eps = d.rms_eps; A.scale = 1.0f / std::sqrt((float)HD);
+    A.S1 = S1; A.S3 = S3; A.S5 = S5;
+    A.lw_qkv = 0;
+    A.lw_part = A.lw_qkv + (size_t)S1 * Nqkv;
+    A.lw_attn = A.lw_part + (size_t)NH * nchunk_max * (HD + 2);
+    A.lw_o = A.lw_attn + (size_t)NH * HD;
+    A.lw_act = A.lw_o + (size_t)S3 * H;
+    A.lw_d = A.lw_act + (size_t)I;
+    A.lw_layer = A.lw_d + (size_t)S5 * H;
+    A.lw_am = (size_t)d.n_layers * A.lw_layer;
+    A.nchunk_max = nchunk_max;
+    std::vector<mk::LayerW> tab(d.n_layers);
+    for (int i = 0; i < d.n_layers; ++i) {
+        const Layer &L = layers[i];
+        tab[i] = mk::LayerW{mk_mat(L.qkv), mk_mat(L.o), mk_mat(L.gate_up), mk_mat(L.down), L.qkv_b, L.in_norm,
+                            L.post_norm, kc[i], vc[i]};
+    }
+    dev_free(pk.d_layers); dev_free(pk.ll); dev_free(pk.err);
+    pk.d_layers = nullptr; pk.ll = nullptr; pk.err = nullptr;
+    pk.d_layers = dev_alloc<mk::LayerW>(d.n_layers);
+    HIPCHK(hipMemcpy(pk.d_layers, tab.data(), tab.size() * sizeof(mk::LayerW), hipMemcpyHostToDevice));
+    pk.words = A.lw_am + 2 * (size_t)pk.nb;
+    pk.ll = dev_alloc<mk::u64>(pk.words);
+    HIPCHK(hipMemset(pk.ll, 0, pk.words * sizeof(mk::u64)));      // tag 0 is never used
+    pk.err = dev_alloc<unsigned>(1);
+    A.layers = pk.d_layers; A.ll = pk.ll; A.err = pk.err;
+    pk.kv0 = kc[0];
+    pk.ok = true;
+    return true;
+}
+
+// One decode column through the persistent kernel.  Returns false (nothing launched) when the column or the model
+// does not fit it.
+bool sp_engine::persistent_step(const sp_token &t, int flags) {
+    if (t.tree_count != 0 || t.ctx_hi < t.ctx_lo || t.slot != t.ctx_hi % n_slots || !(flags & SP_F_LOGITS)) return false;
+    if (pk.kv0 != (kc.empty() ? nullptr : kc[0])) pk.tried = false;       // KV pool reallocated: rebuild tables
+    if (!persistent_setup()) return false;
+    const int nlin = t.ctx_hi - t.ctx_lo + 1;
+    if ((nlin + ATT_CH - 1) / ATT_CH > pk.args.nchunk_max) return false;
+    mk::Args A = pk.args;
+    pk.launch = pk.launch % 0xFFFFFu + 1;
+    A.tag0 = pk.launch << 12;
+    A.tok = dtoks;
+    A.logits = logits;
+    A.out_id = am_out;
+    HIPCHK(hipMemsetAsync(pk.err, 0, sizeof(unsigned), stream));
+    void *args[] = {&A};
+    HIPCHK(hipLaunchCooperativeKernel(pick_decode_kernel(embed.fmt, d.head_dim), dim3(pk.nb), dim3(mk::NT), args, 0,
+                                      stream));
+    return true;
 }
 
 void sp_engine::step(int n, int flags, const AttnPlan &ap) {
@@ -546,6 +688,21 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         }
         const bool use_graph = flags & SP_F_GRAPH;
         const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX);
+        if (n == 1 && (flags & SP_F_PERSISTENT)) {
+            HIPCHK(hipMemcpyAsync(e->dtoks, toks, sizeof(sp_token), hipMemcpyHostToDevice, e->stream));
+            if (e->persistent_step(toks[0], sflags)) {
+                e->last_path = 1;
+                unsigned err = 0;
+                if (logits_dev)
+                    HIPCHK(hipMemcpyAsync(logits_dev, e->logits, (size_t)d.vocab * sizeof(float), hipMemcpyDeviceToDevice, e->stream));
+                if (argmax_host) HIPCHK(hipMemcpyAsync(argmax_host, e->am_out, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
+                HIPCHK(hipMemcpyAsync(&err, e->pk.err, sizeof(unsigned), hipMemcpyDeviceToHost, e->stream));
+                HIPCHK(hipStreamSynchronize(e->stream));
+                require(err == 0, SP_EHIP, "persistent decode kernel: a cross-block exchange timed out");
+                return;
+            }
+        }
+        e->last_path = 0;
         const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
         HIPCHK(hipMemcpyAsync(e->dtoks, toks, n * sizeof(sp_token), hipMemcpyHostToDevice, e->stream));
         HIPCHK(hipMemcpyAsync(e->dgroups, ap.groups.data(), ap.ngroups * sizeof(AttnGroup), hipMemcpyHostToDevice, e->stream));
@@ -587,6 +744,14 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         }
     });
 }
+
+int sp_engine_last_path(const sp_engine *e) { return e ? e->last_path : -1; }
+
+#ifdef SP_DECODE_TRACE
+int sp_debug_decode_trace(unsigned long long *host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(mk::trace_buf), sizeof(mk::trace_buf)) == hipSuccess ? SP_OK : SP_EHIP;
+}
+#endif
 
 int sp_engine_logits(sp_engine *e, float **logits_dev) {
     if (!e || !logits_dev) { g_err = "NULL argument"; return SP_EINVAL; }
