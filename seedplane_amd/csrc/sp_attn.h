@@ -203,6 +203,127 @@ __global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
     if (lane == 0) { out[0] = m; out[1] = l; }
 }
 
+// Decode attention without a split-K combine: one block per (kv head, column) takes every visible key of a column
+// whose keys are one ring range (no tree block).  Wave w owns a contiguous slice of the keys and walks it in
+// sub-chunks of 32: S = Q K^T on MFMA (rows = the G query heads of the kv head, K fragments straight from the cache),
+// online softmax per row, P and V^T staged in the wave's own LDS region, O += P V on MFMA.  The 8 wave states are
+// merged in wave order and the fp16 attention rows written as k_attn_combine writes them.
+constexpr int DEC_WAVES = 8, DEC_KC = 32, DEC_MAX_KEYS = 256;
+template <int HD>
+__global__ void __launch_bounds__(64 * DEC_WAVES) k_attn_dec(AttnArgs a, f16 *out, int ldo) {
+    constexpr int ST = HD / 32, NDT = HD / 16, KP = DEC_KC + 8;
+    __shared__ __align__(16) f16 vt[DEC_WAVES][HD][KP];      // V^T of the wave's current sub-chunk
+    __shared__ __align__(16) f16 ps[DEC_WAVES][16][KP];      // P of the wave's current sub-chunk
+    __shared__ float wm[DEC_WAVES][16], wl[DEC_WAVES][16];
+    __shared__ float wo[DEC_WAVES][8][HD];                   // wave outputs of the (at most 8) query heads
+    const int kvh = blockIdx.x, b = blockIdx.y;
+    const sp_token t = a.toks[b];
+    const int G = a.NH / a.NKV;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const int nlin = t.ctx_hi - t.ctx_lo + 1;
+    const int kw = ((nlin + DEC_WAVES - 1) / DEC_WAVES + DEC_KC - 1) / DEC_KC * DEC_KC;   // keys per wave
+    const int v_lo = w * kw, v_hi = min(nlin, v_lo + kw);
+    const size_t head_base = ((size_t)t.seq * a.NKV + kvh) * a.n_slots;
+    // Q fragments (rows = query heads of this kv head, scaled, fp16)
+    f16x8 qa[ST];
+    const float *qrow = a.q + (size_t)b * a.NH * HD + (size_t)(kvh * G + min(r16, G - 1)) * HD;
+#pragma unroll
+    for (int st = 0; st < ST; ++st) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qa[st][e] = r16 < G ? (f16)(qrow[st * 32 + g4 * 8 + e] * a.scale) : (f16)0.f;
+    }
+    float mrow[4], lrow[4];
+    f32x4 o[NDT];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { mrow[j] = -INFINITY; lrow[j] = 0.f; }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    for (int v0 = v_lo; v0 < v_hi; v0 += DEC_KC) {
+        // V rows of the sub-chunk (lane: key v0 + lane / 2, dims (lane & 1) * HD/2 ..) -> V^T in LDS
+        constexpr int VPL = HD / 2 / 8;                      // 16-byte pieces per lane
+        {
+            const int key = v0 + (lane >> 1);
+            const bool live = key < v_hi;
+            const size_t off = (head_base + (size_t)((t.ctx_lo + key) % a.n_slots)) * HD + (lane & 1) * (HD / 2);
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                const f16x8 vv = live ? *(const f16x8 *)(a.vc + off + i * 8) : zero8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vt[w][(lane & 1) * (HD / 2) + i * 8 + e][lane >> 1] = vv[e];
+            }
+        }
+        // S = Q K^T for 2 tiles of 16 keys; K fragments from the cache (lane: key r16, dims g4 * 8 ..)
+        f32x4 sc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int key = v0 + kt * 16 + r16;
+            const bool live = key < v_hi;
+            const size_t off = (head_base + (size_t)((t.ctx_lo + key) % a.n_slots)) * HD + g4 * 8;
+            sc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < ST; ++st)
+                sc[kt] = mfma16(qa[st], live ? *(const f16x8 *)(a.kc + off + st * 32) : zero8, sc[kt]);
+        }
+        // online softmax: lane holds rows 4 g4 + j, keys v0 + kt * 16 + r16
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float mx = mrow[j];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) if (v0 + kt * 16 + r16 < v_hi) mx = fmaxf(mx, sc[kt][j]);
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, SP_WAVE));
+            const float corr = mrow[j] == -INFINITY ? 0.f : expf(mrow[j] - mx);
+            float ls = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const float pe = v0 + kt * 16 + r16 < v_hi ? expf(sc[kt][j] - mx) : 0.f;
+                ps[w][4 * g4 + j][kt * 16 + r16] = (f16)pe;
+                ls += pe;
+            }
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) ls += __shfl_xor(ls, sh, SP_WAVE);
+            lrow[j] = lrow[j] * corr + ls;
+            mrow[j] = mx;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) o[dt][j] *= corr;
+        }
+        __builtin_amdgcn_wave_barrier();                     // LDS is in order within a wave: P and V^T are in place
+        const f16x8 pa = *(const f16x8 *)&ps[w][r16][g4 * 8];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+            o[dt] = mfma16(pa, *(const f16x8 *)&vt[w][dt * 16 + r16][g4 * 8], o[dt]);
+        __builtin_amdgcn_wave_barrier();
+    }
+    // wave states -> LDS, merged in wave order
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int h = 4 * g4 + j;
+        if (r16 == 0) { wm[w][h] = mrow[j]; wl[w][h] = lrow[j]; }
+        if (h < G && h < 8) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) wo[w][h][dt * 16 + r16] = o[dt][j];
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * HD; i += blockDim.x) {
+        const int h = i / HD, d = i - h * HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w2 = 0; w2 < DEC_WAVES; ++w2) if (wl[w2][h] > 0.f) M = fmaxf(M, wm[w2][h]);
+        float L = 0.f, acc = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < DEC_WAVES; ++w2) {
+            if (wl[w2][h] > 0.f) {
+                const float f = expf(wm[w2][h] - M);
+                L += f * wl[w2][h];
+                acc += f * wo[w2][h][d];
+            }
+        }
+        out[(size_t)b * ldo + (kvh * G + h) * HD + d] = (f16)(acc / L);
+    }
+}
+
 // out[b][h*HD + d] (fp16) = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}; one block (HD threads) per
 // (head, column), chunk statistics loaded in parallel.
 __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const int *col_nchunk, int NH, int HD,

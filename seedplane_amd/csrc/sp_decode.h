@@ -126,19 +126,29 @@ __device__ __forceinline__ bool ll_gather(unsigned *err, const u64 *src, int n, 
 }
 
 // ----------------------------------------------------------------------------------------------- shared memory
-constexpr int MAX_H = 4096, MAX_K = 16384, STAGE = 8192, MAX_G = 8, MAX_CHUNKS = 64;
+constexpr int MAX_H = 2048, MAX_K = 9216, STAGE = 4608, MAX_G = 8, MAX_CHUNKS = 64;
+constexpr int RING_BYTES = 96 * 1024, RING_WAVE = RING_BYTES / NWV;
+struct AttnLds {
+    __align__(16) f16 qh[16][128 + 8];         // scaled, rotated queries of the group (rows >= G zero)
+    __align__(16) f16 k_s[ATT_CH][128 + 8];   // keys of the chunk, row-major (B operand of S = Q K^T)
+    __align__(16) f16 vt_s[128][ATT_CH + 8];  // values of the chunk, transposed (B operand of O = P V)
+    __align__(16) f16 p_s[16][ATT_CH + 8];    // softmax numerators, row = query head (A operand of O = P V)
+    float tmp[10 * 128];                      // q / k / v rows of the group (+ bias) before RoPE
+    float rc[64], rs[64];                     // RoPE cos / sin of this position
+    float amax[NWV + 1][16], asum[NWV][16];   // per-wave row maxima / sums of the chunk softmax
+    __align__(16) f16 kn[128], vn[128];
+};
 struct Smem {
     float x[MAX_H];             // residual stream (private copy)
     __align__(16) f16 a[MAX_K]; // A operand of the current GEMV (fp16, absolute k index, zero past K)
     unsigned stage[STAGE];      // gathered payloads
     f32x4 red[NWV * 2 * 64];    // wave partials of one GEMV item
-    float q[MAX_G][128];        // attention: scaled, rotated queries of the group
-    __align__(16) f16 kn[128], vn[128];
-    __align__(16) f16 k_s[ATT_CH][128 + 8];   // keys of the chunk, row-major (B operand of S = Q K^T)
-    __align__(16) f16 vt_s[128][ATT_CH + 8];  // values of the chunk, transposed (B operand of O = P V)
-    __align__(16) f16 p_s[16][ATT_CH + 8];    // softmax numerators, row = query head (A operand of O = P V)
     float w[MAX_CHUNKS];
     float redf[16];
+    union {
+        AttnLds att;                                   // attention items
+        __align__(16) unsigned char ring[RING_BYTES];  // weight tiles prefetched by DMA, one region per wave
+    } u;
 };
 __shared__ Smem S;
 
@@ -174,12 +184,12 @@ struct WaveJob {
 };
 
 template <int FMT, int RG>
-__device__ __forceinline__ void tiles_load(const Mat &m, const WaveJob &j, int round, WaveTiles<FMT, RG> &t) {
+__device__ __forceinline__ void tiles_load(const Mat &m, const WaveJob &j, int first, int round, WaveTiles<FMT, RG> &t) {
     constexpr int M = MaxT<FMT, RG>::V;
     const int lane = threadIdx.x & 63, r = lane & 15;
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        const int idx = round * M + i;
+        const int idx = first + round * M + i;
         if (idx >= j.count) break;
         const int kt = j.kt0 + idx * j.nsub;
 #pragma unroll
@@ -193,73 +203,156 @@ __device__ __forceinline__ void tiles_load(const Mat &m, const WaveJob &j, int r
 }
 
 template <int FMT, int RG>
-__device__ __forceinline__ void tiles_mac(const WaveJob &j, int round, const WaveTiles<FMT, RG> &t, f32x4 acc[RG]) {
-    constexpr int M = MaxT<FMT, RG>::V, KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
-    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-    const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    const f16x8 ones8 = (f16x8){1, 1, 1, 1, 1, 1, 1, 1};
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-        const int idx = round * M + i;
-        if (idx >= j.count) break;
-        const int kt = j.kt0 + idx * j.nsub;
-#pragma unroll
-        for (int st = 0; st < ST; ++st) {
-            const f16x8 xa = r == 0 ? *(const f16x8 *)(S.a + kt * KT + st * 32 + 8 * g) : zero8;
-            f32x4 xs = (f32x4){0.f, 0.f, 0.f, 0.f};
-            if constexpr (FMT == 3) xs = mfma16(xa, ones8, xs);
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg) {
-                const f16x8 b = unpack_step<FMT>(t.wt[i][rg], st);
-                if constexpr (FMT == 1) {
-                    acc[rg] = mfma16(xa, b, acc[rg]);
-                } else if constexpr (FMT == 2) {
-                    const uint32_t d = t.s8[i][rg];
-                    const float scale = (float)__builtin_bit_cast(f16, (uint16_t)(st == 0 ? (d & 0xffffu) : (d >> 16)));
-                    acc[rg] += scale * mfma16(xa, b, (f32x4){0.f, 0.f, 0.f, 0.f});
-                } else {
-                    uint32_t d;
-                    if (st == 0) d = t.s4[i][rg].x; else if (st == 1) d = t.s4[i][rg].y; else if (st == 2) d = t.s4[i][rg].z; else d = t.s4[i][rg].w;
-                    const float scale = (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
-                    const float zero = (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
-                    const f32x4 dd = mfma16(xa, b, (f32x4){0.f, 0.f, 0.f, 0.f});
-                    acc[rg] += scale * (dd - zero * xs);
-                }
-            }
-        }
-    }
-}
+__device__ __forceinline__ void tiles_mac(const WaveJob &j, int first, int round, const WaveTiles<FMT, RG> &t, f32x4 acc[RG]);
 
 // Number of items block b holds in a phase of `items` items.
 __device__ __forceinline__ int my_items(int items) {
     return items > (int)blockIdx.x ? (items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
 }
 
-// One batch of a block's items in a GEMV phase (see above): the wave's job and its prefetched tiles.
+// ------------------------------------------------------------------------------------------ DMA ring
+// Weight tiles can be copied straight into LDS (global_load_lds_dwordx4: lane l's 16 bytes land at the wave's LDS
+// base + 16 l, no registers involved) well before a phase's input arrives: each wave owns RING_WAVE bytes and
+// prefetches the first CAP tiles (or gate/up pairs) of its job in the next phase.
+template <int FMT> struct SideBytes { static constexpr int V = FMT == 1 ? 0 : FMT == 2 ? 64 : 256; };
+template <int FMT, int RG> struct Ring {
+    static constexpr int CAP = RING_WAVE / (RG * (TILE_BYTES + SideBytes<FMT>::V));
+    static constexpr int SIDE = CAP * RG * TILE_BYTES;     // offset of the side data inside a wave region
+};
+
+__device__ __forceinline__ void dma16(const void *g, unsigned char *l) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *g, unsigned char *l) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)l, 4, 0, 0);
+}
+
+template <int FMT, int RG>
+__device__ __forceinline__ void ring_issue(const Mat &m, const WaveJob &j, int npf) {
+    unsigned char *base = S.u.ring + (threadIdx.x >> 6) * RING_WAVE;
+    const int lane = threadIdx.x & 63;
+    for (int idx = 0; idx < npf; ++idx) {
+        const int kt = j.kt0 + idx * j.nsub;
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            const size_t tile = (size_t)(j.unit * RG + rg) * m.nkt + kt;
+            const int slot = idx * RG + rg;
+            dma16(m.w + tile * TILE_BYTES + lane * 16, base + slot * TILE_BYTES);
+            if constexpr (FMT == 2) { if (lane < 16) dma4(m.sz + tile * 32 + lane * 2, base + Ring<FMT, RG>::SIDE + slot * 64); }
+            if constexpr (FMT == 3) { if (lane < 16) dma16(m.sz + tile * 128 + lane * 8, base + Ring<FMT, RG>::SIDE + slot * 256); }
+        }
+    }
+}
+
+// One tile (or gate/up pair) k-tile kt: codes wt[rg], side data s8 / s4, A fragments from S.a.
+template <int FMT, int RG>
+__device__ __forceinline__ void mac_tile(int kt, const u32x4 *wt, const uint32_t *s8, const u32x4 *s4, f32x4 acc[RG]) {
+    constexpr int KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    const f16x8 ones8 = (f16x8){1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+    for (int st = 0; st < ST; ++st) {
+        const f16x8 xa = r == 0 ? *(const f16x8 *)(S.a + kt * KT + st * 32 + 8 * g) : zero8;
+        f32x4 xs = (f32x4){0.f, 0.f, 0.f, 0.f};
+        if constexpr (FMT == 3) xs = mfma16(xa, ones8, xs);
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            const f16x8 b = unpack_step<FMT>(wt[rg], st);
+            if constexpr (FMT == 1) {
+                acc[rg] = mfma16(xa, b, acc[rg]);
+            } else if constexpr (FMT == 2) {
+                const uint32_t d = s8[rg];
+                const float scale = (float)__builtin_bit_cast(f16, (uint16_t)(st == 0 ? (d & 0xffffu) : (d >> 16)));
+                acc[rg] += scale * mfma16(xa, b, (f32x4){0.f, 0.f, 0.f, 0.f});
+            } else {
+                uint32_t d;
+                if (st == 0) d = s4[rg].x; else if (st == 1) d = s4[rg].y; else if (st == 2) d = s4[rg].z; else d = s4[rg].w;
+                const float scale = (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
+                const float zero = (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
+                const f32x4 dd = mfma16(xa, b, (f32x4){0.f, 0.f, 0.f, 0.f});
+                acc[rg] += scale * (dd - zero * xs);
+            }
+        }
+    }
+}
+
+template <int FMT, int RG>
+__device__ __forceinline__ void ring_mac(const WaveJob &j, int npf, f32x4 acc[RG]) {
+    const unsigned char *base = S.u.ring + (threadIdx.x >> 6) * RING_WAVE;
+    const int lane = threadIdx.x & 63, r = lane & 15;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");      // this wave's DMA copies have landed
+    for (int idx = 0; idx < npf; ++idx) {
+        u32x4 wt[RG], s4[RG];
+        uint32_t s8[RG];
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            const int slot = idx * RG + rg;
+            wt[rg] = *(const u32x4 *)(base + slot * TILE_BYTES + lane * 16);
+            if constexpr (FMT == 2) s8[rg] = *(const uint32_t *)(base + Ring<FMT, RG>::SIDE + slot * 64 + r * 4);
+            if constexpr (FMT == 3) s4[rg] = *(const u32x4 *)(base + Ring<FMT, RG>::SIDE + slot * 256 + r * 16);
+        }
+        mac_tile<FMT, RG>(j.kt0 + idx * j.nsub, wt, s8, s4, acc);
+    }
+}
+
+template <int FMT, int RG>
+__device__ __forceinline__ void tiles_mac(const WaveJob &j, int first, int round, const WaveTiles<FMT, RG> &t, f32x4 acc[RG]) {
+    constexpr int M = MaxT<FMT, RG>::V;
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int idx = first + round * M + i;
+        if (idx >= j.count) break;
+        mac_tile<FMT, RG>(j.kt0 + idx * j.nsub, t.wt[i], t.s8[i], t.s4[i], acc);
+    }
+}
+
+// One batch of a block's items in a GEMV phase: the wave's job, how many of its tiles sit in the ring, and the
+// register-prefetched first round of the rest.
 template <int FMT, int RG>
 struct Phase {
     WaveJob j;
     WaveTiles<FMT, RG> t;
-    int nb;                                   // items in this batch
+    int nb, npf;
 };
 
-// Sets up batch b0 of the block's `mine` items and issues the first round of weight loads.
+// Wave job for batch b0 of the block's `mine` items (see the work decomposition above).
 template <int FMT, int RG>
-__device__ __forceinline__ void phase_load(const Mat &m, int nsplit, int b0, int mine, Phase<FMT, RG> &p) {
+__device__ __forceinline__ WaveJob phase_job(const Mat &m, int nsplit, int b0, int mine, int &nb) {
     const int wv = threadIdx.x >> 6;
-    p.nb = min(NWV, mine - b0);
-    const int il = wv % p.nb, sub = wv / p.nb, nsub = (NWV - il + p.nb - 1) / p.nb;
+    nb = min(NWV, mine - b0);
+    const int il = wv % nb, sub = wv / nb, nsub = (NWV - il + nb - 1) / nb;
     const int it = (int)blockIdx.x + (b0 + il) * (int)gridDim.x;
-    p.j.unit = it / nsplit; p.j.sp = it - p.j.unit * nsplit;
-    const int k0 = (int)((long)m.nkt * p.j.sp / nsplit), k1 = (int)((long)m.nkt * (p.j.sp + 1) / nsplit);
-    p.j.kt0 = k0 + sub; p.j.nsub = nsub;
-    p.j.count = k1 - k0 > sub ? (k1 - k0 - sub + nsub - 1) / nsub : 0;
-    tiles_load<FMT, RG>(m, p.j, 0, p.t);
+    WaveJob j;
+    j.unit = it / nsplit; j.sp = it - j.unit * nsplit;
+    const int k0 = (int)((long)m.nkt * j.sp / nsplit), k1 = (int)((long)m.nkt * (j.sp + 1) / nsplit);
+    j.kt0 = k0 + sub; j.nsub = nsub;
+    j.count = k1 - k0 > sub ? (k1 - k0 - sub + nsub - 1) / nsub : 0;
+    return j;
 }
 
-// Multiply-accumulates the batch against S.a and reduces every item over its waves.  Rounds of M tiles are software
-// pipelined: round r + 1 is loaded into the second register set before round r is consumed.  Returns true in
-// lanes 0..15 of the wave that reduced an item; out[rg] = row unit * 16 + lane.
+// DMA-prefetch this block's first batch of a phase into the ring (call when the ring is free).
+template <int FMT, int RG>
+__device__ __forceinline__ void phase_prefetch(const Mat &m, int nsplit) {
+    const int mine = my_items(m.groups * nsplit);
+    if (mine == 0) return;
+    int nb;
+    const WaveJob j = phase_job<FMT, RG>(m, nsplit, 0, mine, nb);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");    // earlier LDS reads of the ring are complete
+    ring_issue<FMT, RG>(m, j, min(j.count, Ring<FMT, RG>::CAP));
+}
+
+// Sets up batch b0 and issues the register loads of the first round past the ring-resident tiles.
+template <int FMT, int RG>
+__device__ __forceinline__ void phase_load(const Mat &m, int nsplit, int b0, int mine, bool prefetched, Phase<FMT, RG> &p) {
+    p.j = phase_job<FMT, RG>(m, nsplit, b0, mine, p.nb);
+    p.npf = prefetched && b0 == 0 ? min(p.j.count, Ring<FMT, RG>::CAP) : 0;
+    tiles_load<FMT, RG>(m, p.j, p.npf, 0, p.t);
+}
+
+// Multiply-accumulates the batch against S.a -- ring tiles first, then rounds of M register tiles (software
+// pipelined over two register sets) -- and reduces every item over its waves.  Returns true in lanes 0..15 of the
+// wave that reduced an item; out[rg] = row unit * 16 + lane.
 template <int FMT, int RG>
 __device__ __forceinline__ bool phase_finish(const Mat &m, Phase<FMT, RG> &p, float out[RG]) {
     constexpr int M = MaxT<FMT, RG>::V;
@@ -267,18 +360,23 @@ __device__ __forceinline__ bool phase_finish(const Mat &m, Phase<FMT, RG> &p, fl
     f32x4 acc[RG];
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) acc[rg] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const int rounds = (p.j.count + M - 1) / M;
+    if (RG == 2) MK_TRACE_ATT(6);
+    if (p.npf > 0) ring_mac<FMT, RG>(p.j, p.npf, acc);
+    if (RG == 2) MK_TRACE_ATT(7);
+    const int rounds = (p.j.count - p.npf + M - 1) / M;
     WaveTiles<FMT, RG> t1;
     for (int r = 0; r < rounds; r += 2) {
-        if (r + 1 < rounds) tiles_load<FMT, RG>(m, p.j, r + 1, t1);
-        tiles_mac<FMT, RG>(p.j, r, p.t, acc);
-        if (r + 2 < rounds) tiles_load<FMT, RG>(m, p.j, r + 2, p.t);
-        if (r + 1 < rounds) tiles_mac<FMT, RG>(p.j, r + 1, t1, acc);
+        if (r + 1 < rounds) tiles_load<FMT, RG>(m, p.j, p.npf, r + 1, t1);
+        tiles_mac<FMT, RG>(p.j, p.npf, r, p.t, acc);
+        if (r + 2 < rounds) tiles_load<FMT, RG>(m, p.j, p.npf, r + 2, p.t);
+        if (r + 1 < rounds) tiles_mac<FMT, RG>(p.j, p.npf, r + 1, t1, acc);
     }
+    if (RG == 2) MK_TRACE_ATT(8);
     __syncthreads();                          // the previous batch's readers of S.red are done
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) S.red[(wv * RG + rg) * 64 + lane] = acc[rg];
     __syncthreads();
+    if (RG == 2) MK_TRACE_ATT(9);
     if (wv >= p.nb) return false;
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {         // wave il reduces item il over its waves il, il + nb, ...
@@ -319,10 +417,12 @@ __device__ __forceinline__ size_t qkv_pos(int row, int sp, int nsplit, int NH, i
     return ((size_t)g * nsplit + sp) * (G + 2) * HD + off;
 }
 
-// Attention item (kv head g, chunk c of ATT_CH visible keys) of one layer.  The chunk's cached keys / values are
-// loaded before the q / k / v partials are awaited; the new key / value (last visible position) come from the
-// partials (+ bias, RoPE) and the item owning the last chunk writes them to their slot.  Output: {m, l, acc[HD]}
-// per query head of the group as LL words.
+// Attention item (kv head g, chunk c of ATT_CH visible keys) of one layer.  Everything that does not depend on
+// this step's q / k / v -- the chunk's cached keys / values into LDS (values transposed), the qkv bias, the RoPE
+// cos / sin of this position -- is done before the q / k / v partials are awaited.  The new key / value (last
+// visible position) come from the partials (+ bias, RoPE); the item owning the last chunk writes them to their
+// slot.  S = Q K^T and O = P V run on MFMA (rows = the group's query heads), one key tile / two dim tiles per wave.
+// Output: {m, l, acc[HD]} per query head of the group as LL words.
 template <int HD>
 __device__ __forceinline__ bool attn_item(const AttnCtx a, const LayerW &W, u64 *R, unsigned tg, const sp_token &t,
                                           int g, int c, int nch) {
@@ -332,8 +432,12 @@ __device__ __forceinline__ bool attn_item(const AttnCtx a, const LayerW &W, u64 
     const int nlin = t.ctx_hi - t.ctx_lo + 1;
     const int v0 = c * ATT_CH, cnt = min(ATT_CH, nlin - v0);
     const size_t head_base = ((size_t)t.seq * NKV + g) * a.n_slots;
-    constexpr int CPR = HD / 8, PER = (ATT_CH * CPR + NT - 1) / NT;   // 16-byte chunks per thread (K and V each)
+    constexpr int HALF = HD / 2, CPR = HD / 8, PER = (ATT_CH * CPR + NT - 1) / NT;
+    constexpr int NB_PER = (10 * HD + NT - 1) / NT;               // bias values per thread ((G + 2) * HD <= 10 HD)
+    const int qrow0 = g * G * HD, krow0 = NH * HD + g * HD, vrow0 = (NH + NKV) * HD + g * HD;
+    // ---- independent of this step: K / V chunk, bias, rope table
     f16x8 kr[PER], vr[PER];
+    float bias[NB_PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int e = threadIdx.x + i * NT, jr = e / CPR, ch = e - jr * CPR;
@@ -344,116 +448,128 @@ __device__ __forceinline__ bool attn_item(const AttnCtx a, const LayerW &W, u64 
             vr[i] = *(const f16x8 *)(W.vc + off);
         }
     }
-    MK_TRACE_ATT(0);
-    const int nw = a.S1 * (G + 2) * HD;
-    if (!ll_gather(a.err, R + a.lw_qkv + (size_t)g * nw, nw, tg | 1, s.stage)) return false;
-    MK_TRACE_ATT(1);
-    const int qrow0 = g * G * HD, krow0 = NH * HD + g * HD, vrow0 = (NH + NKV) * HD + g * HD;
-    float *tmp = (float *)s.k_s;              // (G + 2) * HD floats; the K chunk overwrites it below
-    for (int i = threadIdx.x; i < (G + 2) * HD; i += NT) {
-        float v = __uint_as_float(s.stage[i]);
-        for (int sp = 1; sp < a.S1; ++sp) v += __uint_as_float(s.stage[sp * (G + 2) * HD + i]);
-        const int row = i < G * HD ? qrow0 + i : (i < (G + 1) * HD ? krow0 + i - G * HD : vrow0 + i - (G + 1) * HD);
-        tmp[i] = v + W.qkv_b[row];
+#pragma unroll
+    for (int i = 0; i < NB_PER; ++i) {
+        const int e = threadIdx.x + i * NT;
+        const int row = e < G * HD ? qrow0 + e : (e < (G + 1) * HD ? krow0 + e - G * HD : vrow0 + e - (G + 1) * HD);
+        bias[i] = e < (G + 2) * HD ? W.qkv_b[row] : 0.f;
     }
-    __syncthreads();
-    // RoPE (non-interleaved halves, phase = float(pos) * inv_freq) on the G query heads and the key
-    MK_TRACE_ATT(2);
-    const float fpos = (float)t.pos;
-    constexpr int HALF = HD / 2;
-    for (int i = threadIdx.x; i < (G + 1) * HALF; i += NT) {
-        const int head = i / HALF, j = i - head * HALF;
-        const float ph = fpos * a.inv_freq[j];
-        const float cs = cosf(ph), sn = sinf(ph);
-        const float x1 = tmp[head * HD + j], x2 = tmp[head * HD + j + HALF];
-        const float o1 = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(-x2, sn));
-        const float o2 = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
-        if (head < G) { s.q[head][j] = o1 * a.scale; s.q[head][j + HALF] = o2 * a.scale; }
-        else { s.kn[j] = (f16)o1; s.kn[j + HALF] = (f16)o2; }
+    if ((int)threadIdx.x < HALF) {
+        const float ph = (float)t.pos * a.inv_freq[threadIdx.x];
+        s.u.att.rc[threadIdx.x] = cosf(ph);
+        s.u.att.rs[threadIdx.x] = sinf(ph);
     }
-    for (int i = threadIdx.x; i < HD; i += NT) s.vn[i] = (f16)tmp[(G + 1) * HD + i];
-    __syncthreads();
-    MK_TRACE_ATT(3);
-    if (c == nch - 1) {                           // this item owns the new position: write its key / value
-        for (int i = threadIdx.x; i < HD; i += NT) {
-            W.kc[(head_base + t.slot) * HD + i] = s.kn[i];
-            W.vc[(head_base + t.slot) * HD + i] = s.vn[i];
-        }
-    }
+    const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int e = threadIdx.x + i * NT, jr = e / CPR, ch = e - jr * CPR;
         if (e < ATT_CH * CPR) {
-            const bool live = jr < cnt, fresh = live && t.ctx_lo + v0 + jr == t.ctx_hi;
-            const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-            const f16x8 kk = fresh ? *(const f16x8 *)&s.kn[ch * 8] : (live ? kr[i] : zero8);
-            const f16x8 vv = fresh ? *(const f16x8 *)&s.vn[ch * 8] : (live ? vr[i] : zero8);
-            *(f16x8 *)&s.k_s[jr][ch * 8] = kk;
+            const bool live = jr < cnt && t.ctx_lo + v0 + jr != t.ctx_hi;   // the new key is filled in below
+            const f16x8 kk = live ? kr[i] : zero8, vv = live ? vr[i] : zero8;
+            *(f16x8 *)&s.u.att.k_s[jr][ch * 8] = kk;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) s.vt_s[ch * 8 + q][jr] = vv[q];
+            for (int q = 0; q < 8; ++q) s.u.att.vt_s[ch * 8 + q][jr] = vv[q];
+        }
+    }
+    MK_TRACE_ATT(0);
+    // ---- this step's q / k / v partials
+    const int nw = a.S1 * (G + 2) * HD;
+    if (!ll_gather(a.err, R + a.lw_qkv + (size_t)g * nw, nw, tg | 1, s.stage)) return false;
+    MK_TRACE_ATT(1);
+    float *tmp = s.u.att.tmp;
+#pragma unroll
+    for (int i = 0; i < NB_PER; ++i) {
+        const int e = threadIdx.x + i * NT;
+        if (e < (G + 2) * HD) {
+            float v = __uint_as_float(s.stage[e]);
+            for (int sp = 1; sp < a.S1; ++sp) v += __uint_as_float(s.stage[sp * (G + 2) * HD + e]);
+            tmp[e] = v + bias[i];
         }
     }
     __syncthreads();
-    MK_TRACE_ATT(4);
-    // wave 0: S = Q K^T on MFMA (rows = the group's query heads, columns = the chunk's keys), chunk-local softmax,
-    // O = P V on MFMA.  Lane l holds D rows 4 (l / 16) + j, column l % 16.
-    if (wv == 0) {
-        constexpr int ST = HD / 32, NKT = ATT_CH / 16, NDT = HD / 16;
-        const int r16 = lane & 15, g4 = lane >> 4;
-        f16x8 qa[ST];
-#pragma unroll
-        for (int st = 0; st < ST; ++st) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qa[st][e] = r16 < G ? (f16)s.q[r16][st * 32 + g4 * 8 + e] : (f16)0.f;
+    MK_TRACE_ATT(2);
+    // RoPE (non-interleaved halves) on the G query heads (-> fp16, scaled) and the key; the value as is
+    for (int i = threadIdx.x; i < (G + 1) * HALF; i += NT) {
+        const int head = i / HALF, j = i - head * HALF;
+        const float cs = s.u.att.rc[j], sn = s.u.att.rs[j];
+        const float x1 = tmp[head * HD + j], x2 = tmp[head * HD + j + HALF];
+        const float o1 = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(-x2, sn));
+        const float o2 = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
+        if (head < G) { s.u.att.qh[head][j] = (f16)(o1 * a.scale); s.u.att.qh[head][j + HALF] = (f16)(o2 * a.scale); }
+        else { s.u.att.kn[j] = (f16)o1; s.u.att.kn[j + HALF] = (f16)o2; }
+    }
+    for (int i = threadIdx.x; i < HD; i += NT) s.u.att.vn[i] = (f16)tmp[(G + 1) * HD + i];
+    for (int i = threadIdx.x; i < (16 - G) * HD; i += NT) s.u.att.qh[G + i / HD][i % HD] = (f16)0.f;
+    __syncthreads();
+    const int jn = t.ctx_hi - t.ctx_lo - v0;      // row of the new key in this chunk (if any)
+    if (jn >= 0 && jn < cnt) {
+        for (int i = threadIdx.x; i < HD; i += NT) { s.u.att.k_s[jn][i] = s.u.att.kn[i]; s.u.att.vt_s[i][jn] = s.u.att.vn[i]; }
+    }
+    if (c == nch - 1) {                           // this item owns the new position: write its key / value
+        for (int i = threadIdx.x; i < HD; i += NT) {
+            W.kc[(head_base + t.slot) * HD + i] = s.u.att.kn[i];
+            W.vc[(head_base + t.slot) * HD + i] = s.u.att.vn[i];
         }
-        f32x4 sc[NKT];
+    }
+    __syncthreads();
+    MK_TRACE_ATT(3);
+    // ---- S = Q K^T: wave w takes key tile w (16 keys); lane l holds rows 4 (l / 16) + j, key l % 16
+    constexpr int ST = HD / 32, NDT = HD / 16;
+    static_assert(ATT_CH == 16 * NWV, "one key tile per wave");
+    const int r16 = lane & 15, g4 = lane >> 4;
+    f32x4 sc = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-            sc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int st = 0; st < ST; ++st)
+        sc = mfma16(*(const f16x8 *)&s.u.att.qh[r16][st * 32 + g4 * 8], *(const f16x8 *)&s.u.att.k_s[wv * 16 + r16][st * 32 + g4 * 8], sc);
+    const bool live = wv * 16 + r16 < cnt;
 #pragma unroll
-            for (int st = 0; st < ST; ++st)
-                sc[kt] = mfma16(qa[st], *(const f16x8 *)&s.k_s[kt * 16 + r16][st * 32 + g4 * 8], sc[kt]);
-        }
-        float mrow[4], lrow[4];
+    for (int j = 0; j < 4; ++j) {                 // per-row max over this wave's 16 keys
+        float m = live ? sc[j] : -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float m = -INFINITY;
+        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, SP_WAVE));
+        if (r16 == 0) s.u.att.amax[wv][4 * g4 + j] = m;
+    }
+    __syncthreads();
+    float lsum[4];
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt) m = kt * 16 + r16 < cnt ? fmaxf(m, sc[kt][j]) : m;
+    for (int j = 0; j < 4; ++j) {
+        const int h = 4 * g4 + j;
+        float M = s.u.att.amax[0][h];
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, SP_WAVE));
-            float l = 0.f;
+        for (int w2 = 1; w2 < NWV; ++w2) M = fmaxf(M, s.u.att.amax[w2][h]);
+        const float pe = live ? expf(sc[j] - M) : 0.f;
+        s.u.att.p_s[h][wv * 16 + r16] = (f16)pe;
+        float l = pe;
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt) {
-                const float pe = kt * 16 + r16 < cnt ? expf(sc[kt][j] - m) : 0.f;
-                s.p_s[4 * g4 + j][kt * 16 + r16] = (f16)pe;
-                l += pe;
-            }
+        for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, SP_WAVE);
+        lsum[j] = l;
+        if (wv == 0 && r16 == 0) s.u.att.amax[NWV][h] = M;
+    }
+    if (r16 == 0) {
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, SP_WAVE);
-            mrow[j] = m; lrow[j] = l;
-        }
-        __builtin_amdgcn_wave_barrier();
-        f32x4 ov[NDT];
+        for (int j = 0; j < 4; ++j) s.u.att.asum[wv][4 * g4 + j] = lsum[j];
+    }
+    __syncthreads();
+    // ---- O = P V: wave w takes dim tiles w, w + NWV, ...
+    u64 *P0 = R + a.lw_part;
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) ov[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int dt = wv; dt < NDT; dt += NWV) {
+        f32x4 ov = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < ATT_CH / 32; ++ks) {
-            const f16x8 pa = *(const f16x8 *)&s.p_s[r16][ks * 32 + g4 * 8];
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-                ov[dt] = mfma16(pa, *(const f16x8 *)&s.vt_s[dt * 16 + r16][ks * 32 + g4 * 8], ov[dt]);
-        }
+        for (int ks = 0; ks < ATT_CH / 32; ++ks)
+            ov = mfma16(*(const f16x8 *)&s.u.att.p_s[r16][ks * 32 + g4 * 8], *(const f16x8 *)&s.u.att.vt_s[dt * 16 + r16][ks * 32 + g4 * 8], ov);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int h = 4 * g4 + j;
-            if (h < G) {
-                u64 *dst = R + a.lw_part + ((size_t)(g * G + h) * a.nchunk_max + c) * (HD + 2);
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) ll_put(dst + 2 + dt * 16 + r16, tg | 2, __float_as_uint(ov[dt][j]));
-                if (r16 == 0) { ll_put(dst, tg | 2, __float_as_uint(mrow[j])); ll_put(dst + 1, tg | 2, __float_as_uint(lrow[j])); }
-            }
+            if (h < G) ll_put(P0 + ((size_t)(g * G + h) * a.nchunk_max + c) * (HD + 2) + 2 + dt * 16 + r16, tg | 2, __float_as_uint(ov[j]));
         }
+    }
+    if (wv == 0 && lane < G) {                    // m and l of query head `lane` (l summed over waves in order)
+        float L = s.u.att.asum[0][lane];
+        for (int w2 = 1; w2 < NWV; ++w2) L += s.u.att.asum[w2][lane];
+        u64 *dst = P0 + ((size_t)(g * G + lane) * a.nchunk_max + c) * (HD + 2);
+        ll_put(dst, tg | 2, __float_as_uint(s.u.att.amax[NWV][lane]));
+        ll_put(dst + 1, tg | 2, __float_as_uint(L));
     }
     __syncthreads();
     MK_TRACE_ATT(5);
@@ -522,6 +638,7 @@ __global__ void __launch_bounds__(NT) k_decode(Args a) {
         __syncthreads();
     }
 
+    phase_prefetch<FMT, 1>(L > 0 ? a.layers[0].qkv : a.head, L > 0 ? S1 : 1);
     MK_TRACE(0);
     for (int l = 0; l <= L; ++l) {
         const int te = 1 + l * 12;                              // trace event base of this layer
@@ -539,7 +656,7 @@ __global__ void __launch_bounds__(NT) k_decode(Args a) {
             int bi = 0x7fffffff;
             for (int b0 = 0; b0 == 0 || b0 < mine; b0 += NWV) {
                 Phase<FMT, 1> p;
-                if (mine > 0) phase_load<FMT, 1>(m1, nsplit, b0, mine, p);
+                if (mine > 0) phase_load<FMT, 1>(m1, nsplit, b0, mine, true, p);
                 if (b0 == 0) {
                     MK_TRACE(te);
                     if (l > 0) {
@@ -596,6 +713,7 @@ __global__ void __launch_bounds__(NT) k_decode(Args a) {
         for (int it = blockIdx.x; it < NKV * nch; it += gridDim.x)
             if (!attn_item<HD>(ac, W, R, tg, t, it / nch, it % nch, nch)) return;
         MK_TRACE(te + 3);
+        phase_prefetch<FMT, 1>(W.o, S3);                       // the ring is free again: o_proj tiles
         for (int h = blockIdx.x; h < NH; h += gridDim.x)
             if (!combine_head<HD>(ac, R, tg, h, nch)) return;
         MK_TRACE(te + 4);
@@ -604,7 +722,7 @@ __global__ void __launch_bounds__(NT) k_decode(Args a) {
             const int mine = my_items(W.o.groups * S3);
             for (int b0 = 0; b0 < mine; b0 += NWV) {
                 Phase<FMT, 1> p;
-                phase_load<FMT, 1>(W.o, S3, b0, mine, p);
+                phase_load<FMT, 1>(W.o, S3, b0, mine, true, p);
                 if (b0 == 0) {
                     if (!ll_gather(err, R + lw_attn, NH * HD, tg | 3, S.stage)) return;
                     MK_TRACE(te + 5);
@@ -620,12 +738,13 @@ __global__ void __launch_bounds__(NT) k_decode(Args a) {
             }
         }
         // ---------------- P4: x += o partials; xn = norm(x); gate_up pairs -> act = SiLU(gate) * up (fp16)
+        phase_prefetch<FMT, 2>(W.gu, 1);
         MK_TRACE(te + 6);
         {
             const int mine = my_items(W.gu.groups);
             for (int b0 = 0; b0 == 0 || b0 < mine; b0 += NWV) {
                 Phase<FMT, 2> p;
-                if (mine > 0) phase_load<FMT, 2>(W.gu, 1, b0, mine, p);
+                if (mine > 0) phase_load<FMT, 2>(W.gu, 1, b0, mine, true, p);
                 if (b0 == 0) {
                     if (!ll_gather(err, R + lw_o, S3 * H, tg | 4, S.stage)) return;
                     MK_TRACE(te + 7);
@@ -644,6 +763,7 @@ __global__ void __launch_bounds__(NT) k_decode(Args a) {
             }
         }
         // ---------------- P5: down partials; the input is the act slice this block's items read
+        phase_prefetch<FMT, 1>(W.down, S5);
         MK_TRACE(te + 8);
         {
             const int mine = my_items(W.down.groups * S5);
@@ -655,7 +775,7 @@ __global__ void __launch_bounds__(NT) k_decode(Args a) {
             }
             for (int b0 = 0; b0 < mine; b0 += NWV) {
                 Phase<FMT, 1> p;
-                phase_load<FMT, 1>(W.down, S5, b0, mine, p);
+                phase_load<FMT, 1>(W.down, S5, b0, mine, true, p);
                 if (b0 == 0) {
                     if (!ll_gather(err, R + lw_act + kmin, min(I, kmax) - kmin, tg | 5, S.stage)) return;
                     MK_TRACE(te + 9);
@@ -670,6 +790,8 @@ __global__ void __launch_bounds__(NT) k_decode(Args a) {
                 }
             }
         }
+        // next layer's qkv tiles (or the LM head's) into the ring while the down partials travel
+        phase_prefetch<FMT, 1>(l + 1 < L ? a.layers[l + 1].qkv : a.head, l + 1 < L ? S1 : 1);
         MK_TRACE(te + 10);
     }
 }

@@ -232,6 +232,7 @@ struct sp_engine {
     // attention plan of one forward call: same-sequence column groups (multi-query kernel) or one block row per column
     struct AttnPlan {
         bool mq = false;
+        bool dec = false;        // every column a plain ring range of at most DEC_MAX_KEYS keys: k_attn_dec
         int ngroups = 0, nchunk = 1, splits = 1;
         std::vector<AttnGroup> groups;
         std::vector<int> colnc;
@@ -335,6 +336,10 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
         }
     }
     p.nchunk = graph ? max_nchunk : mx;
+    if (!p.mq && d.n_heads / d.n_kv_heads <= 8) {
+        p.dec = true;
+        for (int c = 0; c < n; ++c) p.dec = p.dec && t[c].tree_count == 0 && nlin_of(t[c]) <= DEC_MAX_KEYS;
+    }
     return p;
 }
 
@@ -484,21 +489,26 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
             dim3 agrid(nchunk, NKV, ap.ngroups * ap.splits);
             if (HD == 64) launch_attn_mq_hd<64>(G, agrid, st, am);
             else launch_attn_mq_hd<128>(G, agrid, st, am);
+        } else if (ap.dec) {
+            AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
+            if (HD == 64) hipLaunchKernelGGL(k_attn_dec<64>, dim3(NKV, n), dim3(64 * DEC_WAVES), 0, st, aa, attn, NH * HD);
+            else hipLaunchKernelGGL(k_attn_dec<128>, dim3(NKV, n), dim3(64 * DEC_WAVES), 0, st, aa, attn, NH * HD);
         } else {
             AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
             dim3 agrid(nchunk, NKV, n);
             if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
             else launch_attn_hd<128>(G, agrid, st, aa);
         }
-        hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn, NH * HD);
+        if (!ap.dec)
+            hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn, NH * HD);
         launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, st);
         hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, ly.post_norm, H, d.rms_eps, xn, H);
         launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, st);
         launch_gemv(ly.down, EPI_RESID, act, I, n, x, nullptr, H, nullptr, st);
     }
     if (logits_on) {
-        hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, final_norm, H, d.rms_eps, xn, H);
         const DevMat &hm = d.tied_head ? embed : head;
+        hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, final_norm, H, d.rms_eps, xn, H);
         launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, st);
         if (flags & SP_F_ARGMAX) {
             hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, n), dim3(256), 0, st, logits, d.vocab, d.vocab, am_v, am_i);
@@ -708,7 +718,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         HIPCHK(hipMemcpyAsync(e->dgroups, ap.groups.data(), ap.ngroups * sizeof(AttnGroup), hipMemcpyHostToDevice, e->stream));
         HIPCHK(hipMemcpyAsync(e->dcolnc, ap.colnc.data(), n * sizeof(int), hipMemcpyHostToDevice, e->stream));
         if (use_graph) {
-            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : -1);
+            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? -2 : -1));
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 // record on the private stream (the caller's may be the null stream, which cannot capture)
