@@ -39,54 +39,89 @@ __global__ void __launch_bounds__(256) k_embed(const uint8_t *w, const f16 *sz, 
 }
 
 // out[b][k] = fp16(x * rsqrt(mean(x^2) + eps) * w).  Replaces Qwen2Engine._norm (qwen_engine.py:90-92): the weight
-// multiply happens in fp32 before the cast.  One block per column, x read once into registers (H <= 16 * 256).
-constexpr int NORM_PER_THREAD = 16;
-__global__ void __launch_bounds__(256) k_rmsnorm(const float *x, int ldx, const float *w, int H, float eps, f16 *out,
-                                                 int ldo) {
+// multiply happens in fp32 before the cast.  One block of 1024 threads per column; every load (x, the weight and
+// the NP split-K slices) is issued before the first use.  With NP > 0 the residual update of a split-K GEMV is
+// completed first: x[b] += part[0][b] + ... + part[NP-1][b] (in slice order) and written back to x.
+constexpr int NORM_THREADS = 1024, NORM_PER_THREAD = 4;
+template <int NP>
+__global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, const float *part, size_t pstride,
+                                                          const float *w, int H, float eps, f16 *out, int ldo) {
     __shared__ float red[16];
     const int b = blockIdx.x;
-    const float *xr = x + (size_t)b * ldx;
-    float v[NORM_PER_THREAD];
-    float ss = 0.f;
+    float *xr = x + (size_t)b * ldx;
+    float v[NORM_PER_THREAD], wk[NORM_PER_THREAD], pv[NP > 0 ? NP : 1][NORM_PER_THREAD];
 #pragma unroll
     for (int i = 0; i < NORM_PER_THREAD; ++i) {
-        const int k = threadIdx.x + i * 256;
+        const int k = threadIdx.x + i * NORM_THREADS;
         v[i] = k < H ? xr[k] : 0.f;
-        ss += v[i] * v[i];
+        wk[i] = k < H ? w[k] : 0.f;
+#pragma unroll
+        for (int s = 0; s < NP; ++s) pv[s][i] = k < H ? part[(size_t)s * pstride + (size_t)b * ldx + k] : 0.f;
     }
+    if constexpr (NP > 0) {
+#pragma unroll
+        for (int i = 0; i < NORM_PER_THREAD; ++i) {
+            const int k = threadIdx.x + i * NORM_THREADS;
+#pragma unroll
+            for (int s = 0; s < NP; ++s) v[i] += pv[s][i];
+            if (k < H) xr[k] = v[i];
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NORM_PER_THREAD; ++i) ss += v[i] * v[i];
     ss = block_sum(ss, red);
     const float rs = 1.0f / sqrtf(ss / (float)H + eps);
 #pragma unroll
     for (int i = 0; i < NORM_PER_THREAD; ++i) {
-        const int k = threadIdx.x + i * 256;
-        if (k < H) out[(size_t)b * ldo + k] = (f16)((v[i] * rs) * w[k]);
+        const int k = threadIdx.x + i * NORM_THREADS;
+        if (k < H) out[(size_t)b * ldo + k] = (f16)((v[i] * rs) * wk[i]);
     }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 struct RopeArgs {
-    const float *qkv;       // [n][Nqkv] fp32 (bias already added)
+    const float *qkv;       // [n][Nqkv] fp32 (bias already added) when nparts == 0
     int Nqkv, NH, NKV, HD;
     const float *inv_freq;  // [HD/2]
     const sp_token *toks;
     float *q;               // [n][NH*HD] fp32, rotated
     f16 *kc, *vc;           // this layer's K/V: [seq][kvh][slot][HD]
     int n_slots;
+    const float *part;      // NP > 0: the projection is part[0] + ... + part[NP-1] + bias (slices [n][Nqkv])
+    size_t pstride;
+    const float *bias;
 };
+
+template <int NP>
+__device__ __forceinline__ float qkv_value(const RopeArgs &a, int b, int idx) {
+    if constexpr (NP == 0) {
+        return a.qkv[(size_t)b * a.Nqkv + idx];
+    } else {
+        const float *p = a.part + (size_t)b * a.Nqkv + idx;
+        float t[NP];
+#pragma unroll
+        for (int s = 0; s < NP; ++s) t[s] = p[(size_t)s * a.pstride];
+        float v = t[0];
+#pragma unroll
+        for (int s = 1; s < NP; ++s) v += t[s];
+        return v + a.bias[idx];
+    }
+}
 // Non-interleaved half rotation x*cos + rotate_half(x)*sin with phase = float(pos) * inv_freq (qwen_engine.py:94-103,
-// rope_kv.comp:1-32); K and V of every column are written to their slot.
-__global__ void __launch_bounds__(256) k_rope_kv(RopeArgs a) {
+// rope_kv.comp:1-32); K and V of every column are written to their slot.  One block of ROPE_THREADS per column.
+constexpr int ROPE_THREADS = 1024;
+template <int NP>
+__global__ void __launch_bounds__(ROPE_THREADS) k_rope_kv(RopeArgs a) {
     const int b = blockIdx.x;
     const sp_token t = a.toks[b];
     const int half = a.HD >> 1;
-    const float *src = a.qkv + (size_t)b * a.Nqkv;
     const float fpos = (float)t.pos;
     for (int idx = threadIdx.x; idx < (a.NH + a.NKV) * half; idx += blockDim.x) {
         const int head = idx / half, i = idx - head * half;
         const float ph = fpos * a.inv_freq[i];
         const float c = cosf(ph), s = sinf(ph);
-        const float *v = src + head * a.HD;
-        const float x1 = v[i], x2 = v[i + half];
+        const float x1 = qkv_value<NP>(a, b, head * a.HD + i), x2 = qkv_value<NP>(a, b, head * a.HD + i + half);
         const float o1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(-x2, s));
         const float o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
         if (head < a.NH) {
@@ -98,10 +133,10 @@ __global__ void __launch_bounds__(256) k_rope_kv(RopeArgs a) {
             k[i] = (f16)o1; k[i + half] = (f16)o2;
         }
     }
-    const float *vsrc = src + (a.NH + a.NKV) * a.HD;
+    const int v0 = (a.NH + a.NKV) * a.HD;
     for (int idx = threadIdx.x; idx < a.NKV * a.HD; idx += blockDim.x) {
         const int kvh = idx / a.HD, d = idx - kvh * a.HD;
-        a.vc[(((size_t)t.seq * a.NKV + kvh) * a.n_slots + t.slot) * a.HD + d] = (f16)vsrc[idx];
+        a.vc[(((size_t)t.seq * a.NKV + kvh) * a.n_slots + t.slot) * a.HD + d] = (f16)qkv_value<NP>(a, b, v0 + idx);
     }
 }
 

@@ -11,6 +11,7 @@
 #include <functional>
 #include <map>
 #include <tuple>
+#include <type_traits>
 #include <string>
 #include <utility>
 #include <vector>
@@ -87,57 +88,96 @@ DevMat upload_matrix(int fmt, int rows, int cols, const void *data, const void *
 
 // ------------------------------------------------------------------------------------------- GEMV planning/launch
 constexpr int GEMV_MAX_MT = 4;
+constexpr int GEMV_MAX_SLICES = 8;
+constexpr int GEMV_MAX_LDS = 64 * 1024;
 
 struct GemvPlan {
-    int units, nw, rg;
+    int units, nw, rg, r, s, kslice;
 };
 
-// One block per unit; waves per block chosen so that each wave owns at least ~2 k-tiles and small matrices still
-// spread over many waves (bs1 GEMVs are latency-bound).
-GemvPlan plan_gemv(const DevMat &m, int mt) {
+#ifdef SP_GEMV_TUNE
+// plan override for launch-shape sweeps (row groups per wave, waves per block, slices); 0 keeps the heuristic
+int g_tune[3] = {0, 0, 0};
+#endif
+
+// Launch shape of one GEMV (from launch-shape sweeps of the Qwen2-1.5B matrices at 1, 16, 33 and 64 columns).
+// Small-batch GEMVs are latency-bound: every wave issues its share of the weights in one or two batches, and the
+// grid must fit the chip at once (256 CUs).  Matrices with few row groups (qkv, o, down) are split along K into
+// slices that the consuming kernel adds up; the LM head and the wider column tiles give each wave two row groups
+// (R = 2), which doubles the loads in flight per wave and halves the activation reads per weight byte.
+GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok) {
     GemvPlan p;
     p.rg = m.paired ? 2 : 1;
     p.units = m.rows_pad / 16 / p.rg;
-    int nw = mt == 1 ? 16 : 8;
-    while (nw > 4 && m.nkt < 2 * nw) nw >>= 1;
-    if (p.units >= 4096 && nw > 8) nw = 8;
-    p.nw = nw;
+    const int tb = mt == 1 ? (m.fmt == 3 ? 2 : 4) : 2;
+    if (mt == 1) p.r = p.units >= 2048 && p.units % 2 == 0 ? 2 : 1;
+    else p.r = p.units % 2 == 0 && !(m.fmt == 3 && m.paired) ? 2 : 1;    // (the Q4 pair with R = 2 would spill)
+    int s = 1;
+    if (split_ok && !m.paired) {
+        s = std::max(1, 1024 / (p.units / p.r));
+        s = std::min(s, std::max(1, m.nkt / 2));
+        s = std::min(s, mt == 1 ? GEMV_MAX_SLICES : 4);
+    }
+#ifdef SP_GEMV_TUNE
+    if (g_tune[0] > 0 && p.units % g_tune[0] == 0) p.r = g_tune[0];
+    if (g_tune[2] > 0) s = (split_ok && !m.paired) ? std::min(g_tune[2], GEMV_MAX_SLICES) : 1;
+#endif
+    p.s = s;
+    p.kslice = (m.nkt + s - 1) / s;
+    int nw = mt == 1 ? std::min(4, (p.kslice + tb - 1) / tb) : std::min(8, p.kslice);
+#ifdef SP_GEMV_TUNE
+    if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 16 : 8);
+#endif
+    while (nw > 1 && (size_t)nw * p.r * p.rg * mt * 1024 > GEMV_MAX_LDS) --nw;
+    p.nw = std::max(1, nw);
     return p;
 }
 
-template <int FMT, int RG>
-void launch_gemv_rg(int mt, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+template <int FMT, int RG, int R>
+void launch_gemv_r(int mt, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
     switch (mt) {
-        case 1: hipLaunchKernelGGL((k_gemv<FMT, 1, RG>), grid, block, smem, st, a); break;
-        case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, RG>), grid, block, smem, st, a); break;
-        case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, RG>), grid, block, smem, st, a); break;
-        default: hipLaunchKernelGGL((k_gemv<FMT, 4, RG>), grid, block, smem, st, a); break;
+        case 1: hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R>), grid, block, smem, st, a); break;
+        case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, RG, R>), grid, block, smem, st, a); break;
+        case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, RG, R>), grid, block, smem, st, a); break;
+        default: hipLaunchKernelGGL((k_gemv<FMT, 4, RG, R>), grid, block, smem, st, a); break;
     }
 }
 template <int FMT>
-void launch_gemv_fmt(int mt, bool paired, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
-    if (paired) launch_gemv_rg<FMT, 2>(mt, grid, block, smem, st, a);
-    else launch_gemv_rg<FMT, 1>(mt, grid, block, smem, st, a);
+void launch_gemv_fmt(int mt, bool paired, int r, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+    if (paired) {
+        if (r == 2) launch_gemv_r<FMT, 2, 2>(mt, grid, block, smem, st, a);
+        else launch_gemv_r<FMT, 2, 1>(mt, grid, block, smem, st, a);
+    } else {
+        if (r == 2) launch_gemv_r<FMT, 1, 2>(mt, grid, block, smem, st, a);
+        else launch_gemv_r<FMT, 1, 1>(mt, grid, block, smem, st, a);
+    }
 }
 
-void launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, float *out_f32, f16 *out_f16, int ldo,
-                 const float *bias, hipStream_t st) {
+// Launches y = W x for mcols columns.  With `part` given (and a matrix that is not the SwiGLU pair) the plan may
+// split K: the kernel then writes raw slices to part[s][m][ldo] and the return value is the slice count that the
+// consumer must add (plus the bias, for EPI_STORE); otherwise the epilogue is applied and 0 is returned.
+int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, float *out_f32, f16 *out_f16, int ldo,
+                const float *bias, hipStream_t st, float *part = nullptr, size_t pstride = 0) {
     require(mcols >= 1 && mcols <= 16 * GEMV_MAX_MT, SP_EINVAL, "gemv columns out of range");
     require((epi == EPI_SILU) == m.paired, SP_EINVAL, "gemv epilogue does not match the matrix packing");
     const int mt = (mcols + 15) / 16;
-    GemvPlan p = plan_gemv(m, mt);
+    const GemvPlan p = plan_gemv(m, mt, part != nullptr);
+    require(p.units % p.r == 0 && p.s >= 1 && p.s <= GEMV_MAX_SLICES, SP_EINVAL, "gemv plan out of range");
     GemvArgs a;
     a.w = m.w; a.sz = m.sz; a.nkt = m.nkt; a.units = p.units;
     a.n_real = m.paired ? m.rows / 2 : m.rows;
     a.x = x; a.ldx = ldx; a.m = mcols;
     a.out_f32 = out_f32; a.out_f16 = out_f16; a.ldo = ldo; a.bias = bias; a.epi = epi;
-    dim3 grid(p.units), block(64 * p.nw);
-    const size_t smem = (size_t)p.nw * p.rg * mt * 64 * 16;
+    a.kslice = p.kslice; a.pstride = pstride;
+    if (p.s > 1) { a.epi = EPI_PART; a.out_f32 = part; a.bias = nullptr; }
+    dim3 grid(p.units / p.r, p.s), block(64 * p.nw);
+    const size_t smem = p.nw > 1 ? (size_t)p.nw * p.r * p.rg * mt * 64 * 16 : 0;
     switch (m.fmt) {
-        case 1: launch_gemv_fmt<1>(mt, m.paired, grid, block, smem, st, a); break;
-        case 2: launch_gemv_fmt<2>(mt, m.paired, grid, block, smem, st, a); break;
-        default: launch_gemv_fmt<3>(mt, m.paired, grid, block, smem, st, a); break;
+        case 1: launch_gemv_fmt<1>(mt, m.paired, p.r, grid, block, smem, st, a); break;
+        case 2: launch_gemv_fmt<2>(mt, m.paired, p.r, grid, block, smem, st, a); break;
+        default: launch_gemv_fmt<3>(mt, m.paired, p.r, grid, block, smem, st, a); break;
     }
+    return p.s > 1 ? p.s : 0;
 }
 
 // ------------------------------------------------------------------------------------------- attention dispatch
@@ -169,6 +209,34 @@ void launch_attn_mq_hd(int G, dim3 grid, hipStream_t st, const AttnMqArgs &a) {
     }
 }
 
+template <class F>
+void by_slices(int np, F &&f) {
+    switch (np) {
+        case 0: f(std::integral_constant<int, 0>()); break;
+        case 1: f(std::integral_constant<int, 1>()); break;
+        case 2: f(std::integral_constant<int, 2>()); break;
+        case 3: f(std::integral_constant<int, 3>()); break;
+        case 4: f(std::integral_constant<int, 4>()); break;
+        case 5: f(std::integral_constant<int, 5>()); break;
+        case 6: f(std::integral_constant<int, 6>()); break;
+        case 7: f(std::integral_constant<int, 7>()); break;
+        default: f(std::integral_constant<int, 8>()); break;
+    }
+}
+
+// RMSNorm of n columns of x, first adding np pending split-K residual slices
+void launch_rmsnorm(int n, float *x, int H, const float *part, int np, size_t ps, const float *w, float eps, f16 *out,
+                    hipStream_t st) {
+    by_slices(np, [&](auto c) {
+        hipLaunchKernelGGL((k_rmsnorm<decltype(c)::value>), dim3(n), dim3(NORM_THREADS), 0, st, x, H, part, ps, w, H, eps,
+                           out, H);
+    });
+}
+
+void launch_rope(int n, const RopeArgs &ra, int np, hipStream_t st) {
+    by_slices(np, [&](auto c) { hipLaunchKernelGGL((k_rope_kv<decltype(c)::value>), dim3(n), dim3(ROPE_THREADS), 0, st, ra); });
+}
+
 template <int FMT>
 void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x, hipStream_t st) {
     hipLaunchKernelGGL((k_embed<FMT>), dim3(n), dim3(256), 0, st, m.w, m.sz, m.nkt, toks, H, x, H);
@@ -197,6 +265,8 @@ struct sp_engine {
     // activations
     int Nqkv = 0, maxT = 0, max_nchunk = 0;
     float *x = nullptr, *qkv = nullptr, *q = nullptr, *logits = nullptr, *attn_part = nullptr;
+    float *gpart = nullptr;      // split-K GEMV slices [GEMV_MAX_SLICES][maxT][max(H, Nqkv)]
+    size_t gpart_stride = 0;
     f16 *xn = nullptr, *attn = nullptr, *act = nullptr;
     float *am_v = nullptr;
     int *am_i = nullptr, *am_out = nullptr;
@@ -254,7 +324,7 @@ void sp_engine::free_all() {
     layers.clear();
     embed.release(); head.release();
     dev_free(final_norm); dev_free(inv_freq);
-    for (void *p : {(void *)x, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)xn, (void *)attn,
+    for (void *p : {(void *)x, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)gpart, (void *)xn, (void *)attn,
                     (void *)act, (void *)am_v, (void *)am_i, (void *)am_out,
                     (void *)dtoks, (void *)dgroups, (void *)dcolnc, (void *)d_kl, (void *)d_vl, (void *)d_move})
         dev_free(p);
@@ -277,6 +347,8 @@ void sp_engine::alloc_activations() {
     x = dev_alloc<float>((size_t)maxT * H);
     xn = dev_alloc<f16>((size_t)maxT * kmax);
     qkv = dev_alloc<float>((size_t)maxT * Nqkv);
+    gpart_stride = (size_t)maxT * std::max(H, Nqkv);
+    gpart = dev_alloc<float>(GEMV_MAX_SLICES * gpart_stride);
     q = dev_alloc<float>((size_t)maxT * d.n_heads * d.head_dim);
     attn = dev_alloc<f16>((size_t)maxT * d.n_heads * d.head_dim);
     act = dev_alloc<f16>((size_t)maxT * I);
@@ -475,12 +547,14 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
         default: launch_embed<3>(embed, dtoks, n, H, x, st); break;
     }
     const bool logits_on = flags & SP_F_LOGITS;
+    const size_t ps = gpart_stride;
+    int pend = 0;     // residual slices of a split-K o / down GEMV waiting in gpart (added by the next RMSNorm)
     for (int l = 0; l < d.n_layers; ++l) {
         Layer &ly = layers[l];
-        hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, ly.in_norm, H, d.rms_eps, xn, H);
-        launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st);
-        RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots};
-        hipLaunchKernelGGL(k_rope_kv, dim3(n), dim3(256), 0, st, ra);
+        launch_rmsnorm(n, x, H, gpart, pend, ps, ly.in_norm, d.rms_eps, xn, st);
+        const int sq = launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, gpart, ps);
+        RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots, gpart, ps, ly.qkv_b};
+        launch_rope(n, ra, sq, st);
         if (l + 1 == d.n_layers && !logits_on) break;   // K/V-only: the last layer only needs its K/V
         const int G = NH / NKV;
         if (ap.mq) {
@@ -501,14 +575,14 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
         }
         if (!ap.dec)
             hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn, NH * HD);
-        launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, st);
-        hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, ly.post_norm, H, d.rms_eps, xn, H);
+        pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, st, gpart, ps);
+        launch_rmsnorm(n, x, H, gpart, pend, ps, ly.post_norm, d.rms_eps, xn, st);
         launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, st);
-        launch_gemv(ly.down, EPI_RESID, act, I, n, x, nullptr, H, nullptr, st);
+        pend = launch_gemv(ly.down, EPI_RESID, act, I, n, x, nullptr, H, nullptr, st, gpart, ps);
     }
     if (logits_on) {
         const DevMat &hm = d.tied_head ? embed : head;
-        hipLaunchKernelGGL(k_rmsnorm, dim3(n), dim3(256), 0, st, x, H, final_norm, H, d.rms_eps, xn, H);
+        launch_rmsnorm(n, x, H, gpart, pend, ps, final_norm, d.rms_eps, xn, st);
         launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, st);
         if (flags & SP_F_ARGMAX) {
             hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, n), dim3(256), 0, st, logits, d.vocab, d.vocab, am_v, am_i);
@@ -561,7 +635,7 @@ int sp_engine_create(const sp_model_desc *desc, sp_engine **out) {
         require(d.hidden % 128 == 0 && d.intermediate % 128 == 0 && (d.n_heads * d.head_dim) % 128 == 0, SP_EINVAL,
                 "hidden, intermediate and heads*head_dim must be multiples of 128");
         require(d.inv_freq != nullptr, SP_EINVAL, "inv_freq is NULL");
-        require(d.hidden <= NORM_PER_THREAD * 256, SP_EINVAL, "hidden must be <= 4096");
+        require(d.hidden <= NORM_PER_THREAD * NORM_THREADS, SP_EINVAL, "hidden must be <= 4096");
         e->d = d;
         e->d.inv_freq = nullptr;
         HIPCHK(hipGetDevice(&e->device));
@@ -757,6 +831,10 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
 
 int sp_engine_last_path(const sp_engine *e) { return e ? e->last_path : -1; }
 
+#ifdef SP_GEMV_TUNE
+void sp_debug_gemv_plan(int r, int nw, int s) { g_tune[0] = r; g_tune[1] = nw; g_tune[2] = s; }
+#endif
+
 #ifdef SP_DECODE_TRACE
 int sp_debug_decode_trace(unsigned long long *host) {
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(mk::trace_buf), sizeof(mk::trace_buf)) == hipSuccess ? SP_OK : SP_EHIP;
@@ -815,11 +893,11 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
         switch (kind) {
             case SP_T_QKV: m = &e->layers[cur].qkv;
                 launch = [&] { launch_gemv(e->layers[cur].qkv, EPI_STORE, e->xn, H, n_cols, e->qkv, nullptr, e->Nqkv,
-                                           e->layers[cur].qkv_b, st); next_layer(); };
+                                           e->layers[cur].qkv_b, st, e->gpart, e->gpart_stride); next_layer(); };
                 break;
             case SP_T_O: m = &e->layers[cur].o;
                 launch = [&] { launch_gemv(e->layers[cur].o, EPI_RESID, e->attn, NHD, n_cols, e->x, nullptr, H, nullptr,
-                                           st); next_layer(); };
+                                           st, e->gpart, e->gpart_stride); next_layer(); };
                 break;
             case SP_T_GATE_UP: m = &e->layers[cur].gate_up;
                 launch = [&] { launch_gemv(e->layers[cur].gate_up, EPI_SILU, e->xn, H, n_cols, nullptr, e->act, I,
@@ -827,7 +905,7 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
                 break;
             case SP_T_DOWN: m = &e->layers[cur].down;
                 launch = [&] { launch_gemv(e->layers[cur].down, EPI_RESID, e->act, I, n_cols, e->x, nullptr, H, nullptr,
-                                           st); next_layer(); };
+                                           st, e->gpart, e->gpart_stride); next_layer(); };
                 break;
             case SP_T_HEAD: case SP_T_EMBED: m = d.tied_head || kind == SP_T_EMBED ? &e->embed : &e->head;
                 launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->logits, nullptr, d.vocab, nullptr, st); };
