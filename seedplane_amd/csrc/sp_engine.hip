@@ -100,21 +100,21 @@ struct GemvPlan {
 int g_tune[3] = {0, 0, 0};
 #endif
 
-// Launch shape of one GEMV (from launch-shape sweeps of the Qwen2-1.5B matrices at 1, 16, 33 and 64 columns).
-// Small-batch GEMVs are latency-bound: every wave issues its share of the weights in one or two batches, and the
-// grid must fit the chip at once (256 CUs).  Matrices with few row groups (qkv, o, down) are split along K into
-// slices that the consuming kernel adds up; the LM head and the wider column tiles give each wave two row groups
-// (R = 2), which doubles the loads in flight per wave and halves the activation reads per weight byte.
+// Launch shape of one GEMV, from launch-shape sweeps (row groups per wave x waves x slices) of the Qwen2-0.5B fp16,
+// 1.5B int8 and 7B int4 matrices at 1, 16 and 32-33 columns.  Small-batch GEMVs are latency-bound: what counts is
+// the number of waves with loads in flight and a grid that the chip (256 CUs) holds at once.  Matrices with few row
+// groups (qkv, o, down) are split along K into slices that the consuming kernel adds up; the LM head and the wider
+// column tiles give each wave two row groups (R = 2: twice the loads in flight per wave, half the activation reads
+// per weight byte).
 GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok) {
     GemvPlan p;
     p.rg = m.paired ? 2 : 1;
     p.units = m.rows_pad / 16 / p.rg;
-    const int tb = mt == 1 ? (m.fmt == 3 ? 2 : 4) : 2;
     if (mt == 1) p.r = p.units >= 2048 && p.units % 2 == 0 ? 2 : 1;
-    else p.r = p.units % 2 == 0 && !(m.fmt == 3 && m.paired) ? 2 : 1;    // (the Q4 pair with R = 2 would spill)
+    else p.r = p.units % 2 == 0 && !m.paired ? 2 : 1;
     int s = 1;
     if (split_ok && !m.paired) {
-        s = std::max(1, 1024 / (p.units / p.r));
+        s = std::max(1, 2048 / (p.units / p.r));
         s = std::min(s, std::max(1, m.nkt / 2));
         s = std::min(s, mt == 1 ? GEMV_MAX_SLICES : 4);
     }
@@ -124,9 +124,9 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok) {
 #endif
     p.s = s;
     p.kslice = (m.nkt + s - 1) / s;
-    int nw = mt == 1 ? std::min(4, (p.kslice + tb - 1) / tb) : std::min(8, p.kslice);
+    int nw = std::min(p.kslice, mt > 1 && p.kslice >= 32 ? 8 : 4);
 #ifdef SP_GEMV_TUNE
-    if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 16 : 8);
+    if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 4 : 8);
 #endif
     while (nw > 1 && (size_t)nw * p.r * p.rg * mt * 1024 > GEMV_MAX_LDS) --nw;
     p.nw = std::max(1, nw);

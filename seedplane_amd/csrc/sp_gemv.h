@@ -52,9 +52,10 @@ __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
     }
 }
 
-// Threads per block: single-column-tile variants use up to 16 waves; wider variants up to 8 waves (256 VGPRs) so the
-// activation fragments of several column tiles stay in registers without spilling.  TB = k-tiles per wave in flight.
-template <int MT> struct GemvLimits { static constexpr int MAX_THREADS = MT == 1 ? 1024 : 512; };
+// Threads per block: single-column-tile variants use up to 4 waves, wider ones up to 8 (each wave may then hold up to
+// 256 VGPRs: the weight tiles and activation fragments of a whole batch stay in registers without spilling).
+// TB = k-tiles per wave whose loads are in flight together.
+template <int MT> struct GemvLimits { static constexpr int MAX_THREADS = MT == 1 ? 256 : 512; };
 template <int FMT, int MT> struct GemvBatch { static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : 4) : 2; };
 
 template <int RG>
