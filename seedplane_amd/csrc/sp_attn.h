@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, con
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NORM_PER_THREAD; ++i) ss += v[i] * v[i];
-    ss = block_sum(ss, red);
+    ss = block_sum_dpp(ss, red);
     const float rs = 1.0f / sqrtf(ss / (float)H + eps);
 #pragma unroll
     for (int i = 0; i < NORM_PER_THREAD; ++i) {
@@ -217,9 +217,9 @@ __global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
         }
         sc = acc;
     }
-    const float m = wave_max(sc);
+    const float m = wave_max_dpp(sc);
     const float ex = (sc == -INFINITY) ? 0.f : expf(sc - m);
-    const float l = wave_sum(ex);
+    const float l = wave_sum_dpp(ex);
     e_s[h][lane] = ex;
     __syncthreads();
 
@@ -238,34 +238,69 @@ __global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
     if (lane == 0) { out[0] = m; out[1] = l; }
 }
 
-// Decode attention without a split-K combine: one block per (kv head, column) takes every visible key of a column
-// whose keys are one ring range (no tree block).  Wave w owns a contiguous slice of the keys and walks it in
-// sub-chunks of 32: S = Q K^T on MFMA (rows = the G query heads of the kv head, K fragments straight from the cache),
-// online softmax per row, P and V^T staged in the wave's own LDS region, O += P V on MFMA.  The 8 wave states are
-// merged in wave order and the fp16 attention rows written as k_attn_combine writes them.
-constexpr int DEC_WAVES = 8, DEC_KC = 32, DEC_MAX_KEYS = 256;
-template <int HD>
-__global__ void __launch_bounds__(64 * DEC_WAVES) k_attn_dec(AttnArgs a, f16 *out, int ldo) {
+// Decode attention on MFMA for columns whose keys are one ring range (no tree block).  One block per (kv head, column,
+// split of NWV * SUB * DEC_KC keys); wave w owns SUB * DEC_KC consecutive keys of the split and issues all of their
+// K and V loads before the first use (one memory round trip per block).  Per sub-chunk of DEC_KC keys: S = Q K^T on
+// MFMA (rows = the G query heads of the kv head, K fragments straight from the cache), online softmax per row, P and
+// V^T staged in the wave's own LDS region, O += P V on MFMA.  The wave states are merged in wave order; a column
+// whose keys fit one split gets its fp16 attention row directly, otherwise each split writes {m, l, acc} in
+// k_attn_part's layout and k_attn_combine merges the splits.
+constexpr int DEC_KC = 32;
+template <int HD, int NWV, int SUB>
+__global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int ldo, int direct) {
+    constexpr int DEC_WAVES = NWV, DEC_SUB = SUB, DEC_KW = DEC_KC * SUB, DEC_KB = NWV * DEC_KW;
     constexpr int ST = HD / 32, NDT = HD / 16, KP = DEC_KC + 8;
+    constexpr int VPL = HD / 2 / 8;                          // 16-byte V pieces per lane per sub-chunk
     __shared__ __align__(16) f16 vt[DEC_WAVES][HD][KP];      // V^T of the wave's current sub-chunk
     __shared__ __align__(16) f16 ps[DEC_WAVES][16][KP];      // P of the wave's current sub-chunk
     __shared__ float wm[DEC_WAVES][16], wl[DEC_WAVES][16];
     __shared__ float wo[DEC_WAVES][8][HD];                   // wave outputs of the (at most 8) query heads
-    const int kvh = blockIdx.x, b = blockIdx.y;
+    const int kvh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
     const sp_token t = a.toks[b];
     const int G = a.NH / a.NKV;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
     const int nlin = t.ctx_hi - t.ctx_lo + 1;
-    const int kw = ((nlin + DEC_WAVES - 1) / DEC_WAVES + DEC_KC - 1) / DEC_KC * DEC_KC;   // keys per wave
-    const int v_lo = w * kw, v_hi = min(nlin, v_lo + kw);
+    const int b_lo = split * DEC_KB;
+    if (b_lo >= nlin) return;
+    const int v_lo = b_lo + w * DEC_KW, v_hi = min(nlin, v_lo + DEC_KW);
     const size_t head_base = ((size_t)t.seq * a.NKV + kvh) * a.n_slots;
-    // Q fragments (rows = query heads of this kv head, scaled, fp16)
+    const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    // ---- every load of the wave: K fragments (lane: key r16 of a 16-key tile, dims g4 * 8 ..) and V rows (lane:
+    // key lane / 2 of a sub-chunk, dims (lane & 1) * HD/2 ..)
+    f16x8 kf[DEC_SUB][2][ST], vf[DEC_SUB][VPL];
+#pragma unroll
+    for (int sc = 0; sc < DEC_SUB; ++sc) {
+        const int v0 = v_lo + sc * DEC_KC;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int key = v0 + kt * 16 + r16;
+            const bool live = key < v_hi;
+            const size_t off = (head_base + (size_t)((t.ctx_lo + (live ? key : 0)) % a.n_slots)) * HD + g4 * 8;
+#pragma unroll
+            for (int st = 0; st < ST; ++st) kf[sc][kt][st] = live ? *(const f16x8 *)(a.kc + off + st * 32) : zero8;
+        }
+        const int key = v0 + (lane >> 1);
+        const bool live = key < v_hi;
+        const size_t off = (head_base + (size_t)((t.ctx_lo + (live ? key : 0)) % a.n_slots)) * HD + (lane & 1) * (HD / 2);
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) vf[sc][i] = live ? *(const f16x8 *)(a.vc + off + i * 8) : zero8;
+    }
+    // Q fragments (rows = query heads of this kv head, scaled, fp16): unconditional vector loads from a clamped row
+    // (a load under a per-lane condition is issued and waited for one at a time)
     f16x8 qa[ST];
-    const float *qrow = a.q + (size_t)b * a.NH * HD + (size_t)(kvh * G + min(r16, G - 1)) * HD;
+    {
+        const float *qrow = a.q + (size_t)b * a.NH * HD + (size_t)(kvh * G + min(r16, G - 1)) * HD + g4 * 8;
+        f32x4 qv[ST][2];
 #pragma unroll
-    for (int st = 0; st < ST; ++st) {
+        for (int st = 0; st < ST; ++st) {
+            qv[st][0] = *(const f32x4 *)(qrow + st * 32);
+            qv[st][1] = *(const f32x4 *)(qrow + st * 32 + 4);
+        }
+        const float qs = r16 < G ? a.scale : 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qa[st][e] = r16 < G ? (f16)(qrow[st * 32 + g4 * 8 + e] * a.scale) : (f16)0.f;
+        for (int st = 0; st < ST; ++st)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qa[st][e] = (f16)(qv[st][e >> 2][e & 3] * qs);
     }
     float mrow[4], lrow[4];
     f32x4 o[NDT];
@@ -273,51 +308,37 @@ __global__ void __launch_bounds__(64 * DEC_WAVES) k_attn_dec(AttnArgs a, f16 *ou
     for (int j = 0; j < 4; ++j) { mrow[j] = -INFINITY; lrow[j] = 0.f; }
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    for (int v0 = v_lo; v0 < v_hi; v0 += DEC_KC) {
-        // V rows of the sub-chunk (lane: key v0 + lane / 2, dims (lane & 1) * HD/2 ..) -> V^T in LDS
-        constexpr int VPL = HD / 2 / 8;                      // 16-byte pieces per lane
-        {
-            const int key = v0 + (lane >> 1);
-            const bool live = key < v_hi;
-            const size_t off = (head_base + (size_t)((t.ctx_lo + key) % a.n_slots)) * HD + (lane & 1) * (HD / 2);
 #pragma unroll
-            for (int i = 0; i < VPL; ++i) {
-                const f16x8 vv = live ? *(const f16x8 *)(a.vc + off + i * 8) : zero8;
+    for (int sc = 0; sc < DEC_SUB; ++sc) {
+        const int v0 = v_lo + sc * DEC_KC;
+        if (v0 >= v_hi) break;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vt[w][(lane & 1) * (HD / 2) + i * 8 + e][lane >> 1] = vv[e];
-            }
-        }
-        // S = Q K^T for 2 tiles of 16 keys; K fragments from the cache (lane: key r16, dims g4 * 8 ..)
-        f32x4 sc[2];
+        for (int i = 0; i < VPL; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vt[w][(lane & 1) * (HD / 2) + i * 8 + e][lane >> 1] = vf[sc][i][e];
+        f32x4 sc2[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            const int key = v0 + kt * 16 + r16;
-            const bool live = key < v_hi;
-            const size_t off = (head_base + (size_t)((t.ctx_lo + key) % a.n_slots)) * HD + g4 * 8;
-            sc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            sc2[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int st = 0; st < ST; ++st)
-                sc[kt] = mfma16(qa[st], live ? *(const f16x8 *)(a.kc + off + st * 32) : zero8, sc[kt]);
+            for (int st = 0; st < ST; ++st) sc2[kt] = mfma16(qa[st], kf[sc][kt][st], sc2[kt]);
         }
         // online softmax: lane holds rows 4 g4 + j, keys v0 + kt * 16 + r16
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float mx = mrow[j];
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) if (v0 + kt * 16 + r16 < v_hi) mx = fmaxf(mx, sc[kt][j]);
-#pragma unroll
-            for (int sh = 1; sh < 16; sh <<= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, SP_WAVE));
+            for (int kt = 0; kt < 2; ++kt) if (v0 + kt * 16 + r16 < v_hi) mx = fmaxf(mx, sc2[kt][j]);
+            mx = row16_max(mx);
             const float corr = mrow[j] == -INFINITY ? 0.f : expf(mrow[j] - mx);
             float ls = 0.f;
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
-                const float pe = v0 + kt * 16 + r16 < v_hi ? expf(sc[kt][j] - mx) : 0.f;
+                const float pe = v0 + kt * 16 + r16 < v_hi ? expf(sc2[kt][j] - mx) : 0.f;
                 ps[w][4 * g4 + j][kt * 16 + r16] = (f16)pe;
                 ls += pe;
             }
-#pragma unroll
-            for (int sh = 1; sh < 16; sh <<= 1) ls += __shfl_xor(ls, sh, SP_WAVE);
+            ls = row16_sum(ls);
             lrow[j] = lrow[j] * corr + ls;
             mrow[j] = mx;
 #pragma unroll
@@ -355,7 +376,13 @@ __global__ void __launch_bounds__(64 * DEC_WAVES) k_attn_dec(AttnArgs a, f16 *ou
                 acc += f * wo[w2][h][d];
             }
         }
-        out[(size_t)b * ldo + (kvh * G + h) * HD + d] = (f16)(acc / L);
+        if (direct) {
+            out[(size_t)b * ldo + (kvh * G + h) * HD + d] = (f16)(acc / L);
+        } else {
+            float *pp = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + split) * (HD + 2);
+            pp[2 + d] = acc;
+            if (d == 0) { pp[0] = M; pp[1] = L; }
+        }
     }
 }
 
@@ -375,7 +402,7 @@ __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const i
         mloc = fmaxf(mloc, w_s[c]);
     }
     // block max
-    mloc = wave_max(mloc);
+    mloc = wave_max_dpp(mloc);
     if ((tid & 63) == 0) red[tid >> 6] = mloc;
     __syncthreads();
     float M = red[0];
@@ -387,7 +414,7 @@ __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const i
         lsum += wc * p[(size_t)c * (HD + 2) + 1];
     }
     __syncthreads();
-    const float L = block_sum(lsum, red + 8);
+    const float L = block_sum_dpp(lsum, red + 8);
     if (tid < HD) {
         float acc = 0.f;
 #pragma unroll 4
@@ -589,8 +616,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
                 sc[st][j] = v;
                 m = fmaxf(m, v);
             }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, SP_WAVE));
+            m = row16_max(m);
             float l = 0.f;
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
@@ -598,8 +624,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
                 sc[st][j] = e;
                 l += e;
             }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, SP_WAVE);
+            l = row16_sum(l);
             mrow[j] = m; lrow[j] = l;
         }
         // ---- P (fp16) to LDS in row-major, read back as the A operand

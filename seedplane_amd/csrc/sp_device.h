@@ -70,6 +70,46 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, SP_WAVE));
     return v;
 }
+// Reductions over the 16 lanes of a DPP row (lanes 16k .. 16k+15) on DPP moves instead of LDS-routed shuffles:
+// pair with lane ^ 1, lane ^ 2 (quad permutes), then the mirror lane within 8 and within 16.  Every step combines
+// two equal partial results of a pair in both orders, so all 16 lanes end with the same bits.
+// (The identity element is returned where a source lane is disabled.)
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v, float identity) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v, 0.f);      // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v, 0.f);      // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v, 0.f);     // row_half_mirror
+    v += dpp_mov<0x140>(v, 0.f);     // row_mirror
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v, -INFINITY));
+    v = fmaxf(v, dpp_mov<0x4E>(v, -INFINITY));
+    v = fmaxf(v, dpp_mov<0x141>(v, -INFINITY));
+    v = fmaxf(v, dpp_mov<0x140>(v, -INFINITY));
+    return v;
+}
+// Whole-wave sum / max: the four row results combined in row order (uniform across the wave).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = row16_sum(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (a + b) + (c + d);
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = row16_max(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
 // (value, index) max with the smallest index winning ties.
 __device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
@@ -86,6 +126,18 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 __device__ __forceinline__ float block_sum(float v, float *red) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int j = 0; j < nw; ++j) t += red[j];
+    return t;
+}
+
+// Block-wide sum on DPP wave reductions (same contract as block_sum).
+__device__ __forceinline__ float block_sum_dpp(float v, float *red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_sum_dpp(v);
     __syncthreads();
     if (lane == 0) red[w] = v;
     __syncthreads();

@@ -237,6 +237,37 @@ void launch_rope(int n, const RopeArgs &ra, int np, hipStream_t st) {
     by_slices(np, [&](auto c) { hipLaunchKernelGGL((k_rope_kv<decltype(c)::value>), dim3(n), dim3(ROPE_THREADS), 0, st, ra); });
 }
 
+// decode attention split: waves per block x 32-key sub-chunks per wave
+#ifdef SP_GEMV_TUNE
+int g_tune_attn[2] = {0, 0};
+#endif
+struct DecShape { int nwv, sub; };
+DecShape dec_shape() {
+#ifdef SP_GEMV_TUNE
+    if (g_tune_attn[0] > 0) return DecShape{g_tune_attn[0], g_tune_attn[1]};
+#endif
+    return DecShape{4, 2};
+}
+int dec_keys_per_block() { const DecShape d = dec_shape(); return d.nwv * d.sub * DEC_KC; }
+
+template <int HD>
+void launch_attn_dec_hd(dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct) {
+    const DecShape d = dec_shape();
+#ifdef SP_GEMV_TUNE
+    if (d.nwv == 1 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 1>), grid, dim3(64), 0, st, aa, out, ldo, direct); return; }
+    if (d.nwv == 2 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 1>), grid, dim3(128), 0, st, aa, out, ldo, direct); return; }
+    if (d.nwv == 4 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 1>), grid, dim3(256), 0, st, aa, out, ldo, direct); return; }
+    if (d.nwv == 2 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 2>), grid, dim3(128), 0, st, aa, out, ldo, direct); return; }
+    if (d.nwv == 1 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 2>), grid, dim3(64), 0, st, aa, out, ldo, direct); return; }
+#endif
+    (void)d;
+    hipLaunchKernelGGL((k_attn_dec<HD, 4, 2>), grid, dim3(256), 0, st, aa, out, ldo, direct);
+}
+void launch_attn_dec(int HD, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct) {
+    if (HD == 64) launch_attn_dec_hd<64>(grid, st, aa, out, ldo, direct);
+    else launch_attn_dec_hd<128>(grid, st, aa, out, ldo, direct);
+}
+
 template <int FMT>
 void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x, hipStream_t st) {
     hipLaunchKernelGGL((k_embed<FMT>), dim3(n), dim3(256), 0, st, m.w, m.sz, m.nkt, toks, H, x, H);
@@ -302,7 +333,8 @@ struct sp_engine {
     // attention plan of one forward call: same-sequence column groups (multi-query kernel) or one block row per column
     struct AttnPlan {
         bool mq = false;
-        bool dec = false;        // every column a plain ring range of at most DEC_MAX_KEYS keys: k_attn_dec
+        bool dec = false;        // every column a plain ring range (no tree block): k_attn_dec over key splits
+        bool dec_direct = false; // ... and every column fits one split: no combine
         int ngroups = 0, nchunk = 1, splits = 1;
         std::vector<AttnGroup> groups;
         std::vector<int> colnc;
@@ -408,9 +440,39 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
         }
     }
     p.nchunk = graph ? max_nchunk : mx;
-    if (!p.mq && d.n_heads / d.n_kv_heads <= 8) {
+    bool dec_ok = true;
+#ifdef SP_GEMV_TUNE
+    dec_ok = g_tune_attn[0] >= 0;
+#endif
+    if (!p.mq && d.n_heads / d.n_kv_heads <= 8 && dec_ok) {
+        // the MFMA decode kernel pays off once its key splits fill the chip (long contexts, large batches); short
+        // ranges stay on the 64-key chunk kernel, which spreads them over more CUs
         p.dec = true;
-        for (int c = 0; c < n; ++c) p.dec = p.dec && t[c].tree_count == 0 && nlin_of(t[c]) <= DEC_MAX_KEYS;
+        long work = 0;
+        for (int c = 0; c < n; ++c) {
+            p.dec = p.dec && t[c].tree_count == 0 && nlin_of(t[c]) >= 1;
+            work += (long)(nlin_of(t[c]) + dec_keys_per_block() - 1) / dec_keys_per_block() * d.n_kv_heads;
+        }
+        bool force = false;
+#ifdef SP_GEMV_TUNE
+        force = g_tune_attn[0] > 0;
+#endif
+        if (work < 256 && !force) p.dec = false;
+    }
+    if (p.dec) {
+        // splits of dec_keys_per_block() keys; a graph is sized for the longest range the ring allows
+        int ms = 1;
+        for (int c = 0; c < n; ++c) {
+            p.colnc[c] = (nlin_of(t[c]) + dec_keys_per_block() - 1) / dec_keys_per_block();
+            ms = std::max(ms, p.colnc[c]);
+        }
+        p.nchunk = graph ? (n_slots + dec_keys_per_block() - 1) / dec_keys_per_block() : ms;
+        p.dec_direct = p.nchunk == 1;
+        if (p.nchunk > max_nchunk || p.nchunk > ATT_MAX_CHUNKS) {      // splits must fit the partial buffer
+            p.dec = p.dec_direct = false;
+            p.nchunk = graph ? max_nchunk : mx;
+            for (int c = 0; c < n; ++c) p.colnc[c] = (nlin_of(t[c]) + t[c].tree_count + ATT_CH - 1) / ATT_CH;
+        }
     }
     return p;
 }
@@ -565,15 +627,14 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
             else launch_attn_mq_hd<128>(G, agrid, st, am);
         } else if (ap.dec) {
             AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
-            if (HD == 64) hipLaunchKernelGGL(k_attn_dec<64>, dim3(NKV, n), dim3(64 * DEC_WAVES), 0, st, aa, attn, NH * HD);
-            else hipLaunchKernelGGL(k_attn_dec<128>, dim3(NKV, n), dim3(64 * DEC_WAVES), 0, st, aa, attn, NH * HD);
+            launch_attn_dec(HD, dim3(NKV, n, nchunk), st, aa, attn, NH * HD, ap.dec_direct ? 1 : 0);
         } else {
             AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
             dim3 agrid(nchunk, NKV, n);
             if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
             else launch_attn_hd<128>(G, agrid, st, aa);
         }
-        if (!ap.dec)
+        if (!ap.dec_direct)
             hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn, NH * HD);
         pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, st, gpart, ps);
         launch_rmsnorm(n, x, H, gpart, pend, ps, ly.post_norm, d.rms_eps, xn, st);
@@ -792,7 +853,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         HIPCHK(hipMemcpyAsync(e->dgroups, ap.groups.data(), ap.ngroups * sizeof(AttnGroup), hipMemcpyHostToDevice, e->stream));
         HIPCHK(hipMemcpyAsync(e->dcolnc, ap.colnc.data(), n * sizeof(int), hipMemcpyHostToDevice, e->stream));
         if (use_graph) {
-            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? -2 : -1));
+            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? (ap.dec_direct ? -3 : -2) : -1));
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 // record on the private stream (the caller's may be the null stream, which cannot capture)
@@ -833,6 +894,7 @@ int sp_engine_last_path(const sp_engine *e) { return e ? e->last_path : -1; }
 
 #ifdef SP_GEMV_TUNE
 void sp_debug_gemv_plan(int r, int nw, int s) { g_tune[0] = r; g_tune[1] = nw; g_tune[2] = s; }
+void sp_debug_attn_plan(int nwv, int sub) { g_tune_attn[0] = nwv; g_tune_attn[1] = sub; }
 #endif
 
 #ifdef SP_DECODE_TRACE

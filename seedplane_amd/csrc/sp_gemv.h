@@ -58,26 +58,42 @@ __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
 template <int MT> struct GemvLimits { static constexpr int MAX_THREADS = MT == 1 ? 256 : 512; };
 template <int FMT, int MT> struct GemvBatch { static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : 4) : 2; };
 
+// Lane holds D[m = mt*16 + 4g + j][n = unit*16 + r], j < 4.  Operands the epilogue reads (bias, the residual) are
+// loaded from clamped addresses before any store, so their loads are in flight together.
 template <int RG>
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int unit, int mt, const f32x4 &v0, const f32x4 &v1) {
     const int r = threadIdx.x & 15, g = (threadIdx.x >> 4) & 3;
     const int n = unit * 16 + r;
     if (n >= a.n_real) return;
+    int mrow[4];
+    bool live[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int m = mt * 16 + 4 * g + j;
-        if (m >= a.m) continue;
-        if constexpr (RG == 2) {
-            a.out_f16[(size_t)m * a.ldo + n] = (f16)(silu_f(v0[j]) * v1[j]);
-        } else if (a.epi == EPI_STORE) {
-            float v = v0[j];
-            if (a.bias) v += a.bias[n];
-            a.out_f32[(size_t)m * a.ldo + n] = v;
-        } else if (a.epi == EPI_RESID) {
-            a.out_f32[(size_t)m * a.ldo + n] += v0[j];
-        } else {
-            a.out_f32[(size_t)blockIdx.y * a.pstride + (size_t)m * a.ldo + n] = v0[j];
-        }
+        live[j] = m < a.m;
+        mrow[j] = live[j] ? m : a.m - 1;
+    }
+    if constexpr (RG == 2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (live[j]) a.out_f16[(size_t)mrow[j] * a.ldo + n] = (f16)(silu_f(v0[j]) * v1[j]);
+    } else if (a.epi == EPI_STORE) {
+        const float bn = a.bias ? a.bias[n] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (live[j]) a.out_f32[(size_t)mrow[j] * a.ldo + n] = v0[j] + bn;
+    } else if (a.epi == EPI_RESID) {
+        float prev[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) prev[j] = a.out_f32[(size_t)mrow[j] * a.ldo + n];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (live[j]) a.out_f32[(size_t)mrow[j] * a.ldo + n] = prev[j] + v0[j];
+    } else {
+        float *dst = a.out_f32 + (size_t)blockIdx.y * a.pstride;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (live[j]) dst[(size_t)mrow[j] * a.ldo + n] = v0[j];
     }
 }
 
