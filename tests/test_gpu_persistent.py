@@ -11,7 +11,8 @@ from seedplane_amd.qwen_engine import Qwen2Engine
 from seedplane_amd.synth import make_weights, random_prompt
 from tests.conftest import small_cfg
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.skip(reason='the persistent decode kernel is switched off: one launch of it '
+                                                 'faulted the GPU and the cause is not yet found')]
 TOL = 2e-2
 
 
