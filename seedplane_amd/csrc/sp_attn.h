@@ -238,6 +238,127 @@ __global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
     if (lane == 0) { out[0] = m; out[1] = l; }
 }
 
+// k_attn_part with the RoPE / KV-write step folded in, for plain decode columns (no tree block): each block rotates
+// the queries of its kv head from the projection (split-K slices + bias, in slice order, exactly as k_rope_kv), and
+// the block whose chunk holds the column's newest position (ctx_hi) also rotates its key, writes key and value to
+// their cache slot and uses them for that row.  Same arithmetic and summation order as k_rope_kv + k_attn_part, so
+// the results are bit-identical; one launch (and one dependent step) fewer per layer.
+template <int HD, int G>
+__global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs r, int np) {
+    constexpr int KP = HD + 8, HALF = HD / 2;
+    __shared__ float q_s[G][HD];
+    __shared__ __align__(16) f16 k_s[ATT_CH][KP];
+    __shared__ __align__(16) f16 v_s[ATT_CH][HD];
+    __shared__ float e_s[G][ATT_CH];
+
+    const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const sp_token t = a.toks[b];
+    const int nlin = t.ctx_hi >= t.ctx_lo ? t.ctx_hi - t.ctx_lo + 1 : 0;
+    const int v0 = c * ATT_CH;
+    if (v0 >= nlin) return;
+    const int cnt = min(ATT_CH, nlin - v0);
+    const int jn = nlin - 1 - v0;                   // row of the newest position in this chunk (< cnt: owned here)
+    const bool own = jn < cnt;
+    const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
+    constexpr int NT = 64 * G;
+    const size_t head_base = ((size_t)t.seq * a.NKV + kvh) * a.n_slots;
+
+    // projection value idx of this column: the finished row, or the split-K slices in slice order plus the bias
+    // (all slice loads are issued before the first add; up to 8 slices)
+    auto proj = [&](int idx) -> float {
+        if (np == 0) return r.qkv[(size_t)b * r.Nqkv + idx];
+        const float *p = r.part + (size_t)b * r.Nqkv + idx;
+        float tv[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) tv[s] = s < np ? p[(size_t)s * r.pstride] : 0.f;
+        const float bias = r.bias[idx];
+        float v = tv[0];
+#pragma unroll
+        for (int s = 1; s < 8; ++s) if (s < np) v += tv[s];
+        return v + bias;
+    };
+    // the chunk's cached K/V rows into registers first, so their loads overlap the projection loads below
+    constexpr int CPR = HD / 8;                     // 16-byte chunks per row
+    constexpr int PER = (ATT_CH * CPR + NT - 1) / NT;
+    f16x8 kr[PER], vr[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        // unconditional loads (rows past the chunk re-read row 0) so that all of them are in flight together
+        const int i = tid + k * NT, j = i < cnt * CPR ? i / CPR : 0, ch = i % CPR;
+        const size_t off = (head_base + (t.ctx_lo + v0 + j) % a.n_slots) * HD + ch * 8;
+        kr[k] = *(const f16x8 *)(a.kc + off);
+        vr[k] = *(const f16x8 *)(a.vc + off);
+    }
+    const float fpos = (float)t.pos;
+    // queries of the group (then the key of the newest position, in the owning block), rotated
+    const int nrot = (own ? G + 1 : G) * HALF;
+    for (int i = tid; i < nrot; i += NT) {
+        const int hh = i / HALF, j = i - hh * HALF;
+        const int head = hh < G ? kvh * G + hh : a.NH + kvh;
+        const float ph = fpos * r.inv_freq[j];
+        const float cs = cosf(ph), sn = sinf(ph);
+        const float x1 = proj(head * HD + j), x2 = proj(head * HD + j + HALF);
+        const float o1 = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(-x2, sn));
+        const float o2 = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
+        if (hh < G) {
+            q_s[hh][j] = o1 * a.scale;
+            q_s[hh][j + HALF] = o2 * a.scale;
+        } else {
+            const f16 k1 = (f16)o1, k2 = (f16)o2;
+            k_s[jn][j] = k1; k_s[jn][j + HALF] = k2;
+            f16 *kd = r.kc + (head_base + t.slot) * HD;
+            kd[j] = k1; kd[j + HALF] = k2;
+        }
+    }
+    if (own) {
+        for (int d = tid; d < HD; d += NT) {
+            const f16 v = (f16)proj((a.NH + a.NKV + kvh) * HD + d);
+            v_s[jn][d] = v;
+            r.vc[(head_base + t.slot) * HD + d] = v;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = tid + k * NT, j = i / CPR, ch = i - j * CPR;
+        if (i < cnt * CPR && !(own && j == jn)) {   // the newest row came from the projection
+            *(f16x8 *)&k_s[j][ch * 8] = kr[k];
+            *(f16x8 *)&v_s[j][ch * 8] = vr[k];
+        }
+    }
+    __syncthreads();
+
+    float sc = -INFINITY;
+    if (lane < cnt) {
+        float acc = 0.f;
+#pragma unroll 4
+        for (int d = 0; d < HD; d += 8) {
+            const f16x8 kv = *(const f16x8 *)&k_s[lane][d];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += q_s[h][d + e] * (float)kv[e];
+        }
+        sc = acc;
+    }
+    const float m = wave_max_dpp(sc);
+    const float ex = (sc == -INFINITY) ? 0.f : expf(sc - m);
+    const float l = wave_sum_dpp(ex);
+    e_s[h][lane] = ex;
+    __syncthreads();
+
+    float *out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + c) * (HD + 2);
+    constexpr int DPL = HD / 64;                    // output dims per lane
+    float o[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[i] = 0.f;
+    for (int j = 0; j < cnt; ++j) {
+        const float p = e_s[h][j];
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) o[i] += p * (float)v_s[j][lane + 64 * i];
+    }
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) out[2 + lane + 64 * i] = o[i];
+    if (lane == 0) { out[0] = m; out[1] = l; }
+}
+
 // Decode attention on MFMA for columns whose keys are one ring range (no tree block).  One block per (kv head, column,
 // split of NWV * SUB * DEC_KC keys); wave w owns SUB * DEC_KC consecutive keys of the split and issues all of their
 // K and V loads before the first use (one memory round trip per block).  Per sub-chunk of DEC_KC keys: S = Q K^T on

@@ -197,6 +197,20 @@ void launch_attn_hd(int G, dim3 grid, hipStream_t st, const AttnArgs &a) {
 }
 
 template <int HD>
+void launch_attn_rope_hd(int G, dim3 grid, hipStream_t st, const AttnArgs &a, const RopeArgs &r, int np) {
+    switch (G) {
+        case 1: hipLaunchKernelGGL((k_attn_part_rope<HD, 1>), grid, dim3(64 * 1), 0, st, a, r, np); break;
+        case 2: hipLaunchKernelGGL((k_attn_part_rope<HD, 2>), grid, dim3(64 * 2), 0, st, a, r, np); break;
+        case 3: hipLaunchKernelGGL((k_attn_part_rope<HD, 3>), grid, dim3(64 * 3), 0, st, a, r, np); break;
+        case 4: hipLaunchKernelGGL((k_attn_part_rope<HD, 4>), grid, dim3(64 * 4), 0, st, a, r, np); break;
+        case 5: hipLaunchKernelGGL((k_attn_part_rope<HD, 5>), grid, dim3(64 * 5), 0, st, a, r, np); break;
+        case 6: hipLaunchKernelGGL((k_attn_part_rope<HD, 6>), grid, dim3(64 * 6), 0, st, a, r, np); break;
+        case 7: hipLaunchKernelGGL((k_attn_part_rope<HD, 7>), grid, dim3(64 * 7), 0, st, a, r, np); break;
+        default: hipLaunchKernelGGL((k_attn_part_rope<HD, 8>), grid, dim3(64 * 8), 0, st, a, r, np); break;
+    }
+}
+
+template <int HD>
 void launch_attn_mq_hd(int G, dim3 grid, hipStream_t st, const AttnMqArgs &a) {
     switch (G) {
         case 1: hipLaunchKernelGGL((k_attn_mq<HD, 1>), grid, dim3(256), 0, st, a); break;
@@ -339,6 +353,7 @@ struct sp_engine {
         bool mq = false;
         bool dec = false;        // every column a plain ring range (no tree block): k_attn_dec over key splits
         bool dec_direct = false; // ... and every column fits one split: no combine
+        bool rope_fused = false; // chunk kernel with RoPE / KV write folded in (plain columns of distinct sequences)
         int ngroups = 0, nchunk = 1, splits = 1;
         std::vector<AttnGroup> groups;
         std::vector<int> colnc;
@@ -462,6 +477,18 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
         force = g_tune_attn[0] > 0;
 #endif
         if (work < 256 && !force) p.dec = false;
+    }
+    if (!p.mq && !p.dec) {
+        // every column a plain ring range of its own sequence: no column sees another column's new key, so each
+        // attention block may rotate and store the key of the position it holds
+        bool plain = true;
+        std::vector<int> seqs;
+        for (int c = 0; c < n; ++c) {
+            plain = plain && t[c].tree_count == 0 && nlin_of(t[c]) >= 1 && t[c].slot == t[c].ctx_hi % n_slots;
+            seqs.push_back(t[c].seq);
+        }
+        std::sort(seqs.begin(), seqs.end());
+        p.rope_fused = plain && std::adjacent_find(seqs.begin(), seqs.end()) == seqs.end();
     }
     if (p.dec) {
         // splits of dec_keys_per_block() keys; a graph is sized for the longest range the ring allows
@@ -669,10 +696,16 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
         launch_rmsnorm(n, x, H, gpart, pend, ps, ly.in_norm, d.rms_eps, xn, st);
         const int sq = launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, gpart, ps);
         RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots, gpart, ps, ly.qkv_b};
-        launch_rope(n, ra, sq, st);
+        const bool fused = ap.rope_fused && logits_on;
+        if (!fused) launch_rope(n, ra, sq, st);
         if (l + 1 == d.n_layers && !logits_on) break;   // K/V-only: the last layer only needs its K/V
         const int G = NH / NKV;
-        if (ap.mq) {
+        if (fused) {
+            AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
+            dim3 agrid(nchunk, NKV, n);
+            if (HD == 64) launch_attn_rope_hd<64>(G, agrid, st, aa, ra, sq);
+            else launch_attn_rope_hd<128>(G, agrid, st, aa, ra, sq);
+        } else if (ap.mq) {
             AttnMqArgs am{q, kc[l], vc[l], dtoks, dgroups, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD),
                           attn_part, ap.splits};
             dim3 agrid(nchunk, NKV, ap.ngroups * ap.splits);
@@ -898,7 +931,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         HIPCHK(hipMemcpyAsync(e->dgroups, ap.groups.data(), ap.ngroups * sizeof(AttnGroup), hipMemcpyHostToDevice, e->stream));
         HIPCHK(hipMemcpyAsync(e->dcolnc, ap.colnc.data(), n * sizeof(int), hipMemcpyHostToDevice, e->stream));
         if (use_graph) {
-            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? (ap.dec_direct ? -3 : -2) : -1));
+            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? (ap.dec_direct ? -3 : -2) : (ap.rope_fused ? -4 : -1)));
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 // record on the private stream (the caller's may be the null stream, which cannot capture)
