@@ -509,17 +509,26 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
 
 // out[b][h*HD + d] (fp16) = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}; one block (HD threads) per
 // (head, column), chunk statistics loaded in parallel.
+// The chunk outputs are read in batches of CMB_BATCH with every load of a batch in flight together (the first batch
+// before the weights are known); the accumulation runs over the chunks in ascending order.
+constexpr int CMB_BATCH = 16;
 __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const int *col_nchunk, int NH, int HD,
                                                       int nchunk, f16 *out, int ldo) {
     __shared__ float w_s[ATT_MAX_CHUNKS];
+    __shared__ float l_s[ATT_MAX_CHUNKS];
     __shared__ float red[16];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
     const int nc = col_nchunk[b];
     const float *p = part + ((size_t)b * NH + h) * nchunk * (HD + 2);
+    const int d = min(tid, HD - 1), last = max(nc - 1, 0);     // clamped: every load is in bounds
+    float v[CMB_BATCH];
+#pragma unroll
+    for (int i = 0; i < CMB_BATCH; ++i) v[i] = p[(size_t)min(i, last) * (HD + 2) + 2 + d];
     float mloc = -INFINITY;
     for (int c = tid; c < nc; c += nt) {
         const float mc = p[(size_t)c * (HD + 2)], lc = p[(size_t)c * (HD + 2) + 1];
         w_s[c] = lc > 0.f ? mc : -INFINITY;
+        l_s[c] = lc;
         mloc = fmaxf(mloc, w_s[c]);
     }
     // block max
@@ -532,16 +541,21 @@ __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const i
     for (int c = tid; c < nc; c += nt) {
         const float wc = w_s[c] == -INFINITY ? 0.f : expf(w_s[c] - M);
         w_s[c] = wc;
-        lsum += wc * p[(size_t)c * (HD + 2) + 1];
+        lsum += wc * l_s[c];
     }
     __syncthreads();
     const float L = block_sum_dpp(lsum, red + 8);
-    if (tid < HD) {
-        float acc = 0.f;
-#pragma unroll 4
-        for (int c = 0; c < nc; ++c) acc += w_s[c] * p[(size_t)c * (HD + 2) + 2 + tid];
-        out[(size_t)b * ldo + h * HD + tid] = (f16)(acc / L);
+    float acc = 0.f;
+    for (int c0 = 0; c0 < nc; c0 += CMB_BATCH) {
+        if (c0 > 0) {
+#pragma unroll
+            for (int i = 0; i < CMB_BATCH; ++i) v[i] = p[(size_t)min(c0 + i, last) * (HD + 2) + 2 + d];
+        }
+#pragma unroll
+        for (int i = 0; i < CMB_BATCH; ++i)
+            if (c0 + i < nc) acc += w_s[c0 + i] * v[i];
     }
+    if (tid < HD) out[(size_t)b * ldo + h * HD + tid] = (f16)(acc / L);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -635,8 +649,12 @@ struct AttnMqArgs {
 
 template <int HD, int G>
 __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
-    constexpr int KP = HD + 8, VP = ATT_CH + 8;
+    constexpr int KP = HD + 8, VP = ATT_CH + 8;      // padded rows (halves): 68 / 36 dwords, 16-byte aligned
     constexpr int ST = HD / 32;                      // MFMA k-steps over head dim
+    constexpr int CPR = HD / 8;                      // 16-byte pieces per key row
+    constexpr int KPER = ATT_CH * CPR / 256;         // K pieces per thread
+    constexpr int VPER = ATT_CH / 2 * CPR / 256;     // V (key pair, piece) items per thread
+    static_assert(KPER * 256 == ATT_CH * CPR && VPER * 256 == ATT_CH / 2 * CPR, "chunk staging split");
     __shared__ __align__(16) f16 k_s[ATT_CH][KP];
     __shared__ __align__(16) f16 vt_s[HD][VP];
     __shared__ __align__(16) f16 p_s[4][16][VP];
@@ -654,133 +672,159 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     if (split * 64 >= R) return;                    // 4 row tiles of 16 rows per block
     const int cnt = min(ATT_CH, nvis - v0);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-
-    for (int i = tid; i < gr.ncols; i += 256) {
-        const sp_token t = a.toks[gr.first_col + i];
-        clo_s[i] = t.ctx_lo; chi_s[i] = t.ctx_hi; ctc_s[i] = t.tree_count; cmask_s[i] = t.tree_mask;
-    }
-    const size_t head_base = ((size_t)gr.seq * a.NKV + kvh) * a.n_slots;
-    constexpr int CPR = HD / 8;
-    for (int i = tid; i < ATT_CH * CPR; i += 256) {
-        const int j = i / CPR, ch = i - j * CPR;
-        f16x8 kv = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, vv = kv;
-        if (j < cnt) {
-            const int vis = v0 + j;
-            int slot, kp;
-            if (vis < gr.nlin) { kp = gr.lo + vis; slot = kp % a.n_slots; }
-            else { const int tj = vis - gr.nlin; kp = -(1 + tj); slot = (gr.tree_base + tj) % a.n_slots; }
-            if (ch == 0) kpos_s[j] = kp;
-            const size_t off = (head_base + slot) * HD + ch * 8;
-            kv = *(const f16x8 *)(a.kc + off);
-            vv = *(const f16x8 *)(a.vc + off);
-        } else if (ch == 0) {
-            kpos_s[j] = INT_MIN;
-        }
-        *(f16x8 *)&k_s[j][ch * 8] = kv;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vt_s[ch * 8 + e][j] = vv[e];
-    }
-    __syncthreads();
-
     const int r16 = lane & 15, g4 = lane >> 4;
     const int n_tiles = (R + 15) / 16;
-    {                                                // one row tile per wave; the barriers below are uniform
-        const int rt = split * 4 + wv;
-        const bool active = rt < n_tiles;
-        // ---- Q fragments (A operand): row rt*16 + r16, dims 32s + 8*g4 .. +8
-        f16x8 qa[ST];
-        {
-            const int row = rt * 16 + r16;
-            if (row < R) {
-                const int col = row / G, h = row - col * G;
-                const float *qp = a.q + (size_t)(gr.first_col + col) * a.NH * HD + (kvh * G + h) * HD;
+    const int rt = split * 4 + wv;                   // this wave's row tile
+    const bool active = rt < n_tiles;
+    const size_t head_base = ((size_t)gr.seq * a.NKV + kvh) * a.n_slots;
+    const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    // visible key j of the chunk (j < cnt): its cache slot and its ring position / tree code
+    auto key_at = [&](int j, int &kp) {
+        const int vis = v0 + j;
+        if (vis < gr.nlin) { kp = gr.lo + vis; return kp % a.n_slots; }
+        const int tj = vis - gr.nlin;
+        kp = -(1 + tj);
+        return (gr.tree_base + tj) % a.n_slots;
+    };
+
+    // ---- every global load before the first LDS store.  Keys past cnt load key 0 of the chunk (clamped address,
+    // unconditional load) and are replaced by zeros.  K: item i = key i / CPR, piece i % CPR.  V: item i = key pair
+    // i % 32, piece i / 32 (a wave's 64 items: 32 key pairs x 2 pieces, see the transposed store below).
+    f16x8 kf[KPER], vf[VPER][2];
 #pragma unroll
-                for (int s = 0; s < ST; ++s) {
-                    const f32x4 x0 = *(const f32x4 *)(qp + 32 * s + 8 * g4);
-                    const f32x4 x1 = *(const f32x4 *)(qp + 32 * s + 8 * g4 + 4);
-                    qa[s] = (f16x8){(f16)(x0[0] * a.scale), (f16)(x0[1] * a.scale), (f16)(x0[2] * a.scale),
-                                    (f16)(x0[3] * a.scale), (f16)(x1[0] * a.scale), (f16)(x1[1] * a.scale),
-                                    (f16)(x1[2] * a.scale), (f16)(x1[3] * a.scale)};
-                }
-            } else {
+    for (int i = 0; i < KPER; ++i) {
+        const int idx = tid + 256 * i, j = idx / CPR, ch = idx - j * CPR;
+        int kp;
+        const int slot = key_at(j < cnt ? j : 0, kp);
+        kf[i] = *(const f16x8 *)(a.kc + (head_base + slot) * HD + ch * 8);
+    }
 #pragma unroll
-                for (int s = 0; s < ST; ++s) qa[s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-            }
+    for (int i = 0; i < VPER; ++i) {
+        const int idx = tid + 256 * i, kp2 = idx & 31, ch = idx >> 5;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * kp2 + h;
+            int kp;
+            const int slot = key_at(j < cnt ? j : 0, kp);
+            vf[i][h] = *(const f16x8 *)(a.vc + (head_base + slot) * HD + ch * 8);
         }
-        // ---- S = Q K^T: 4 slot tiles of 16; lane holds S[row 4*g4 + j][slot 16*st + r16]
-        f32x4 sc[4];
+    }
+    // Q fragments (A operand) of row rt*16 + r16, dims 32s + 8*g4 .. +8, from a clamped row; rows past R are zero
+    f16x8 qa[ST];
+    {
+        const int row = rt * 16 + r16;
+        const int rowc = row < R ? row : R - 1;
+        const int col = rowc / G, h = rowc - col * G;
+        const float *qp = a.q + (size_t)(gr.first_col + col) * a.NH * HD + (kvh * G + h) * HD + 8 * g4;
+        f32x4 x[ST][2];
+#pragma unroll
+        for (int s = 0; s < ST; ++s) {
+            x[s][0] = *(const f32x4 *)(qp + 32 * s);
+            x[s][1] = *(const f32x4 *)(qp + 32 * s + 4);
+        }
+        const float qs = row < R ? a.scale : 0.f;
+#pragma unroll
+        for (int s = 0; s < ST; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qa[s][e] = (f16)(x[s][e >> 2][e & 3] * qs);
+    }
+    const sp_token ct = a.toks[gr.first_col + min(tid, gr.ncols - 1)];
+
+    // ---- LDS: K row-major; V transposed, two keys per dword: lane (key pair p, piece ch) writes the dword holding
+    // keys 2p, 2p+1 of dims 8ch .. 8ch+7.  A wave's 32 pairs x 2 pieces hit 64 distinct banks (the two pieces' rows
+    // are 8 * 36 dwords apart).
+#pragma unroll
+    for (int i = 0; i < KPER; ++i) {
+        const int idx = tid + 256 * i, j = idx / CPR, ch = idx - j * CPR;
+        *(f16x8 *)&k_s[j][ch * 8] = j < cnt ? kf[i] : zero8;
+    }
+#pragma unroll
+    for (int i = 0; i < VPER; ++i) {
+        const int idx = tid + 256 * i, kp2 = idx & 31, ch = idx >> 5;
+        const f16x8 va = 2 * kp2 < cnt ? vf[i][0] : zero8, vb = 2 * kp2 + 1 < cnt ? vf[i][1] : zero8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const f16x2 pr = (f16x2){va[e], vb[e]};
+            *(f16x2 *)&vt_s[ch * 8 + e][2 * kp2] = pr;
+        }
+    }
+    if (tid < ATT_CH) {
+        int kp = INT_MIN;
+        if (tid < cnt) (void)key_at(tid, kp);
+        kpos_s[tid] = kp;
+    }
+    if (tid < gr.ncols) { clo_s[tid] = ct.ctx_lo; chi_s[tid] = ct.ctx_hi; ctc_s[tid] = ct.tree_count; cmask_s[tid] = ct.tree_mask; }
+    __syncthreads();
+    if (!active) return;                             // no block-wide barrier follows
+
+    // ---- S = Q K^T: 4 slot tiles of 16; lane holds S[row 4*g4 + j][slot 16*st + r16]
+    f32x4 sc[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < ST; ++s) {
+            const f16x8 kb = *(const f16x8 *)&k_s[16 * st + r16][32 * s + 8 * g4];
+            acc = mfma16(qa[s], kb, acc);
+        }
+        sc[st] = acc;
+    }
+    // ---- mask, chunk-local max / exp / sum per row
+    float mrow[4], lrow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = rt * 16 + 4 * g4 + j;
+        const int col = row < R ? row / G : 0;
+        const int lo = clo_s[col], hi = chi_s[col], tc = ctc_s[col];
+        const unsigned long long mk = cmask_s[col];
+        float m = -INFINITY;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < ST; ++s) {
-                const f16x8 kb = *(const f16x8 *)&k_s[16 * st + r16][32 * s + 8 * g4];
-                acc = mfma16(qa[s], kb, acc);
-            }
-            sc[st] = acc;
+            const int kp = kpos_s[16 * st + r16];
+            bool ok = row < R && kp != INT_MIN;
+            if (ok) ok = kp >= 0 ? (kp >= lo && kp <= hi) : ((-kp - 1) < tc && ((mk >> (-kp - 1)) & 1ull));
+            const float v = ok ? sc[st][j] : -INFINITY;
+            sc[st][j] = v;
+            m = fmaxf(m, v);
         }
-        // ---- mask, chunk-local max / exp / sum per row
-        float mrow[4], lrow[4];
+        m = row16_max(m);
+        float l = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const float e = (m == -INFINITY || sc[st][j] == -INFINITY) ? 0.f : expf(sc[st][j] - m);
+            sc[st][j] = e;
+            l += e;
+        }
+        l = row16_sum(l);
+        mrow[j] = m; lrow[j] = l;
+    }
+    // ---- P (fp16) to this wave's LDS rows, read back as the A operand (LDS is in order within a wave)
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p_s[wv][4 * g4 + j][16 * st + r16] = (f16)sc[st][j];
+    __builtin_amdgcn_wave_barrier();
+    f16x8 pa[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) pa[s2] = *(const f16x8 *)&p_s[wv][r16][32 * s2 + 8 * g4];
+    // ---- O = P V over HD/16 dim tiles; lane holds O[row 4*g4 + j][dim 16*dt + r16]
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt) {
+        f32x4 o = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const f16x8 vb = *(const f16x8 *)&vt_s[16 * dt + r16][32 * s2 + 8 * g4];
+            o = mfma16(pa[s2], vb, o);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = rt * 16 + 4 * g4 + j;
-            const int col = row < R ? row / G : 0;
-            const int lo = clo_s[col], hi = chi_s[col], tc = ctc_s[col];
-            const unsigned long long mk = cmask_s[col];
-            float m = -INFINITY;
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const int kp = kpos_s[16 * st + r16];
-                bool ok = row < R && kp != INT_MIN;
-                if (ok) ok = kp >= 0 ? (kp >= lo && kp <= hi) : ((-kp - 1) < tc && ((mk >> (-kp - 1)) & 1ull));
-                const float v = ok ? sc[st][j] : -INFINITY;
-                sc[st][j] = v;
-                m = fmaxf(m, v);
-            }
-            m = row16_max(m);
-            float l = 0.f;
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const float e = (m == -INFINITY || sc[st][j] == -INFINITY) ? 0.f : expf(sc[st][j] - m);
-                sc[st][j] = e;
-                l += e;
-            }
-            l = row16_sum(l);
-            mrow[j] = m; lrow[j] = l;
-        }
-        // ---- P (fp16) to LDS in row-major, read back as the A operand
-        if (active) {
-#pragma unroll
-            for (int st = 0; st < 4; ++st)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) p_s[wv][4 * g4 + j][16 * st + r16] = (f16)sc[st][j];
-        }
-        __syncthreads();
-        if (active) {
-        f16x8 pa[2];
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) pa[s2] = *(const f16x8 *)&p_s[wv][r16][32 * s2 + 8 * g4];
-        // ---- O = P V over HD/16 dim tiles; lane holds O[row 4*g4 + j][dim 16*dt + r16]
-#pragma unroll
-        for (int dt = 0; dt < HD / 16; ++dt) {
-            f32x4 o = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                const f16x8 vb = *(const f16x8 *)&vt_s[16 * dt + r16][32 * s2 + 8 * g4];
-                o = mfma16(pa[s2], vb, o);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int row = rt * 16 + 4 * g4 + j;
-                if (row < R) {
-                    const int col = row / G, h = row - col * G;
-                    float *out = a.part + (((size_t)(gr.first_col + col) * a.NH + kvh * G + h) * a.nchunk + c) * (HD + 2);
-                    out[2 + 16 * dt + r16] = o[j];
-                    if (dt == 0 && r16 == 0) { out[0] = mrow[j]; out[1] = lrow[j]; }
-                }
+            if (row < R) {
+                const int col = row / G, h = row - col * G;
+                float *out = a.part + (((size_t)(gr.first_col + col) * a.NH + kvh * G + h) * a.nchunk + c) * (HD + 2);
+                out[2 + 16 * dt + r16] = o[j];
+                if (dt == 0 && r16 == 0) { out[0] = mrow[j]; out[1] = lrow[j]; }
             }
         }
-        }
-        __syncthreads();
     }
 }

@@ -125,7 +125,9 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok) {
 #endif
     p.s = s;
     p.kslice = (m.nkt + s - 1) / s;
-    int nw = std::min(p.kslice, mt > 1 && p.kslice >= 32 ? 8 : 4);
+    // several column tiles: 8 waves for the layer matrices (split or paired; shape sweeps at 16 and 33 columns),
+    // 4 for the unsplit head, whose blocks are many already
+    int nw = std::min(p.kslice, mt > 1 && (p.kslice >= 32 || s > 1 || m.paired) ? 8 : 4);
 #ifdef SP_GEMV_TUNE
     if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 4 : 8);
 #endif
