@@ -62,8 +62,10 @@ enum {
     SP_F_LOGITS = 1,      /* run the final norm + LM head and produce fp32 logits for every column   */
     SP_F_ARGMAX = 2,      /* also produce the greedy id per column (first index on ties)             */
     SP_F_GRAPH = 4,       /* capture the step into a hipGraph on first use and replay it afterwards  */
-    SP_F_PERSISTENT = 8   /* one decode column without a tree: run the whole step as one persistent   */
+    SP_F_PERSISTENT = 8,  /* one decode column without a tree: run the whole step as one persistent   */
                           /* cooperative kernel when the model fits it (else the kernel chain runs)  */
+    SP_F_UNFUSED = 16     /* one column: run every RMSNorm and attention combine as a kernel of its   */
+                          /* own instead of inside the next GEMV (same results; for checking)        */
 };
 
 typedef struct sp_model_desc {

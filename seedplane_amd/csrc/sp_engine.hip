@@ -107,7 +107,9 @@ int g_tune[3] = {0, 0, 0};
 // groups (qkv, o, down) are split along K into slices that the consuming kernel adds up; the LM head and the wider
 // column tiles give each wave two row groups (R = 2: twice the loads in flight per wave, half the activation reads
 // per weight byte).
-GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok) {
+// `slices` / `waves` (> 0) replace the slice count and wave count of the heuristic (single-column steps, whose
+// residual must reach the next norm in few slices).
+GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int waves = 0) {
     GemvPlan p;
     p.rg = m.paired ? 2 : 1;
     p.units = m.rows_pad / 16 / p.rg;
@@ -118,6 +120,7 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok) {
         s = std::max(1, 2048 / (p.units / p.r));
         s = std::min(s, std::max(1, m.nkt / 2));
         s = std::min(s, mt == 1 ? GEMV_MAX_SLICES : 4);
+        if (slices > 0) s = std::min(slices, std::max(1, m.nkt / 2));
     }
 #ifdef SP_GEMV_TUNE
     if (g_tune[0] > 0 && p.units % g_tune[0] == 0) p.r = g_tune[0];
@@ -128,9 +131,11 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok) {
     // several column tiles: 8 waves for the layer matrices (split or paired; shape sweeps at 16 and 33 columns),
     // 4 for the unsplit head, whose blocks are many already
     int nw = std::min(p.kslice, mt > 1 && (p.kslice >= 32 || s > 1 || m.paired) ? 8 : 4);
+    if (waves > 0) nw = std::min(p.kslice, std::min(waves, mt == 1 ? 16 : 8));
 #ifdef SP_GEMV_TUNE
-    if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 4 : 8);
+    if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 16 : 8);
 #endif
+    if (mt == 1 && p.r > 1) nw = std::min(nw, 4);
     while (nw > 1 && (size_t)nw * p.r * p.rg * mt * 1024 > GEMV_MAX_LDS) --nw;
     p.nw = std::max(1, nw);
     return p;
@@ -156,24 +161,66 @@ void launch_gemv_fmt(int mt, bool paired, int r, dim3 grid, dim3 block, size_t s
     }
 }
 
+template <int FMT>
+void launch_gemv_pro_fmt(bool paired, int pro, dim3 grid, size_t smem, hipStream_t st, const GemvArgs &a,
+                         const ProArgs &pa) {
+    const dim3 block(pro_threads(pro));
+    if (pro == PRO_NORM) {
+        if (paired) hipLaunchKernelGGL((k_gemv_pro<FMT, 2, PRO_NORM>), grid, block, smem, st, a, pa);
+        else hipLaunchKernelGGL((k_gemv_pro<FMT, 1, PRO_NORM>), grid, block, smem, st, a, pa);
+    } else {
+        if (paired) hipLaunchKernelGGL((k_gemv_pro<FMT, 2, PRO_COMB>), grid, block, smem, st, a, pa);
+        else hipLaunchKernelGGL((k_gemv_pro<FMT, 1, PRO_COMB>), grid, block, smem, st, a, pa);
+    }
+}
+
+static_assert(GEMV_MAX_SLICES <= PRO_MAX_SLICES, "a norm prologue adds at most PRO_MAX_SLICES pending slices");
+// A prologue GEMV takes one column, one row unit per block and (norm) a hidden size up to PRO_NORM_HMAX.
+// (The packer makes K an exact multiple of the k-tile, so a block's k-range never passes H or NH * HD.)
+bool gemv_pro_ok(const DevMat &m, int pro, int H, int HD, int slices = 0, int waves = 0) {
+    if (pro == PRO_NONE) return true;
+    const GemvPlan p = plan_gemv(m, 1, true, slices, waves);
+    const int nt = pro_threads(pro);
+    if (p.r != 1 || p.nw > nt / 64) return false;
+    if (pro == PRO_NORM && (H > PRO_NORM_HMAX || H < 1)) return false;
+    if (pro == PRO_COMB && (HD < 64 || HD > nt || nt % HD != 0 || HD % 64 != 0)) return false;
+    return true;
+}
+
 // Launches y = W x for mcols columns.  With `part` given (and a matrix that is not the SwiGLU pair) the plan may
 // split K: the kernel then writes raw slices to part[s][m][ldo] and the return value is the slice count that the
-// consumer must add (plus the bias, for EPI_STORE); otherwise the epilogue is applied and 0 is returned.
+// consumer must add (plus the bias, for EPI_STORE); otherwise the epilogue is applied and 0 is returned.  With a
+// prologue (pro != PRO_NONE, one column) the activations come from *pa instead of x.
 int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, float *out_f32, f16 *out_f16, int ldo,
-                const float *bias, hipStream_t st, float *part = nullptr, size_t pstride = 0) {
+                const float *bias, hipStream_t st, float *part = nullptr, size_t pstride = 0, int pro = PRO_NONE,
+                const ProArgs *pa = nullptr, int slices = 0, int waves = 0) {
     require(mcols >= 1 && mcols <= 16 * GEMV_MAX_MT, SP_EINVAL, "gemv columns out of range");
     require((epi == EPI_SILU) == m.paired, SP_EINVAL, "gemv epilogue does not match the matrix packing");
+    require(pro == PRO_NONE || (mcols == 1 && pa), SP_EINVAL, "gemv prologue needs one column and its arguments");
     const int mt = (mcols + 15) / 16;
-    const GemvPlan p = plan_gemv(m, mt, part != nullptr);
+    const GemvPlan p = plan_gemv(m, mt, part != nullptr, slices, waves);
     require(p.units % p.r == 0 && p.s >= 1 && p.s <= GEMV_MAX_SLICES, SP_EINVAL, "gemv plan out of range");
     GemvArgs a;
     a.w = m.w; a.sz = m.sz; a.nkt = m.nkt; a.units = p.units;
     a.n_real = m.paired ? m.rows / 2 : m.rows;
     a.x = x; a.ldx = ldx; a.m = mcols;
     a.out_f32 = out_f32; a.out_f16 = out_f16; a.ldo = ldo; a.bias = bias; a.epi = epi;
-    a.kslice = p.kslice; a.pstride = pstride;
+    a.kslice = p.kslice; a.pstride = pstride; a.nwk = p.nw;
     if (p.s > 1) { a.epi = EPI_PART; a.out_f32 = part; a.bias = nullptr; }
     dim3 grid(p.units / p.r, p.s), block(64 * p.nw);
+    if (pro != PRO_NONE) {
+        require(p.r == 1 && p.nw <= pro_threads(pro) / 64, SP_EINVAL, "gemv prologue plan out of range");
+        const int kt = m.fmt == 1 ? 32 : (m.fmt == 2 ? 64 : 128);
+        const size_t klen = ((size_t)p.kslice * kt + 7) & ~(size_t)7;
+        const size_t smem = (size_t)p.nw * p.rg * 1024 + klen * 2 + (size_t)pro_scratch_floats(pro, pa->H, pa->HD) * 4;
+        require(smem <= GEMV_MAX_LDS, SP_EINVAL, "gemv prologue LDS out of range");
+        switch (m.fmt) {
+            case 1: launch_gemv_pro_fmt<1>(m.paired, pro, grid, smem, st, a, *pa); break;
+            case 2: launch_gemv_pro_fmt<2>(m.paired, pro, grid, smem, st, a, *pa); break;
+            default: launch_gemv_pro_fmt<3>(m.paired, pro, grid, smem, st, a, *pa); break;
+        }
+        return p.s > 1 ? p.s : 0;
+    }
     const size_t smem = p.nw > 1 ? (size_t)p.nw * p.r * p.rg * mt * 64 * 16 : 0;
     switch (m.fmt) {
         case 1: launch_gemv_fmt<1>(mt, m.paired, p.r, grid, block, smem, st, a); break;
@@ -315,6 +362,10 @@ struct sp_engine {
     float *x = nullptr, *qkv = nullptr, *q = nullptr, *logits = nullptr, *attn_part = nullptr;
     float *gpart = nullptr;      // split-K GEMV slices [GEMV_MAX_SLICES][maxT][max(H, Nqkv)]
     size_t gpart_stride = 0;
+    // single-column steps with the norms / combine folded into the GEMVs: the residual alternates between x (layer
+    // boundaries) and x2 (after the input norm), and the qkv slices go to gpart2 while the down slices in gpart are
+    // still being read
+    float *x2 = nullptr, *gpart2 = nullptr;
     f16 *xn = nullptr, *attn = nullptr, *act = nullptr;
     float *am_v = nullptr;
     int *am_i = nullptr, *am_out = nullptr;
@@ -377,7 +428,8 @@ void sp_engine::free_all() {
     layers.clear();
     embed.release(); head.release();
     dev_free(final_norm); dev_free(inv_freq);
-    for (void *p : {(void *)x, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)gpart, (void *)xn, (void *)attn,
+    for (void *p : {(void *)x, (void *)x2, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)gpart,
+                    (void *)gpart2, (void *)xn, (void *)attn,
                     (void *)act, (void *)am_v, (void *)am_i, (void *)am_out,
                     (void *)dtoks, (void *)dgroups, (void *)dcolnc, (void *)d_kl, (void *)d_vl, (void *)d_move})
         dev_free(p);
@@ -402,6 +454,8 @@ void sp_engine::alloc_activations() {
     qkv = dev_alloc<float>((size_t)maxT * Nqkv);
     gpart_stride = (size_t)maxT * std::max(H, Nqkv);
     gpart = dev_alloc<float>(GEMV_MAX_SLICES * gpart_stride);
+    gpart2 = dev_alloc<float>(GEMV_MAX_SLICES * gpart_stride);
+    x2 = dev_alloc<float>((size_t)maxT * H);
     q = dev_alloc<float>((size_t)maxT * d.n_heads * d.head_dim);
     attn = dev_alloc<f16>((size_t)maxT * d.n_heads * d.head_dim);
     act = dev_alloc<f16>((size_t)maxT * I);
@@ -693,11 +747,37 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
     const bool logits_on = flags & SP_F_LOGITS;
     const size_t ps = gpart_stride;
     int pend = 0;     // residual slices of a split-K o / down GEMV waiting in gpart (added by the next RMSNorm)
+    // One column: the input RMSNorm runs as the prologue of the qkv GEMV and the attention combine as the prologue of
+    // o_proj (two launches fewer per layer); qkv and the down projection run in ONE_SLICES k-slices, so the prologue
+    // adds few pending slices (launch-shape sweeps: as fast as the many-slice plans with 8 / 16 waves per block).
+    // The prologue writes the updated residual to the other one of x / x2 (its blocks still read the first), so the
+    // residual changes buffer at every layer; the qkv slices go to gpart2 while the blocks still read the down slices
+    // in gpart.  SP_F_UNFUSED keeps the plans and runs the norm and the combine as kernels of their own.
+    constexpr int ONE_SLICES = 2, ONE_QKV_WAVES = 8, ONE_DOWN_WAVES = 16;
+    const bool one = n == 1 && !layers.empty() && gemv_pro_ok(layers[0].qkv, PRO_NORM, H, HD, ONE_SLICES, ONE_QKV_WAVES) &&
+                     gemv_pro_ok(layers[0].o, PRO_COMB, H, HD);
+    const bool fuse = one && !(flags & SP_F_UNFUSED);
+    const int qkv_s = one ? ONE_SLICES : 0, qkv_w = one ? ONE_QKV_WAVES : 0;
+    const int down_s = one ? ONE_SLICES : 0, down_w = one ? ONE_DOWN_WAVES : 0;
+    float *const qpart = fuse ? gpart2 : gpart;
+    float *res = x;                             // residual at the start of the layer
     for (int l = 0; l < d.n_layers; ++l) {
         Layer &ly = layers[l];
-        launch_rmsnorm(n, x, H, gpart, pend, ps, ly.in_norm, d.rms_eps, xn, st);
-        const int sq = launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, gpart, ps);
-        RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots, gpart, ps, ly.qkv_b};
+        float *rmid = res;                      // residual after the input norm
+        int sq;
+        if (fuse) {
+            rmid = res == x ? x2 : x;
+            ProArgs pn{};
+            pn.res = res; pn.res_out = rmid; pn.part = gpart; pn.pstride = ps; pn.np = pend; pn.w = ly.in_norm;
+            pn.eps = d.rms_eps; pn.H = H;
+            sq = launch_gemv(ly.qkv, EPI_STORE, nullptr, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, qpart, ps, PRO_NORM, &pn,
+                             qkv_s, qkv_w);
+        } else {
+            launch_rmsnorm(n, res, H, gpart, pend, ps, ly.in_norm, d.rms_eps, xn, st);
+            sq = launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, qpart, ps, PRO_NONE, nullptr,
+                             qkv_s, qkv_w);
+        }
+        RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots, qpart, ps, ly.qkv_b};
         const bool fused = ap.rope_fused && logits_on;
         if (!fused) launch_rope(n, ra, sq, st);
         if (l + 1 == d.n_layers && !logits_on) break;   // K/V-only: the last layer only needs its K/V
@@ -722,16 +802,24 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
             if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
             else launch_attn_hd<128>(G, agrid, st, aa);
         }
-        if (!ap.dec_direct)
-            hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn, NH * HD);
-        pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, x, nullptr, H, nullptr, st, gpart, ps);
-        launch_rmsnorm(n, x, H, gpart, pend, ps, ly.post_norm, d.rms_eps, xn, st);
+        if (fuse && !ap.dec_direct) {
+            ProArgs pc{};
+            pc.apart = attn_part; pc.colnc = dcolnc; pc.NH = NH; pc.HD = HD; pc.nchunk = nchunk;
+            pend = launch_gemv(ly.o, EPI_RESID, nullptr, NH * HD, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_COMB, &pc);
+        } else {
+            if (!ap.dec_direct)
+                hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn, NH * HD);
+            pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, rmid, nullptr, H, nullptr, st, gpart, ps);
+        }
+        launch_rmsnorm(n, rmid, H, gpart, pend, ps, ly.post_norm, d.rms_eps, xn, st);
         launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, st);
-        pend = launch_gemv(ly.down, EPI_RESID, act, I, n, x, nullptr, H, nullptr, st, gpart, ps);
+        pend = launch_gemv(ly.down, EPI_RESID, act, I, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_NONE, nullptr,
+                           down_s, down_w);
+        res = rmid;
     }
     if (logits_on) {
         const DevMat &hm = d.tied_head ? embed : head;
-        launch_rmsnorm(n, x, H, gpart, pend, ps, final_norm, d.rms_eps, xn, st);
+        launch_rmsnorm(n, res, H, gpart, pend, ps, final_norm, d.rms_eps, xn, st);
         launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, st);
         if (flags & SP_F_ARGMAX) {
             hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, n), dim3(256), 0, st, logits, d.vocab, d.vocab, am_v, am_i);
@@ -920,7 +1008,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             require(nlin + t.tree_count >= 1, SP_EINVAL, "a column must see at least one key");
         }
         const bool use_graph = flags & SP_F_GRAPH;
-        const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX);
+        const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX | SP_F_UNFUSED);
         if (n == 1 && (flags & SP_F_PERSISTENT)) {
             if (e->persistent_step(toks[0], sflags, logits_dev, argmax_host)) {
                 e->last_path = 1;

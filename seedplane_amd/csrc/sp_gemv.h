@@ -21,6 +21,7 @@
 // exactly and only the activations are rounded (to fp16).
 #pragma once
 #include "sp_device.h"
+#include "sp_attn.h"
 
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_PART = 3 };
 
@@ -40,6 +41,7 @@ struct GemvArgs {
     int epi;
     int kslice;            // k-tiles per slice
     size_t pstride;        // EPI_PART: floats between slices
+    int nwk;               // prologue kernels: waves that take k-tiles (the others only help with the prologue)
 };
 template <int FMT>
 __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
@@ -52,10 +54,11 @@ __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
     }
 }
 
-// Threads per block: single-column-tile variants use up to 4 waves, wider ones up to 8 (each wave may then hold up to
-// 256 VGPRs: the weight tiles and activation fragments of a whole batch stay in registers without spilling).
+// Threads per block: single-column-tile variants with one unit per block use up to 16 waves (128 VGPRs each), those
+// with two units up to 4, wider ones up to 8 (each wave may then hold up to 256 VGPRs: the weight tiles and
+// activation fragments of a whole batch stay in registers).
 // TB = k-tiles per wave whose loads are in flight together.
-template <int MT> struct GemvLimits { static constexpr int MAX_THREADS = MT == 1 ? 256 : 512; };
+template <int MT, int R> struct GemvLimits { static constexpr int MAX_THREADS = MT == 1 ? (R == 1 ? 1024 : 256) : 512; };
 template <int FMT, int MT> struct GemvBatch { static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : 4) : 2; };
 
 // Lane holds D[m = mt*16 + 4g + j][n = unit*16 + r], j < 4.  Operands the epilogue reads (bias, the residual) are
@@ -97,14 +100,171 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int unit, int m
     }
 }
 
-template <int FMT, int MT, int RG, int R>
-__global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
+// ---------------------------------------------------------------------------------------------------------------
+// Activation prologues (one column).  The block builds the fp16 activations of its own k-range in LDS, so the kernel
+// that would have produced them (the RMSNorm before qkv / gate_up, the attention combine before o_proj) does not run
+// on its own; the block's first batch of weight loads is issued before the prologue and streams in meanwhile.  Both
+// prologues repeat the arithmetic of the kernel they stand in for operation by operation (same element sums, same
+// reduction trees), so a step gives bit-identical results with and without them.  Prologue kernels run pro_threads()
+// threads (the norm prologue needs 8 waves for the qkv plan; the combine prologue is fastest with 4); the first
+// a.nwk waves take the k-tiles, exactly as a plain launch with a.nwk waves would.
+enum { PRO_NONE = 0, PRO_NORM = 1, PRO_COMB = 2 };
+__host__ __device__ constexpr int pro_threads(int pro) { return pro == PRO_NORM ? 512 : 256; }
+constexpr int PRO_NORM_HMAX = 2048;         // hidden sizes the norm prologue takes (PRO_NORM_HMAX / 512 per thread)
+constexpr int PRO_MAX_SLICES = 8;           // pending residual slices
+struct ProArgs {
+    // PRO_NORM: v = res + part[0] + ... + part[np - 1] (slice order); act = fp16((v * rs) * w) with
+    // rs = 1 / sqrt(mean(v^2) + eps) (k_rmsnorm); block (0, 0) writes v to res_out, a buffer the blocks do not read
+    const float *res;
+    float *res_out;
+    const float *part;
+    size_t pstride;
+    int np;
+    const float *w;
+    float eps;
+    int H;
+    // PRO_COMB: act = the attention partials [NH][nchunk][HD + 2] of column 0 merged as k_attn_combine merges them
+    const float *apart;
+    const int *colnc;
+    int NH, HD, nchunk;
+};
+// LDS floats a prologue needs beyond the activations
+__host__ __device__ inline int pro_scratch_floats(int pro, int H, int HD) {
+    if (pro == PRO_NORM) return H + 16;
+    if (pro == PRO_COMB) return (pro_threads(PRO_COMB) / HD) * (2 * ATT_MAX_CHUNKS + 16);
+    return 0;
+}
+
+__device__ __forceinline__ void pro_norm(const ProArgs &p, f16 *act, int klo, int klen, float *scr) {
+    constexpr int PRO_THREADS = pro_threads(PRO_NORM), PRO_QMAX = PRO_NORM_HMAX / PRO_THREADS;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, H = p.H;
+    float *v_s = scr, *red = scr + H;
+    const bool has_part = p.np > 0;
+    const int last = max(p.np, 1) - 1;
+    // every load first, from clamped addresses: the residual, the slices, the weights of this block's k-range
+    float xv[PRO_QMAX], wk[PRO_QMAX], pv[PRO_MAX_SLICES][PRO_QMAX];
+#pragma unroll
+    for (int q = 0; q < PRO_QMAX; ++q) {
+        xv[q] = p.res[min(tid + PRO_THREADS * q, H - 1)];
+        wk[q] = p.w[min(klo + tid + PRO_THREADS * q, H - 1)];
+    }
+    if (has_part) {
+#pragma unroll
+        for (int s = 0; s < PRO_MAX_SLICES; ++s)
+#pragma unroll
+            for (int q = 0; q < PRO_QMAX; ++q)
+                pv[s][q] = p.part[(size_t)min(s, last) * p.pstride + min(tid + PRO_THREADS * q, H - 1)];
+    }
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+    for (int q = 0; q < PRO_QMAX; ++q) {
+        const int k = tid + PRO_THREADS * q;
+        float v = xv[q];
+        if (has_part) {
+#pragma unroll
+            for (int s = 0; s < PRO_MAX_SLICES; ++s)
+                if (s < p.np) v += pv[s][q];
+        }
+        if (k < H) {
+            v_s[k] = v;
+            if (writer) p.res_out[k] = v;
+        }
+    }
+    __syncthreads();
+    // k_rmsnorm's reduction: virtual thread t < NORM_THREADS squares and sums elements t + NORM_THREADS * i (zeros
+    // past H); real wave w plays virtual waves w, w + PRO_THREADS / 64, ...; the 16 DPP wave sums are then added in
+    // order
+#pragma unroll
+    for (int j = 0; j < NORM_THREADS / PRO_THREADS; ++j) {
+        const int vt = tid + PRO_THREADS * j;
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NORM_PER_THREAD; ++i) {
+            const int k = vt + NORM_THREADS * i;
+            const float v = k < H ? v_s[k] : 0.f;
+            ss += v * v;
+        }
+        ss = wave_sum_dpp(ss);
+        if (lane == 0) red[wv + (PRO_THREADS / 64) * j] = ss;
+    }
+    __syncthreads();
+    float tot = 0.f;
+    for (int j = 0; j < NORM_THREADS / 64; ++j) tot += red[j];
+    const float rs = 1.0f / sqrtf(tot / (float)H + p.eps);
+#pragma unroll
+    for (int q = 0; q < PRO_QMAX; ++q) {
+        const int e = tid + PRO_THREADS * q;
+        if (e < klen) act[e] = (f16)((v_s[klo + e] * rs) * wk[q]);
+    }
+    __syncthreads();
+}
+
+// Heads overlapping the k-range, pro_threads(PRO_COMB) / HD at a time: thread group g of HD threads plays
+// k_attn_combine's block for head h0 + g.
+__device__ __forceinline__ void pro_comb(const ProArgs &p, f16 *act, int klo, int klen, float *scr) {
+    constexpr int PRO_THREADS = pro_threads(PRO_COMB);
+    const int HD = p.HD, tid = threadIdx.x, lane = tid & 63;
+    const int ngrp = PRO_THREADS / HD, grp = tid / HD, gt = tid - grp * HD, gw = gt >> 6, gnw = HD / 64;
+    float *w_s = scr + grp * 2 * ATT_MAX_CHUNKS, *l_s = w_s + ATT_MAX_CHUNKS;
+    float *red = scr + ngrp * 2 * ATT_MAX_CHUNKS + grp * 16;
+    const int h_lo = klo / HD, h_hi = (klo + klen - 1) / HD;
+    const int nc = p.colnc[0], last = max(nc - 1, 0);
+    for (int h0 = h_lo; h0 <= h_hi; h0 += ngrp) {
+        const bool live = h0 + grp <= h_hi;
+        const int h = min(h0 + grp, h_hi);
+        const float *pp = p.apart + (size_t)h * p.nchunk * (HD + 2);
+        float v[CMB_BATCH];
+#pragma unroll
+        for (int i = 0; i < CMB_BATCH; ++i) v[i] = pp[(size_t)min(i, last) * (HD + 2) + 2 + gt];
+        float mloc = -INFINITY;
+        for (int c = gt; c < nc; c += HD) {
+            const float mc = pp[(size_t)c * (HD + 2)], lc = pp[(size_t)c * (HD + 2) + 1];
+            w_s[c] = lc > 0.f ? mc : -INFINITY;
+            l_s[c] = lc;
+            mloc = fmaxf(mloc, w_s[c]);
+        }
+        mloc = wave_max_dpp(mloc);
+        if (lane == 0) red[gw] = mloc;
+        __syncthreads();
+        float M = red[0];
+        for (int i = 1; i < gnw; ++i) M = fmaxf(M, red[i]);
+        float lsum = 0.f;
+        for (int c = gt; c < nc; c += HD) {
+            const float wc = w_s[c] == -INFINITY ? 0.f : expf(w_s[c] - M);
+            w_s[c] = wc;
+            lsum += wc * l_s[c];
+        }
+        __syncthreads();
+        lsum = wave_sum_dpp(lsum);
+        __syncthreads();
+        if (lane == 0) red[8 + gw] = lsum;
+        __syncthreads();
+        float L = 0.f;
+        for (int j = 0; j < gnw; ++j) L += red[8 + j];
+        float acc = 0.f;
+        for (int c0 = 0; c0 < nc; c0 += CMB_BATCH) {
+            if (c0 > 0) {
+#pragma unroll
+                for (int i = 0; i < CMB_BATCH; ++i) v[i] = pp[(size_t)min(c0 + i, last) * (HD + 2) + 2 + gt];
+            }
+#pragma unroll
+            for (int i = 0; i < CMB_BATCH; ++i)
+                if (c0 + i < nc) acc += w_s[c0 + i] * v[i];
+        }
+        const int k = h * HD + gt;
+        if (live && k >= klo && k < klo + klen) act[k - klo] = (f16)(acc / L);
+        __syncthreads();                               // w_s / red are reused by the next heads
+    }
+}
+
+template <int FMT, int MT, int RG, int R, int PRO>
+__device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, unsigned char *smem_raw) {
     constexpr int KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
     constexpr int TB = GemvBatch<FMT, MT>::TB;
     constexpr int NR = R * RG;                 // row groups per wave
-    const int NW = blockDim.x >> 6;
+    const int NW = PRO == PRO_NONE ? (int)(blockDim.x >> 6) : a.nwk;   // waves taking k-tiles
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const bool worker = PRO == PRO_NONE || wv < NW;
     const int r = lane & 15, g = lane >> 4;
     const int u0 = blockIdx.x * R;
     const int k0 = blockIdx.y * a.kslice;
@@ -134,13 +294,15 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
         xon[mt] = m < a.m;
         xrow[mt] = a.x + (size_t)(xon[mt] ? m : 0) * a.ldx + 8 * g;
     }
+    // LDS: [cross-wave reduction: NW x NR x MT x 1 KiB][prologue: activations of the k-range, scratch]
+    f32x4 *red = (f32x4 *)smem_raw;
+    f16 *act = (f16 *)(smem_raw + (size_t)NW * NR * MT * 1024);
+    const int klen = (k1 - k0) * KT;
 
-    for (int kb = k0 + wv; kb < k1; kb += NW * TB) {
-        // ---- issue the weight and activation loads of TB k-tiles before anything is consumed
-        u32x4 wt[TB][NR];
-        uint32_t sq8[TB][NR];
-        u32x4 sq4[TB][NR];
-        f16x8 xa[TB][MT][ST];
+    u32x4 wt[TB][NR];
+    uint32_t sq8[TB][NR];
+    u32x4 sq4[TB][NR];
+    auto load_weights = [&](int kb) {
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
             const int kt = kb + t * NW;
@@ -151,11 +313,33 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
                 if constexpr (FMT == 2) sq8[t][i] = *((const uint32_t *)(sbase[i] + (size_t)kt * 32) + r);
                 if constexpr (FMT == 3) sq4[t][i] = *((const u32x4 *)(sbase[i] + (size_t)kt * 128) + r);
             }
+        }
+    };
+    if constexpr (PRO != PRO_NONE) {
+        if (worker && k0 + wv < k1) load_weights(k0 + wv);
+        float *scr = (float *)(act + ((klen + 7) & ~7));
+        if constexpr (PRO == PRO_NORM) pro_norm(p, act, k0 * KT, klen, scr);
+        else pro_comb(p, act, k0 * KT, klen, scr);
+    }
+
+    if (worker) {
+    for (int kb = k0 + wv; kb < k1; kb += NW * TB) {
+        // ---- issue the weight and activation loads of TB k-tiles before anything is consumed
+        if (PRO == PRO_NONE || kb != k0 + wv) load_weights(kb);
+        f16x8 xa[TB][MT][ST];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            const int kt = kb + t * NW;
+            if (kt >= k1) break;
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int s = 0; s < ST; ++s)
-                    xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(xrow[mt] + kt * KT + s * 32) : zero8;
+                for (int s = 0; s < ST; ++s) {
+                    if constexpr (PRO == PRO_NONE)
+                        xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(xrow[mt] + kt * KT + s * 32) : zero8;
+                    else
+                        xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(act + (kt - k0) * KT + s * 32 + 8 * g) : zero8;
+                }
         }
         // ---- MFMA per quant block
 #pragma unroll
@@ -196,22 +380,26 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
             }
         }
     }
+    }
 
     // ---- one wave: finish in registers; several: reduce through LDS in wave order, wave w finishing the (unit,
     // column tile) outputs w, w + NW, ...   Lane holds D[m = mt*16 + 4g + j][n = unit*16 + r].
     if (NW == 1) {
+        if (wv != 0) return;
 #pragma unroll
         for (int rr = 0; rr < R; ++rr)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) gemv_epilogue<RG>(a, u0 + rr, mt, acc[rr * RG][mt], acc[rr * RG + RG - 1][mt]);
         return;
     }
-    f32x4 *red = (f32x4 *)smem_raw;   // [NW][NR*MT][64]
+    if (worker) {
 #pragma unroll
-    for (int i = 0; i < NR; ++i)
+        for (int i = 0; i < NR; ++i)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) red[(wv * NR * MT + i * MT + mt) * 64 + lane] = acc[i][mt];
+            for (int mt = 0; mt < MT; ++mt) red[(wv * NR * MT + i * MT + mt) * 64 + lane] = acc[i][mt];
+    }
     __syncthreads();
+    if (!worker) return;
     for (int o = wv; o < R * MT; o += NW) {
         const int rr = o / MT, mt = o - rr * MT;
         f32x4 v[RG];
@@ -224,4 +412,17 @@ __global__ void __launch_bounds__(GemvLimits<MT>::MAX_THREADS) k_gemv(GemvArgs a
         }
         gemv_epilogue<RG>(a, u0 + rr, mt, v[0], v[RG - 1]);
     }
+}
+
+template <int FMT, int MT, int RG, int R>
+__global__ void __launch_bounds__((GemvLimits<MT, R>::MAX_THREADS)) k_gemv(GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    gemv_run<FMT, MT, RG, R, PRO_NONE>(a, ProArgs{}, smem_raw);
+}
+
+// One column with an activation prologue (PRO_NORM before qkv / gate_up, PRO_COMB before o_proj).
+template <int FMT, int RG, int PRO>
+__global__ void __launch_bounds__(pro_threads(PRO)) k_gemv_pro(GemvArgs a, ProArgs p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    gemv_run<FMT, 1, RG, 1, PRO>(a, p, smem_raw);
 }
