@@ -45,7 +45,8 @@ __global__ void __launch_bounds__(256) k_embed(const uint8_t *w, const f16 *sz, 
 constexpr int NORM_THREADS = 1024, NORM_PER_THREAD = 4;
 template <int NP>
 __global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, const float *part, size_t pstride,
-                                                          const float *w, int H, float eps, f16 *out, int ldo) {
+                                                          const float *w, int H, float eps, f16 *out, int ldo,
+                                                          int mtp) {
     __shared__ float red[16];
     const int b = blockIdx.x;
     float *xr = x + (size_t)b * ldx;
@@ -75,7 +76,7 @@ __global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, con
 #pragma unroll
     for (int i = 0; i < NORM_PER_THREAD; ++i) {
         const int k = threadIdx.x + i * NORM_THREADS;
-        if (k < H) out[(size_t)b * ldo + k] = (f16)((v[i] * rs) * wk[i]);
+        if (k < H) out[act_off(b, k, ldo, mtp)] = (f16)((v[i] * rs) * wk[i]);
     }
 }
 
@@ -368,7 +369,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
 // k_attn_part's layout and k_attn_combine merges the splits.
 constexpr int DEC_KC = 32;
 template <int HD, int NWV, int SUB>
-__global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int ldo, int direct) {
+__global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int ldo, int direct, int mtp) {
     constexpr int DEC_WAVES = NWV, DEC_SUB = SUB, DEC_KW = DEC_KC * SUB, DEC_KB = NWV * DEC_KW;
     constexpr int ST = HD / 32, NDT = HD / 16, KP = DEC_KC + 8;
     constexpr int VPL = HD / 2 / 8;                          // 16-byte V pieces per lane per sub-chunk
@@ -498,7 +499,7 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
             }
         }
         if (direct) {
-            out[(size_t)b * ldo + (kvh * G + h) * HD + d] = (f16)(acc / L);
+            out[act_off(b, (kvh * G + h) * HD + d, ldo, mtp)] = (f16)(acc / L);
         } else {
             float *pp = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + split) * (HD + 2);
             pp[2 + d] = acc;
@@ -513,7 +514,7 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
 // before the weights are known); the accumulation runs over the chunks in ascending order.
 constexpr int CMB_BATCH = 16;
 __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const int *col_nchunk, int NH, int HD,
-                                                      int nchunk, f16 *out, int ldo) {
+                                                      int nchunk, f16 *out, int ldo, int mtp) {
     __shared__ float w_s[ATT_MAX_CHUNKS];
     __shared__ float l_s[ATT_MAX_CHUNKS];
     __shared__ float red[16];
@@ -555,7 +556,7 @@ __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const i
         for (int i = 0; i < CMB_BATCH; ++i)
             if (c0 + i < nc) acc += w_s[c0 + i] * v[i];
     }
-    if (tid < HD) out[(size_t)b * ldo + h * HD + tid] = (f16)(acc / L);
+    if (tid < HD) out[act_off(b, h * HD + tid, ldo, mtp)] = (f16)(acc / L);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

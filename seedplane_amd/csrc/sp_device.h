@@ -26,6 +26,17 @@ template <> struct TileGeom<2> { static constexpr int KT = 64;  static constexpr
 template <> struct TileGeom<3> { static constexpr int KT = 128; static constexpr int STEPS = 4; static constexpr int SZ_BYTES = 256; };
 
 // ----------------------------------------------------------------------------------------------------------------
+// Activation layouts (fp16 GEMV inputs).  Row-major: element (m, k) at m * ld + k.  Fragment-major, for steps of
+// several columns padded to mtp tiles of 16: the 16 x 32 block (column tile mt, k-block kb) is one contiguous 1 KiB
+// in the order of the MFMA A operand (lane g * 16 + r holds column 16 mt + r, k = 32 kb + 8 g .. + 7), so a wave
+// reads a whole fragment with one fully coalesced dwordx4 load; blocks run k-block major:
+//   (m, k) -> ((k / 32) * mtp + m / 16) * 512 + ((k / 8) % 4) * 128 + (m % 16) * 8 + k % 8.
+__host__ __device__ __forceinline__ size_t act_off(int m, int k, int ld, int mtp) {
+    return mtp ? ((size_t)(k >> 5) * mtp + (m >> 4)) * 512 + ((k >> 3) & 3) * 128 + (m & 15) * 8 + (k & 7)
+               : (size_t)m * ld + k;
+}
+
+// ----------------------------------------------------------------------------------------------------------------
 // Exact unpacking.  int8 code c (two's complement) -> fp16: the byte c^0x80 = c+128 is placed under the exponent
 // byte 0x64, giving the fp16 value 1024 + c + 128 exactly; subtracting 1152 (exact in fp16) leaves c.
 __device__ __forceinline__ f16x2 q8_pair(uint32_t u, uint32_t sel) {

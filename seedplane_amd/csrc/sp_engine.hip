@@ -193,7 +193,7 @@ bool gemv_pro_ok(const DevMat &m, int pro, int H, int HD, int slices = 0, int wa
 // prologue (pro != PRO_NONE, one column) the activations come from *pa instead of x.
 int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, float *out_f32, f16 *out_f16, int ldo,
                 const float *bias, hipStream_t st, float *part = nullptr, size_t pstride = 0, int pro = PRO_NONE,
-                const ProArgs *pa = nullptr, int slices = 0, int waves = 0) {
+                const ProArgs *pa = nullptr, int slices = 0, int waves = 0, int xmtp = 0, int omtp = 0) {
     require(mcols >= 1 && mcols <= 16 * GEMV_MAX_MT, SP_EINVAL, "gemv columns out of range");
     require((epi == EPI_SILU) == m.paired, SP_EINVAL, "gemv epilogue does not match the matrix packing");
     require(pro == PRO_NONE || (mcols == 1 && pa), SP_EINVAL, "gemv prologue needs one column and its arguments");
@@ -206,6 +206,8 @@ int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, floa
     a.x = x; a.ldx = ldx; a.m = mcols;
     a.out_f32 = out_f32; a.out_f16 = out_f16; a.ldo = ldo; a.bias = bias; a.epi = epi;
     a.kslice = p.kslice; a.pstride = pstride; a.nwk = p.nw;
+    require(xmtp == 0 || xmtp == mt, SP_EINVAL, "gemv input layout does not match the column count");
+    a.xmtp = xmtp; a.omtp = omtp;
     if (p.s > 1) { a.epi = EPI_PART; a.out_f32 = part; a.bias = nullptr; }
     dim3 grid(p.units / p.r, p.s), block(64 * p.nw);
     if (pro != PRO_NONE) {
@@ -290,10 +292,10 @@ void by_slices(int np, F &&f) {
 
 // RMSNorm of n columns of x, first adding np pending split-K residual slices
 void launch_rmsnorm(int n, float *x, int H, const float *part, int np, size_t ps, const float *w, float eps, f16 *out,
-                    hipStream_t st) {
+                    hipStream_t st, int mtp) {
     by_slices(np, [&](auto c) {
         hipLaunchKernelGGL((k_rmsnorm<decltype(c)::value>), dim3(n), dim3(NORM_THREADS), 0, st, x, H, part, ps, w, H, eps,
-                           out, H);
+                           out, H, mtp);
     });
 }
 
@@ -315,21 +317,21 @@ DecShape dec_shape() {
 int dec_keys_per_block() { const DecShape d = dec_shape(); return d.nwv * d.sub * DEC_KC; }
 
 template <int HD>
-void launch_attn_dec_hd(dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct) {
+void launch_attn_dec_hd(dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct, int mtp) {
     const DecShape d = dec_shape();
 #ifdef SP_GEMV_TUNE
-    if (d.nwv == 1 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 1>), grid, dim3(64), 0, st, aa, out, ldo, direct); return; }
-    if (d.nwv == 2 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 1>), grid, dim3(128), 0, st, aa, out, ldo, direct); return; }
-    if (d.nwv == 4 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 1>), grid, dim3(256), 0, st, aa, out, ldo, direct); return; }
-    if (d.nwv == 2 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 2>), grid, dim3(128), 0, st, aa, out, ldo, direct); return; }
-    if (d.nwv == 1 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 2>), grid, dim3(64), 0, st, aa, out, ldo, direct); return; }
+    if (d.nwv == 1 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 1>), grid, dim3(64), 0, st, aa, out, ldo, direct, mtp); return; }
+    if (d.nwv == 2 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 1>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp); return; }
+    if (d.nwv == 4 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 1>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
+    if (d.nwv == 2 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 2>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp); return; }
+    if (d.nwv == 1 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 2>), grid, dim3(64), 0, st, aa, out, ldo, direct, mtp); return; }
 #endif
     (void)d;
-    hipLaunchKernelGGL((k_attn_dec<HD, 4, 2>), grid, dim3(256), 0, st, aa, out, ldo, direct);
+    hipLaunchKernelGGL((k_attn_dec<HD, 4, 2>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp);
 }
-void launch_attn_dec(int HD, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct) {
-    if (HD == 64) launch_attn_dec_hd<64>(grid, st, aa, out, ldo, direct);
-    else launch_attn_dec_hd<128>(grid, st, aa, out, ldo, direct);
+void launch_attn_dec(int HD, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct, int mtp) {
+    if (HD == 64) launch_attn_dec_hd<64>(grid, st, aa, out, ldo, direct, mtp);
+    else launch_attn_dec_hd<128>(grid, st, aa, out, ldo, direct, mtp);
 }
 
 template <int FMT>
@@ -449,16 +451,17 @@ void sp_engine::alloc_activations() {
     Nqkv = (d.n_heads + 2 * d.n_kv_heads) * d.head_dim;
     maxT = d.max_tokens;
     const int kmax = std::max(std::max(H, I), d.n_heads * d.head_dim);
+    const size_t tpad = (size_t)(maxT + 15) / 16 * 16;       // fragment-major inputs hold whole 16-column tiles
     x = dev_alloc<float>((size_t)maxT * H);
-    xn = dev_alloc<f16>((size_t)maxT * kmax);
+    xn = dev_alloc<f16>(tpad * kmax);
     qkv = dev_alloc<float>((size_t)maxT * Nqkv);
     gpart_stride = (size_t)maxT * std::max(H, Nqkv);
     gpart = dev_alloc<float>(GEMV_MAX_SLICES * gpart_stride);
     gpart2 = dev_alloc<float>(GEMV_MAX_SLICES * gpart_stride);
     x2 = dev_alloc<float>((size_t)maxT * H);
     q = dev_alloc<float>((size_t)maxT * d.n_heads * d.head_dim);
-    attn = dev_alloc<f16>((size_t)maxT * d.n_heads * d.head_dim);
-    act = dev_alloc<f16>((size_t)maxT * I);
+    attn = dev_alloc<f16>(tpad * d.n_heads * d.head_dim);
+    act = dev_alloc<f16>(tpad * I);
     logits = dev_alloc<float>((size_t)maxT * V);
     am_v = dev_alloc<float>((size_t)maxT * ARGMAX_BLOCKS);
     am_i = dev_alloc<int>((size_t)maxT * ARGMAX_BLOCKS);
@@ -467,9 +470,9 @@ void sp_engine::alloc_activations() {
     dgroups = dev_alloc<AttnGroup>(maxT);
     dcolnc = dev_alloc<int>(maxT);
     d_move = dev_alloc<int>(2 * 64);
-    HIPCHK(hipMemset(xn, 0, (size_t)maxT * kmax * sizeof(f16)));
-    HIPCHK(hipMemset(attn, 0, (size_t)maxT * d.n_heads * d.head_dim * sizeof(f16)));
-    HIPCHK(hipMemset(act, 0, (size_t)maxT * I * sizeof(f16)));
+    HIPCHK(hipMemset(xn, 0, tpad * kmax * sizeof(f16)));
+    HIPCHK(hipMemset(attn, 0, tpad * d.n_heads * d.head_dim * sizeof(f16)));
+    HIPCHK(hipMemset(act, 0, tpad * I * sizeof(f16)));
 }
 
 sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool graph) const {
@@ -746,6 +749,8 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
     }
     const bool logits_on = flags & SP_F_LOGITS;
     const size_t ps = gpart_stride;
+    // several columns: the fp16 GEMV inputs (xn, attn, act) are written fragment-major with mtp column tiles
+    const int mtp = n > 1 ? (n + 15) / 16 : 0;
     int pend = 0;     // residual slices of a split-K o / down GEMV waiting in gpart (added by the next RMSNorm)
     // One column: the input RMSNorm runs as the prologue of the qkv GEMV and the attention combine as the prologue of
     // o_proj (two launches fewer per layer); qkv and the down projection run in ONE_SLICES k-slices, so the prologue
@@ -773,9 +778,9 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
             sq = launch_gemv(ly.qkv, EPI_STORE, nullptr, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, qpart, ps, PRO_NORM, &pn,
                              qkv_s, qkv_w);
         } else {
-            launch_rmsnorm(n, res, H, gpart, pend, ps, ly.in_norm, d.rms_eps, xn, st);
+            launch_rmsnorm(n, res, H, gpart, pend, ps, ly.in_norm, d.rms_eps, xn, st, mtp);
             sq = launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, qpart, ps, PRO_NONE, nullptr,
-                             qkv_s, qkv_w);
+                             qkv_s, qkv_w, mtp);
         }
         RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots, qpart, ps, ly.qkv_b};
         const bool fused = ap.rope_fused && logits_on;
@@ -795,7 +800,7 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
             else launch_attn_mq_hd<128>(G, agrid, st, am);
         } else if (ap.dec) {
             AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
-            launch_attn_dec(HD, dim3(NKV, n, nchunk), st, aa, attn, NH * HD, ap.dec_direct ? 1 : 0);
+            launch_attn_dec(HD, dim3(NKV, n, nchunk), st, aa, attn, NH * HD, ap.dec_direct ? 1 : 0, mtp);
         } else {
             AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
             dim3 agrid(nchunk, NKV, n);
@@ -808,19 +813,22 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
             pend = launch_gemv(ly.o, EPI_RESID, nullptr, NH * HD, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_COMB, &pc);
         } else {
             if (!ap.dec_direct)
-                hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn, NH * HD);
-            pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, rmid, nullptr, H, nullptr, st, gpart, ps);
+                hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn,
+                                   NH * HD, mtp);
+            pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_NONE,
+                               nullptr, 0, 0, mtp);
         }
-        launch_rmsnorm(n, rmid, H, gpart, pend, ps, ly.post_norm, d.rms_eps, xn, st);
-        launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, st);
+        launch_rmsnorm(n, rmid, H, gpart, pend, ps, ly.post_norm, d.rms_eps, xn, st, mtp);
+        launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, st, nullptr, 0, PRO_NONE, nullptr, 0, 0, mtp,
+                    mtp);
         pend = launch_gemv(ly.down, EPI_RESID, act, I, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_NONE, nullptr,
-                           down_s, down_w);
+                           down_s, down_w, mtp);
         res = rmid;
     }
     if (logits_on) {
         const DevMat &hm = d.tied_head ? embed : head;
-        launch_rmsnorm(n, res, H, gpart, pend, ps, final_norm, d.rms_eps, xn, st);
-        launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, st);
+        launch_rmsnorm(n, res, H, gpart, pend, ps, final_norm, d.rms_eps, xn, st, mtp);
+        launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, st, nullptr, 0, PRO_NONE, nullptr, 0, 0, mtp);
         if (flags & SP_F_ARGMAX) {
             hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, n), dim3(256), 0, st, logits, d.vocab, d.vocab, am_v, am_i);
             hipLaunchKernelGGL(k_argmax_final, dim3(n), dim3(64), 0, st, am_v, am_i, am_out);
@@ -1118,27 +1126,30 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
         // instead of staying cached between launches
         int cur = layer < 0 ? 0 : layer;
         auto next_layer = [&] { if (layer < 0) cur = (cur + 1) % d.n_layers; };
+        const int tm = n_cols > 1 ? (n_cols + 15) / 16 : 0;     // activation layout of a step with n_cols columns
         std::function<void()> launch;
         const DevMat *m = nullptr;
         switch (kind) {
             case SP_T_QKV: m = &e->layers[cur].qkv;
                 launch = [&] { launch_gemv(e->layers[cur].qkv, EPI_STORE, e->xn, H, n_cols, e->qkv, nullptr, e->Nqkv,
-                                           e->layers[cur].qkv_b, st, e->gpart, e->gpart_stride); next_layer(); };
+                                           e->layers[cur].qkv_b, st, e->gpart, e->gpart_stride, PRO_NONE, nullptr, 0, 0,
+                                           tm); next_layer(); };
                 break;
             case SP_T_O: m = &e->layers[cur].o;
                 launch = [&] { launch_gemv(e->layers[cur].o, EPI_RESID, e->attn, NHD, n_cols, e->x, nullptr, H, nullptr,
-                                           st, e->gpart, e->gpart_stride); next_layer(); };
+                                           st, e->gpart, e->gpart_stride, PRO_NONE, nullptr, 0, 0, tm); next_layer(); };
                 break;
             case SP_T_GATE_UP: m = &e->layers[cur].gate_up;
                 launch = [&] { launch_gemv(e->layers[cur].gate_up, EPI_SILU, e->xn, H, n_cols, nullptr, e->act, I,
-                                           nullptr, st); next_layer(); };
+                                           nullptr, st, nullptr, 0, PRO_NONE, nullptr, 0, 0, tm, tm); next_layer(); };
                 break;
             case SP_T_DOWN: m = &e->layers[cur].down;
                 launch = [&] { launch_gemv(e->layers[cur].down, EPI_RESID, e->act, I, n_cols, e->x, nullptr, H, nullptr,
-                                           st, e->gpart, e->gpart_stride); next_layer(); };
+                                           st, e->gpart, e->gpart_stride, PRO_NONE, nullptr, 0, 0, tm); next_layer(); };
                 break;
             case SP_T_HEAD: case SP_T_EMBED: m = d.tied_head || kind == SP_T_EMBED ? &e->embed : &e->head;
-                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->logits, nullptr, d.vocab, nullptr, st); };
+                launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->logits, nullptr, d.vocab, nullptr, st,
+                                           nullptr, 0, PRO_NONE, nullptr, 0, 0, tm); };
                 break;
             default: throw Fail{SP_EINVAL, "kind must name a matrix"};
         }

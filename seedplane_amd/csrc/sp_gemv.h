@@ -42,6 +42,8 @@ struct GemvArgs {
     int kslice;            // k-tiles per slice
     size_t pstride;        // EPI_PART: floats between slices
     int nwk;               // prologue kernels: waves that take k-tiles (the others only help with the prologue)
+    int xmtp;              // x layout: 0 row-major [m][ldx], else fragment-major with xmtp column tiles (act_off)
+    int omtp;              // EPI_SILU output layout, the same way
 };
 template <int FMT>
 __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
@@ -79,7 +81,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int unit, int m
     if constexpr (RG == 2) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (live[j]) a.out_f16[(size_t)mrow[j] * a.ldo + n] = (f16)(silu_f(v0[j]) * v1[j]);
+            if (live[j]) a.out_f16[act_off(mrow[j], n, a.ldo, a.omtp)] = (f16)(silu_f(v0[j]) * v1[j]);
     } else if (a.epi == EPI_STORE) {
         const float bn = a.bias ? a.bias[n] : 0.f;
 #pragma unroll
@@ -335,9 +337,12 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int s = 0; s < ST; ++s) {
-                    if constexpr (PRO == PRO_NONE)
-                        xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(xrow[mt] + kt * KT + s * 32) : zero8;
-                    else
+                    if constexpr (PRO == PRO_NONE) {
+                        // either layout; columns past m read as zeros (their lanes do not load)
+                        const f16 *src = a.xmtp ? a.x + ((size_t)(kt * ST + s) * a.xmtp + mt) * 512 + lane * 8
+                                                : xrow[mt] + kt * KT + s * 32;
+                        xa[t][mt][s] = xon[mt] ? *(const f16x8 *)src : zero8;
+                    } else
                         xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(act + (kt - k0) * KT + s * 32 + 8 * g) : zero8;
                 }
         }
