@@ -148,6 +148,9 @@ __global__ void __launch_bounds__(ROPE_THREADS) k_rope_kv(RopeArgs a) {
 // merges them with exp(m - M) weights.  Replaces the SDPA call with its causal/slot mask (qwen_engine.py:126-135)
 // and attn_part.comp / attn_combine.comp.
 constexpr int ATT_CH = 64;
+// One partial record per (column, head, chunk): m and l as fp32, then acc[HD] as fp16 (half the bytes of an fp32
+// record; the rounding is below the fp16 rounding of the merged output).  Length in floats:
+__host__ __device__ constexpr int part_floats(int HD) { return 2 + HD / 2; }
 struct AttnArgs {
     const float *q;        // [n][NH*HD]
     const f16 *kc, *vc;    // this layer
@@ -224,7 +227,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
     e_s[h][lane] = ex;
     __syncthreads();
 
-    float *out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + c) * (HD + 2);
+    float *out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + c) * part_floats(HD);
     constexpr int DPL = HD / 64;                    // output dims per lane
     float o[DPL];
 #pragma unroll
@@ -235,7 +238,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
         for (int i = 0; i < DPL; ++i) o[i] += p * (float)v_s[j][lane + 64 * i];
     }
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) out[2 + lane + 64 * i] = o[i];
+    for (int i = 0; i < DPL; ++i) ((f16 *)(out + 2))[lane + 64 * i] = (f16)o[i];
     if (lane == 0) { out[0] = m; out[1] = l; }
 }
 
@@ -345,7 +348,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
     e_s[h][lane] = ex;
     __syncthreads();
 
-    float *out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + c) * (HD + 2);
+    float *out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + c) * part_floats(HD);
     constexpr int DPL = HD / 64;                    // output dims per lane
     float o[DPL];
 #pragma unroll
@@ -356,7 +359,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
         for (int i = 0; i < DPL; ++i) o[i] += p * (float)v_s[j][lane + 64 * i];
     }
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) out[2 + lane + 64 * i] = o[i];
+    for (int i = 0; i < DPL; ++i) ((f16 *)(out + 2))[lane + 64 * i] = (f16)o[i];
     if (lane == 0) { out[0] = m; out[1] = l; }
 }
 
@@ -501,8 +504,8 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
         if (direct) {
             out[act_off(b, (kvh * G + h) * HD + d, ldo, mtp)] = (f16)(acc / L);
         } else {
-            float *pp = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + split) * (HD + 2);
-            pp[2 + d] = acc;
+            float *pp = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + split) * part_floats(HD);
+            ((f16 *)(pp + 2))[d] = (f16)acc;
             if (d == 0) { pp[0] = M; pp[1] = L; }
         }
     }
@@ -520,14 +523,15 @@ __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const i
     __shared__ float red[16];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
     const int nc = col_nchunk[b];
-    const float *p = part + ((size_t)b * NH + h) * nchunk * (HD + 2);
+    const int rec = part_floats(HD);
+    const float *p = part + ((size_t)b * NH + h) * nchunk * rec;
     const int d = min(tid, HD - 1), last = max(nc - 1, 0);     // clamped: every load is in bounds
     float v[CMB_BATCH];
 #pragma unroll
-    for (int i = 0; i < CMB_BATCH; ++i) v[i] = p[(size_t)min(i, last) * (HD + 2) + 2 + d];
+    for (int i = 0; i < CMB_BATCH; ++i) v[i] = (float)((const f16 *)(p + (size_t)min(i, last) * rec + 2))[d];
     float mloc = -INFINITY;
     for (int c = tid; c < nc; c += nt) {
-        const float mc = p[(size_t)c * (HD + 2)], lc = p[(size_t)c * (HD + 2) + 1];
+        const float mc = p[(size_t)c * rec], lc = p[(size_t)c * rec + 1];
         w_s[c] = lc > 0.f ? mc : -INFINITY;
         l_s[c] = lc;
         mloc = fmaxf(mloc, w_s[c]);
@@ -550,7 +554,7 @@ __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const i
     for (int c0 = 0; c0 < nc; c0 += CMB_BATCH) {
         if (c0 > 0) {
 #pragma unroll
-            for (int i = 0; i < CMB_BATCH; ++i) v[i] = p[(size_t)min(c0 + i, last) * (HD + 2) + 2 + d];
+            for (int i = 0; i < CMB_BATCH; ++i) v[i] = (float)((const f16 *)(p + (size_t)min(c0 + i, last) * rec + 2))[d];
         }
 #pragma unroll
         for (int i = 0; i < CMB_BATCH; ++i)
@@ -822,8 +826,8 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
             const int row = rt * 16 + 4 * g4 + j;
             if (row < R) {
                 const int col = row / G, h = row - col * G;
-                float *out = a.part + (((size_t)(gr.first_col + col) * a.NH + kvh * G + h) * a.nchunk + c) * (HD + 2);
-                out[2 + 16 * dt + r16] = o[j];
+                float *out = a.part + (((size_t)(gr.first_col + col) * a.NH + kvh * G + h) * a.nchunk + c) * part_floats(HD);
+                ((f16 *)(out + 2))[16 * dt + r16] = (f16)o[j];
                 if (dt == 0 && r16 == 0) { out[0] = mrow[j]; out[1] = lrow[j]; }
             }
         }

@@ -128,9 +128,9 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
 #endif
     p.s = s;
     p.kslice = (m.nkt + s - 1) / s;
-    // several column tiles: 8 waves for the layer matrices (split or paired; shape sweeps at 16 and 33 columns),
-    // 4 for the unsplit head, whose blocks are many already
-    int nw = std::min(p.kslice, mt > 1 && (p.kslice >= 32 || s > 1 || m.paired) ? 8 : 4);
+    // several column tiles: 8 waves for the split layer matrices and long k-ranges, 4 for the gate_up pair and the
+    // unsplit head (A/B runs of the whole tree-verify step at 33 columns: gate_up with 4 waves -100 us per pass)
+    int nw = std::min(p.kslice, mt > 1 && (p.kslice >= 32 || s > 1) ? 8 : 4);
     if (waves > 0) nw = std::min(p.kslice, std::min(waves, mt == 1 ? 16 : 8));
 #ifdef SP_GEMV_TUNE
     if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 16 : 8);
@@ -983,7 +983,7 @@ int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots) {
         HIPCHK(hipMemcpy(e->d_vl, e->vc.data(), e->d.n_layers * sizeof(f16 *), hipMemcpyHostToDevice));
         e->n_seq = n_seq; e->n_slots = n_slots;
         e->max_nchunk = (n_slots + 64 + ATT_CH - 1) / ATT_CH;
-        e->attn_part = dev_alloc<float>((size_t)e->maxT * e->d.n_heads * e->max_nchunk * (e->d.head_dim + 2));
+        e->attn_part = dev_alloc<float>((size_t)e->maxT * e->d.n_heads * e->max_nchunk * part_floats(e->d.head_dim));
         for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
         e->graphs.clear();
     });

@@ -214,13 +214,14 @@ __device__ __forceinline__ void pro_comb(const ProArgs &p, f16 *act, int klo, in
     for (int h0 = h_lo; h0 <= h_hi; h0 += ngrp) {
         const bool live = h0 + grp <= h_hi;
         const int h = min(h0 + grp, h_hi);
-        const float *pp = p.apart + (size_t)h * p.nchunk * (HD + 2);
+        const int rec = part_floats(HD);
+        const float *pp = p.apart + (size_t)h * p.nchunk * rec;
         float v[CMB_BATCH];
 #pragma unroll
-        for (int i = 0; i < CMB_BATCH; ++i) v[i] = pp[(size_t)min(i, last) * (HD + 2) + 2 + gt];
+        for (int i = 0; i < CMB_BATCH; ++i) v[i] = (float)((const f16 *)(pp + (size_t)min(i, last) * rec + 2))[gt];
         float mloc = -INFINITY;
         for (int c = gt; c < nc; c += HD) {
-            const float mc = pp[(size_t)c * (HD + 2)], lc = pp[(size_t)c * (HD + 2) + 1];
+            const float mc = pp[(size_t)c * rec], lc = pp[(size_t)c * rec + 1];
             w_s[c] = lc > 0.f ? mc : -INFINITY;
             l_s[c] = lc;
             mloc = fmaxf(mloc, w_s[c]);
@@ -247,7 +248,7 @@ __device__ __forceinline__ void pro_comb(const ProArgs &p, f16 *act, int klo, in
         for (int c0 = 0; c0 < nc; c0 += CMB_BATCH) {
             if (c0 > 0) {
 #pragma unroll
-                for (int i = 0; i < CMB_BATCH; ++i) v[i] = pp[(size_t)min(c0 + i, last) * (HD + 2) + 2 + gt];
+                for (int i = 0; i < CMB_BATCH; ++i) v[i] = (float)((const f16 *)(pp + (size_t)min(c0 + i, last) * rec + 2))[gt];
             }
 #pragma unroll
             for (int i = 0; i < CMB_BATCH; ++i)
