@@ -65,7 +65,7 @@ SIGNATURES = {
                              c_void_p]),
     'sp_op_accept_tree': (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_int32, c_void_p, c_int32, ctypes.c_double, c_int32, c_void_p, c_void_p,
-                                  c_void_p]),
+                                  c_void_p, c_void_p]),
 }
 
 _lib = None

@@ -114,6 +114,9 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
     p.rg = m.paired ? 2 : 1;
     p.units = m.rows_pad / 16 / p.rg;
     if (mt == 1) p.r = p.units >= 2048 && p.units % 2 == 0 ? 2 : 1;
+    // the head at 2-3 column tiles: 4 units per wave (each activation fragment feeds 4 weight tiles); the int4 and
+    // 4-tile variants would spill registers
+    else if (!split_ok && !m.paired && p.units % 4 == 0 && mt <= 3 && m.fmt != 3) p.r = 4;
     else p.r = p.units % 2 == 0 && !m.paired ? 2 : 1;
     int s = 1;
     if (split_ok && !m.paired) {
@@ -155,6 +158,13 @@ void launch_gemv_fmt(int mt, bool paired, int r, dim3 grid, dim3 block, size_t s
     if (paired) {
         if (r == 2) launch_gemv_r<FMT, 2, 2>(mt, grid, block, smem, st, a);
         else launch_gemv_r<FMT, 2, 1>(mt, grid, block, smem, st, a);
+    } else if (r == 4) {
+        switch (mt) {
+            case 1: throw Fail{SP_EINVAL, "gemv plan: 4 units per wave need several column tiles"};
+            case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, 1, 4>), grid, block, smem, st, a); break;
+            case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, 1, 4>), grid, block, smem, st, a); break;
+            default: hipLaunchKernelGGL((k_gemv<FMT, 4, 1, 4>), grid, block, smem, st, a); break;
+        }
     } else {
         if (r == 2) launch_gemv_r<FMT, 1, 2>(mt, grid, block, smem, st, a);
         else launch_gemv_r<FMT, 1, 1>(mt, grid, block, smem, st, a);
@@ -371,9 +381,14 @@ struct sp_engine {
     f16 *xn = nullptr, *attn = nullptr, *act = nullptr;
     float *am_v = nullptr;
     int *am_i = nullptr, *am_out = nullptr;
+    // column descriptors of a call: tokens, attention groups, chunk counts, uploaded together from a pinned staging
+    // buffer (one copy per call); `upload_done` marks the copy so the staging buffer is not rewritten before it ran
     sp_token *dtoks = nullptr;
     AttnGroup *dgroups = nullptr;
     int *dcolnc = nullptr;
+    char *d_upload = nullptr, *h_upload = nullptr;
+    size_t upload_bytes = 0;
+    hipEvent_t upload_done = nullptr;
 
     // KV ring
     int n_seq = 0, n_slots = 0;
@@ -433,13 +448,17 @@ void sp_engine::free_all() {
     for (void *p : {(void *)x, (void *)x2, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)gpart,
                     (void *)gpart2, (void *)xn, (void *)attn,
                     (void *)act, (void *)am_v, (void *)am_i, (void *)am_out,
-                    (void *)dtoks, (void *)dgroups, (void *)dcolnc, (void *)d_kl, (void *)d_vl, (void *)d_move})
+                    (void *)d_upload, (void *)d_kl, (void *)d_vl, (void *)d_move})
         dev_free(p);
     for (auto p : kc) dev_free(p);
     for (auto p : vc) dev_free(p);
     kc.clear(); vc.clear();
     dev_free(pk.d_plans); dev_free(pk.d_lp); dev_free(pk.d_aux); dev_free(pk.ll); dev_free(pk.status);
     pk = Persistent{};
+    if (h_upload) (void)hipHostFree(h_upload);
+    if (upload_done) (void)hipEventDestroy(upload_done);
+    h_upload = nullptr; upload_done = nullptr; d_upload = nullptr;
+    dtoks = nullptr; dgroups = nullptr; dcolnc = nullptr;
     if (own_stream && stream) (void)hipStreamDestroy(stream);
     if (capture_stream) (void)hipStreamDestroy(capture_stream);
     stream = nullptr;
@@ -466,9 +485,16 @@ void sp_engine::alloc_activations() {
     am_v = dev_alloc<float>((size_t)maxT * ARGMAX_BLOCKS);
     am_i = dev_alloc<int>((size_t)maxT * ARGMAX_BLOCKS);
     am_out = dev_alloc<int>(maxT);
-    dtoks = dev_alloc<sp_token>(maxT);
-    dgroups = dev_alloc<AttnGroup>(maxT);
-    dcolnc = dev_alloc<int>(maxT);
+    // [tokens][groups][chunk counts], each part 16-byte aligned
+    const size_t tb = ((size_t)maxT * sizeof(sp_token) + 15) & ~(size_t)15;
+    const size_t gb = ((size_t)maxT * sizeof(AttnGroup) + 15) & ~(size_t)15;
+    upload_bytes = tb + gb + (size_t)maxT * sizeof(int);
+    d_upload = dev_alloc<char>(upload_bytes);
+    dtoks = (sp_token *)d_upload;
+    dgroups = (AttnGroup *)(d_upload + tb);
+    dcolnc = (int *)(d_upload + tb + gb);
+    HIPCHK(hipHostMalloc((void **)&h_upload, upload_bytes, hipHostMallocDefault));
+    HIPCHK(hipEventCreateWithFlags(&upload_done, hipEventDisableTiming));
     d_move = dev_alloc<int>(2 * 64);
     HIPCHK(hipMemset(xn, 0, tpad * kmax * sizeof(f16)));
     HIPCHK(hipMemset(attn, 0, tpad * d.n_heads * d.head_dim * sizeof(f16)));
@@ -1025,9 +1051,15 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         }
         e->last_path = 0;
         const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
-        HIPCHK(hipMemcpyAsync(e->dtoks, toks, n * sizeof(sp_token), hipMemcpyHostToDevice, e->stream));
-        HIPCHK(hipMemcpyAsync(e->dgroups, ap.groups.data(), ap.ngroups * sizeof(AttnGroup), hipMemcpyHostToDevice, e->stream));
-        HIPCHK(hipMemcpyAsync(e->dcolnc, ap.colnc.data(), n * sizeof(int), hipMemcpyHostToDevice, e->stream));
+        {
+            HIPCHK(hipEventSynchronize(e->upload_done));       // the previous call's copy has read the staging buffer
+            const size_t go = (char *)e->dgroups - e->d_upload, co = (char *)e->dcolnc - e->d_upload;
+            std::memcpy(e->h_upload, toks, n * sizeof(sp_token));
+            std::memcpy(e->h_upload + go, ap.groups.data(), ap.ngroups * sizeof(AttnGroup));
+            std::memcpy(e->h_upload + co, ap.colnc.data(), n * sizeof(int));
+            HIPCHK(hipMemcpyAsync(e->d_upload, e->h_upload, co + n * sizeof(int), hipMemcpyHostToDevice, e->stream));
+            HIPCHK(hipEventRecord(e->upload_done, e->stream));
+        }
         if (use_graph) {
             auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? (ap.dec_direct ? -3 : -2) : (ap.rope_fused ? -4 : -1)));
             auto it = e->graphs.find(key);
@@ -1295,7 +1327,8 @@ int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32
 int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld, int32_t n_nodes,
                       const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
                       const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,
-                      double temperature, int32_t max_depth, double *resid_dev, int32_t *out_dev, void *stream) {
+                      double temperature, int32_t max_depth, double *resid_dev, int32_t *out_dev, void *stream,
+                      int32_t *out_host) {
     (void)resid_dev;
     return guarded(nullptr, [&] {
         require(p_logits_dev && q_logits_dev && token_dev && trial_start_dev && n_trials_dev && trials_dev && u_dev &&
@@ -1308,7 +1341,8 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
         // the kernel checks every node / trial / token index it follows before using it (err = 2 if one is bad)
         hipStream_t st = (hipStream_t)stream;
-        // exchange words + timeout flag, one set per device, zeroed once; tags never repeat within 2^20 launches
+        // exchange words + error word, one set per device, zeroed once; tags never repeat within 2^20 launches, so
+        // neither needs clearing between launches (the kernel writes every entry of out_dev itself)
         static std::map<int, std::pair<unsigned long long *, unsigned *>> scratch_of;
         static unsigned launches = 0;
         int dev = 0;
@@ -1321,8 +1355,6 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
             it = scratch_of.emplace(dev, std::make_pair(xb, er)).first;
         }
         launches = launches % 0xFFFFFu + 1;
-        HIPCHK(hipMemsetAsync(it->second.second, 0, sizeof(unsigned), st));
-        HIPCHK(hipMemsetAsync(out_dev, 0xff, (max_depth + 4) * sizeof(int32_t), st));
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token_dev, trial_start_dev, n_trials_dev, trials_dev, u_dev,
                      n_u, 1.0 / temperature, it->second.first, it->second.second, launches << 12, n_nodes,
                      n_trials_total, out_dev, max_depth};
@@ -1330,9 +1362,12 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         HIPCHK(hipLaunchCooperativeKernel((const void *)k_accept_tree, dim3(ACC_NB), dim3(ACC_T), args, 0, st));
         unsigned err = 0;
         HIPCHK(hipMemcpyAsync(&err, it->second.second, sizeof(unsigned), hipMemcpyDeviceToHost, st));
+        if (out_host)
+            HIPCHK(hipMemcpyAsync(out_host, out_dev, (max_depth + 4) * sizeof(int32_t), hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
-        require(err != 2, SP_EINVAL, "malformed tree: node, trial or token index out of range");
-        require(err == 0, SP_EHIP, "acceptance exchange timed out");
+        const unsigned code = (err & ~0xfffu) == (launches << 12) ? err & 0xfffu : 0u;
+        require(code != 2, SP_EINVAL, "malformed tree: node, trial or token index out of range");
+        require(code == 0, SP_EHIP, "acceptance exchange timed out");
     });
 }
 

@@ -167,7 +167,8 @@ struct AcceptArgs {
     int n_u;
     double invT;
     unsigned long long *xbuf;   // exchange words [4][ACC_NB][4]
-    unsigned *err;           // set to 1 if an exchange timed out
+    unsigned *err;           // tag_base | 1 if an exchange timed out, tag_base | 2 for a malformed tree (words of
+                             // earlier launches carry other tags, so the word is never cleared)
     unsigned tag_base;       // distinct per launch (low 12 bits are the exchange counter)
     int n_nodes, n_trials_total;
     int *out;                // [0] k, [1..k] accepted node ids, [max_depth+1] final token, [max_depth+2] uniforms used,
@@ -189,6 +190,12 @@ __device__ __forceinline__ double d_w(float l, float m, double invT) {
 }
 
 // All-gather of two doubles per block.  Returns false on timeout (every block then stops).
+// Whether a block of this launch has reported a failure.
+__device__ __forceinline__ bool acc_failed(const AcceptArgs &a) {
+    const unsigned e = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (e & ~0xfffu) == a.tag_base && (e & 0xfffu) != 0;
+}
+
 __device__ bool acc_exchange(const AcceptArgs &a, unsigned &ex, double v0, double v1, AccShared &sh) {
     const unsigned tag = a.tag_base | (ex & 0xfffu);
     unsigned long long *slot = a.xbuf + (size_t)(ex & 3u) * ACC_NB * 4;
@@ -217,8 +224,8 @@ __device__ bool acc_exchange(const AcceptArgs &a, unsigned &ex, double v0, doubl
             if ((unsigned)(x0 >> 32) == tag && (unsigned)(x1 >> 32) == tag && (unsigned)(x2 >> 32) == tag &&
                 (unsigned)(x3 >> 32) == tag)
                 break;
-            if (++spins > (1l << 22) || __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (++spins > (1l << 22) || acc_failed(a)) {
+                __hip_atomic_store(a.err, a.tag_base | 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 sh.ok = 0;
                 break;
             }
@@ -315,7 +322,7 @@ __device__ int acc_draw(const double *w, int lo, int n, double u, const double *
 // Stops every block identically (the condition depends only on the inputs) and reports a malformed tree.
 __device__ __forceinline__ bool acc_bad(const AcceptArgs &a) {
     if (blockIdx.x == 0 && threadIdx.x == 0)
-        __hip_atomic_store(a.err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.err, a.tag_base | 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return false;
 }
 
@@ -418,6 +425,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
     if (threadIdx.x == 0) {
         if (blockIdx.x == 0) {          // every block took the same decisions; block 0 reports them
             a.out[0] = k;
+            for (int i = 1 + k; i <= a.max_depth; ++i) a.out[i] = -1;   // unused path entries
             a.out[a.max_depth + 2] = ui;
             a.out[a.max_depth + 3] = bonus;
         }

@@ -233,11 +233,20 @@ def _splitmix64(x):
     return z ^ (z >> 31)
 
 
+def _splitmix64_np(x):
+    """_splitmix64 on a uint64 array (numpy integer arithmetic wraps modulo 2^64)."""
+    x = x + np.uint64(0x9E3779B97F4A7C15)
+    z = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
 def uniforms(seed, step, n):
-    """Counter-based uniforms in [0, 1): u_i = (splitmix64(splitmix64(seed) ^ (step * 2^20 + i)) >> 11) * 2^-53."""
-    s = _splitmix64(int(seed) & MASK64)
-    return np.array([(_splitmix64(s ^ ((int(step) << 20) + i)) >> 11) * 2.0 ** -53 for i in range(n)],
-                    dtype=np.float64)
+    """Counter-based uniforms in [0, 1): u_i = (splitmix64(splitmix64(seed) ^ (step * 2^20 + i)) >> 11) * 2^-53.
+    (The top 53 bits convert to float64 exactly, so the values do not depend on how the integers are computed.)"""
+    s = np.uint64(_splitmix64(int(seed) & MASK64))
+    ctr = (np.uint64((int(step) << 20) & MASK64) + np.arange(n, dtype=np.uint64))
+    return (_splitmix64_np(s ^ ctr) >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
 
 
 # ===================================================================================== GPU verification
@@ -252,6 +261,7 @@ class TreeVerifier:
         self._lib = _lib
         self.torch = torch
         self._out = {}
+        self._stage = {}
 
     def forward(self, cache, tree: FlatTree, logits_out=None, graph=False):
         """One pass over every node: node i is written at cache position cache.length + i, RoPE position
@@ -315,29 +325,39 @@ class TreeVerifier:
         dev = p_logits.device
         V = p_logits.shape[1]
         md = max(1, tree.max_depth)
-        # one host->device copy: float64 uniforms first (8-byte aligned), then the int32 tree arrays
+        # one host->device copy from a reused pinned buffer: float64 uniforms first (8-byte aligned), then the int32
+        # tree arrays (the call is synchronous, so the buffer is free again when it returns)
         ints = [tree.token, tree.trial_start, tree.n_trials, tree.trials if len(tree.trials) else [0]]
         nu = len(u)
         sizes = [len(x) for x in ints]
-        host = np.empty(nu * 2 + sum(sizes), dtype=np.int32)
+        total = nu * 2 + sum(sizes)
+        stage = self._stage.get(dev)
+        if stage is None or stage[0].numel() < total:
+            cap = max(total, 4096)
+            stage = self._stage[dev] = (torch.empty(cap, dtype=torch.int32, pin_memory=True),
+                                        torch.empty(cap, dtype=torch.int32, device=dev))
+        pinned, buf = stage
+        host = pinned.numpy()
         host[:nu * 2] = np.asarray(u, dtype=np.float64).view(np.int32)
         off, offs = nu * 2, []
         for x, n in zip(ints, sizes):
             host[off:off + n] = x
             offs.append(off)
             off += n
-        buf = torch.from_numpy(host).to(dev)
+        buf[:total].copy_(pinned[:total], non_blocking=True)
         out = self._out.get((dev, md))
         if out is None:
             out = self._out[(dev, md)] = torch.empty(md + 4, dtype=torch.int32, device=dev)
+        res = np.empty(md + 4, dtype=np.int32)
         base = buf.data_ptr()
         at = lambda o: ctypes.c_void_p(base + 4 * o)
         ptr = lambda t: ctypes.c_void_p(t.data_ptr())
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         self._lib.check(self.engine.lib.sp_op_accept_tree(
             ptr(p_logits), ptr(q_logits), V, p_logits.stride(0), tree.size, at(offs[0]), at(offs[1]), at(offs[2]),
-            at(offs[3]), len(tree.trials), at(0), nu, float(temperature), md, None, ptr(out), stream))
-        o = out.cpu().tolist()
+            at(offs[3]), len(tree.trials), at(0), nu, float(temperature), md, None, ptr(out), stream,
+            res.ctypes.data_as(ctypes.c_void_p)))
+        o = res.tolist()
         k = o[0]
         return o[1:1 + k], o[md + 1], o[md + 2], bool(o[md + 3])
 
