@@ -141,8 +141,6 @@ __device__ __forceinline__ void pro_norm(const ProArgs &p, f16 *act, int klo, in
     constexpr int PRO_THREADS = pro_threads(PRO_NORM), PRO_QMAX = PRO_NORM_HMAX / PRO_THREADS;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, H = p.H;
     float *v_s = scr, *red = scr + H;
-    const bool has_part = p.np > 0;
-    const int last = max(p.np, 1) - 1;
     // every load first, from clamped addresses: the residual, the slices, the weights of this block's k-range
     float xv[PRO_QMAX], wk[PRO_QMAX], pv[PRO_MAX_SLICES][PRO_QMAX];
 #pragma unroll
@@ -150,23 +148,22 @@ __device__ __forceinline__ void pro_norm(const ProArgs &p, f16 *act, int klo, in
         xv[q] = p.res[min(tid + PRO_THREADS * q, H - 1)];
         wk[q] = p.w[min(klo + tid + PRO_THREADS * q, H - 1)];
     }
-    if (has_part) {
 #pragma unroll
-        for (int s = 0; s < PRO_MAX_SLICES; ++s)
+    for (int s = 0; s < PRO_MAX_SLICES; ++s) {
+        if (s < p.np) {                              // uniform: only the pending slices are loaded
 #pragma unroll
             for (int q = 0; q < PRO_QMAX; ++q)
-                pv[s][q] = p.part[(size_t)min(s, last) * p.pstride + min(tid + PRO_THREADS * q, H - 1)];
+                pv[s][q] = p.part[(size_t)s * p.pstride + min(tid + PRO_THREADS * q, H - 1)];
+        }
     }
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
 #pragma unroll
     for (int q = 0; q < PRO_QMAX; ++q) {
         const int k = tid + PRO_THREADS * q;
         float v = xv[q];
-        if (has_part) {
 #pragma unroll
-            for (int s = 0; s < PRO_MAX_SLICES; ++s)
-                if (s < p.np) v += pv[s][q];
-        }
+        for (int s = 0; s < PRO_MAX_SLICES; ++s)
+            if (s < p.np) v += pv[s][q];
         if (k < H) {
             v_s[k] = v;
             if (writer) p.res_out[k] = v;
