@@ -683,13 +683,21 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     const bool active = rt < n_tiles;
     const size_t head_base = ((size_t)gr.seq * a.NKV + kvh) * a.n_slots;
     const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    // visible key j of the chunk (j < cnt): its cache slot and its ring position / tree code
+    // visible key j of the chunk (j < cnt): its cache slot and its ring position / tree code (~tree index).  Slots
+    // of a chunk are consecutive from a per-block base (ring keys) or from tree_base (tree keys), so one modulo per
+    // block and a conditional subtraction per key replace a division per key (branch-free: the selects keep the
+    // wave converged).
+    const int lin_base = (gr.lo + v0) % a.n_slots;   // slot of visible key v0 when it is a ring key
+    auto wrap = [&](int x) {                         // x mod n_slots for 0 <= x < n_slots + ATT_CH
+        x = x >= a.n_slots ? x - a.n_slots : x;
+        return a.n_slots >= ATT_CH ? x : x % a.n_slots;
+    };
     auto key_at = [&](int j, int &kp) {
         const int vis = v0 + j;
-        if (vis < gr.nlin) { kp = gr.lo + vis; return kp % a.n_slots; }
+        const bool lin = vis < gr.nlin;
         const int tj = vis - gr.nlin;
-        kp = -(1 + tj);
-        return (gr.tree_base + tj) % a.n_slots;
+        kp = lin ? gr.lo + vis : ~tj;
+        return wrap(lin ? lin_base + j : gr.tree_base + tj);
     };
 
     // ---- every global load before the first LDS store.  Keys past cnt load key 0 of the chunk (clamped address,
@@ -774,20 +782,32 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
         }
         sc[st] = acc;
     }
-    // ---- mask, chunk-local max / exp / sum per row
-    float mrow[4], lrow[4];
+    // ---- mask, chunk-local max / exp / sum per row.  The key codes of the lane's 4 slot tiles and the range / tree
+    // bits of its 4 rows are read once; the mask is selects only (ring key: inside the column's range; tree key:
+    // its bit set in the column's ancestor mask; padding key: never).
+    int kpv[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) kpv[st] = kpos_s[16 * st + r16];
+    int clo[4], chi[4], ctc[4];
+    unsigned long long cmk[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int row = rt * 16 + 4 * g4 + j;
         const int col = row < R ? row / G : 0;
-        const int lo = clo_s[col], hi = chi_s[col], tc = ctc_s[col];
-        const unsigned long long mk = cmask_s[col];
+        clo[j] = clo_s[col]; chi[j] = chi_s[col]; ctc[j] = ctc_s[col]; cmk[j] = cmask_s[col];
+    }
+    float mrow[4], lrow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = rt * 16 + 4 * g4 + j;
         float m = -INFINITY;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            const int kp = kpos_s[16 * st + r16];
-            bool ok = row < R && kp != INT_MIN;
-            if (ok) ok = kp >= 0 ? (kp >= lo && kp <= hi) : ((-kp - 1) < tc && ((mk >> (-kp - 1)) & 1ull));
+            const int kp = kpv[st];
+            const int tj = ~kp;                      // tree index of a tree key (kp = ~tj < 0)
+            const bool in_ring = (kp >= clo[j]) & (kp <= chi[j]);
+            const bool in_tree = (tj < ctc[j]) & (((cmk[j] >> (tj & 63)) & 1ull) != 0);
+            const bool ok = (row < R) & (kp != INT_MIN) & (kp >= 0 ? in_ring : in_tree);
             const float v = ok ? sc[st][j] : -INFINITY;
             sc[st][j] = v;
             m = fmaxf(m, v);
@@ -813,23 +833,26 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) pa[s2] = *(const f16x8 *)&p_s[wv][r16][32 * s2 + 8 * g4];
     // ---- O = P V over HD/16 dim tiles; lane holds O[row 4*g4 + j][dim 16*dt + r16]
+    f32x4 o[HD / 16];
 #pragma unroll
     for (int dt = 0; dt < HD / 16; ++dt) {
-        f32x4 o = (f32x4){0.f, 0.f, 0.f, 0.f};
+        o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const f16x8 vb = *(const f16x8 *)&vt_s[16 * dt + r16][32 * s2 + 8 * g4];
-            o = mfma16(pa[s2], vb, o);
+            o[dt] = mfma16(pa[s2], vb, o[dt]);
         }
+    }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = rt * 16 + 4 * g4 + j;
-            if (row < R) {
-                const int col = row / G, h = row - col * G;
-                float *out = a.part + (((size_t)(gr.first_col + col) * a.NH + kvh * G + h) * a.nchunk + c) * part_floats(HD);
-                ((f16 *)(out + 2))[16 * dt + r16] = (f16)o[j];
-                if (dt == 0 && r16 == 0) { out[0] = mrow[j]; out[1] = lrow[j]; }
-            }
+    for (int j = 0; j < 4; ++j) {
+        const int row = rt * 16 + 4 * g4 + j;
+        if (row < R) {
+            const int col = row / G, h = row - col * G;
+            float *out = a.part + (((size_t)(gr.first_col + col) * a.NH + kvh * G + h) * a.nchunk + c) * part_floats(HD);
+            f16 *oh = (f16 *)(out + 2);
+#pragma unroll
+            for (int dt = 0; dt < HD / 16; ++dt) oh[16 * dt + r16] = (f16)o[dt][j];
+            if (r16 == 0) { out[0] = mrow[j]; out[1] = lrow[j]; }
         }
     }
 }
