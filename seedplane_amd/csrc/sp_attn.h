@@ -267,20 +267,6 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
     constexpr int NT = 64 * G;
     const size_t head_base = ((size_t)t.seq * a.NKV + kvh) * a.n_slots;
 
-    // projection value idx of this column: the finished row, or the split-K slices in slice order plus the bias
-    // (all slice loads are issued before the first add; up to 8 slices)
-    auto proj = [&](int idx) -> float {
-        if (np == 0) return r.qkv[(size_t)b * r.Nqkv + idx];
-        const float *p = r.part + (size_t)b * r.Nqkv + idx;
-        float tv[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) tv[s] = s < np ? p[(size_t)s * r.pstride] : 0.f;
-        const float bias = r.bias[idx];
-        float v = tv[0];
-#pragma unroll
-        for (int s = 1; s < 8; ++s) if (s < np) v += tv[s];
-        return v + bias;
-    };
     // the chunk's cached K/V rows into registers first, so their loads overlap the projection loads below
     constexpr int CPR = HD / 8;                     // 16-byte chunks per row
     constexpr int PER = (ATT_CH * CPR + NT - 1) / NT;
@@ -294,14 +280,53 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
         vr[k] = *(const f16x8 *)(a.vc + off);
     }
     const float fpos = (float)t.pos;
-    // queries of the group (then the key of the newest position, in the owning block), rotated
+    // queries of the group (then the key of the newest position, in the owning block) are rotated; the owning block
+    // also stores the new value.  Every projection load of the thread (all slices and the bias of its rotation pairs
+    // and of its value dim) is issued in one batch from clamped indices before the first add, so the owning block
+    // pays one memory round trip like the others.
     const int nrot = (own ? G + 1 : G) * HALF;
-    for (int i = tid; i < nrot; i += NT) {
+    constexpr int RI = ((G + 1) * HALF + NT - 1) / NT;    // rotation items per thread
+    const int nsl = np == 0 ? 1 : np;                    // slices to load (np == 0: the finished row)
+    const float *prow = np == 0 ? r.qkv + (size_t)b * r.Nqkv : r.part + (size_t)b * r.Nqkv;
+    const size_t pstr = np == 0 ? 0 : r.pstride;
+    float t1[RI][8], t2[RI][8], bb1[RI], bb2[RI], tv[8], bv = 0.f;
+    int id1[RI];
+#pragma unroll
+    for (int ri = 0; ri < RI; ++ri) {
+        const int i = min(tid + ri * NT, nrot - 1);
         const int hh = i / HALF, j = i - hh * HALF;
         const int head = hh < G ? kvh * G + hh : a.NH + kvh;
+        id1[ri] = head * HD + j;
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) {
+            if (sl < nsl) {
+                t1[ri][sl] = prow[(size_t)sl * pstr + id1[ri]];
+                t2[ri][sl] = prow[(size_t)sl * pstr + id1[ri] + HALF];
+            }
+        }
+        bb1[ri] = np == 0 ? 0.f : r.bias[id1[ri]];
+        bb2[ri] = np == 0 ? 0.f : r.bias[id1[ri] + HALF];
+    }
+    const int vidx = (a.NH + a.NKV + kvh) * HD + min(tid, HD - 1);
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl)
+        if (sl < nsl) tv[sl] = prow[(size_t)sl * pstr + vidx];
+    if (np != 0) bv = r.bias[vidx];
+    // the projection value: the finished row, or the slices in slice order plus the bias (as k_rope_kv)
+    auto sum_of = [&](const float *tt, float bias) {
+        float v = tt[0];
+#pragma unroll
+        for (int sl = 1; sl < 8; ++sl) if (sl < np) v += tt[sl];
+        return np == 0 ? v : v + bias;
+    };
+#pragma unroll
+    for (int ri = 0; ri < RI; ++ri) {
+        const int i = tid + ri * NT;
+        if (i >= nrot) break;
+        const int hh = i / HALF, j = i - hh * HALF;
         const float ph = fpos * r.inv_freq[j];
         const float cs = cosf(ph), sn = sinf(ph);
-        const float x1 = proj(head * HD + j), x2 = proj(head * HD + j + HALF);
+        const float x1 = sum_of(t1[ri], bb1[ri]), x2 = sum_of(t2[ri], bb2[ri]);
         const float o1 = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(-x2, sn));
         const float o2 = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
         if (hh < G) {
@@ -314,12 +339,10 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
             kd[j] = k1; kd[j + HALF] = k2;
         }
     }
-    if (own) {
-        for (int d = tid; d < HD; d += NT) {
-            const f16 v = (f16)proj((a.NH + a.NKV + kvh) * HD + d);
-            v_s[jn][d] = v;
-            r.vc[(head_base + t.slot) * HD + d] = v;
-        }
+    if (own && tid < HD) {
+        const f16 v = (f16)sum_of(tv, bv);
+        v_s[jn][tid] = v;
+        r.vc[(head_base + t.slot) * HD + tid] = v;
     }
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
