@@ -4,6 +4,8 @@ The shared library is built in-tree (seedplane_amd/build.py) and loaded from thi
 no fallback: if the library is missing or a call fails, an exception is raised.
 """
 import ctypes
+
+import numpy as np
 import os
 from pathlib import Path
 
@@ -34,6 +36,10 @@ class Token(ctypes.Structure):
 
 
 assert ctypes.sizeof(Token) == 40
+
+# the same layout as a numpy structured dtype (columns built in bulk)
+TOKEN_DTYPE = np.dtype([(name, np.int32 if ctype is c_int32 else np.uint64) for name, ctype in Token._fields_])
+assert TOKEN_DTYPE.itemsize == 40 and all(TOKEN_DTYPE.fields[n][1] == getattr(Token, n).offset for n, _ in Token._fields_)
 
 SIGNATURES = {
     'sp_engine_create': (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(c_void_p)]),

@@ -251,9 +251,16 @@ class Qwen2Engine:
 
     def run(self, cols, flags, logits_out=None, want_ids=False):
         """Low-level: one engine call over column tuples (token, seq, pos, slot, ctx_lo, ctx_hi, tree_base,
-        tree_count, tree_mask).  Returns greedy ids (numpy int32) when want_ids."""
-        n = len(cols)
-        arr = (_lib.Token * n)(*[_lib.Token(*c) for c in cols])
+        tree_count, tree_mask), or a numpy array of _lib.TOKEN_DTYPE.  Returns greedy ids (numpy int32) when
+        want_ids."""
+        if isinstance(cols, np.ndarray):
+            if cols.dtype != _lib.TOKEN_DTYPE or not cols.flags.c_contiguous:
+                raise ValueError('column array must be a contiguous TOKEN_DTYPE array')
+            n = len(cols)
+            arr = cols.ctypes.data_as(ctypes.POINTER(_lib.Token))
+        else:
+            n = len(cols)
+            arr = (_lib.Token * n)(*[_lib.Token(*c) for c in cols])
         ids = np.zeros(n, dtype=np.int32) if want_ids else None
         if want_ids:
             flags |= _lib.SP_F_ARGMAX | _lib.SP_F_LOGITS

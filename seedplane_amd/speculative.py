@@ -163,6 +163,18 @@ class FlatTree:
             i = self.parent[i]
         return m
 
+    def column_arrays(self):
+        """(token int32, depth int32, ancestor masks uint64) arrays, computed once per tree."""
+        cached = getattr(self, '_cols', None)
+        if cached is None:
+            masks = [0] * self.size
+            for i in range(self.size):                     # parents precede children: one pass
+                p = self.parent[i]
+                masks[i] = (1 << i) | (masks[p] if p >= 0 else 0)
+            cached = self._cols = (np.asarray(self.token, dtype=np.int32), np.asarray(self.depth, dtype=np.int32),
+                                   np.asarray(masks, dtype=np.uint64))
+        return cached
+
     def child(self, node, token):
         c0 = self.first_child[node]
         for c in range(c0, c0 + self.n_children[node]):
@@ -263,10 +275,11 @@ class TreeVerifier:
         self._out = {}
         self._stage = {}
 
-    def forward(self, cache, tree: FlatTree, logits_out=None, graph=False):
+    def forward(self, cache, tree: FlatTree, logits_out=None, graph=False, ids=True):
         """One pass over every node: node i is written at cache position cache.length + i, RoPE position
         cache.length + depth[i], and attends to the cache before the root plus its own ancestors.  Returns the
-        greedy ids per node; logits [nodes, vocab] go to `logits_out` when given."""
+        greedy ids per node; logits [nodes, vocab] go to `logits_out` when given.  With ids=False (acceptance
+        sampling needs the logits only) no argmax runs, the call does not wait for the GPU, and None is returned."""
         e = self.engine
         e._check_cache(cache)
         n = tree.size
@@ -276,13 +289,22 @@ class TreeVerifier:
         if cache.window is None and P + n > cache.capacity:
             raise ValueError(f'KV cache capacity {cache.capacity} exceeded')
         S = e._pool_slots
-        cols = []
-        for i in range(n):
-            pos = P + tree.depth[i]
-            lo = 0 if cache.window is None else max(0, pos - cache.window + 1)
-            cols.append((tree.token[i], cache.seq, pos, (P + i) % S, lo, P - 1, P % S, n, tree.ancestors_mask(i)))
+        tok, depth, masks = tree.column_arrays()
+        cols = np.empty(n, dtype=self._lib.TOKEN_DTYPE)
+        pos = P + depth
+        cols['token'] = tok
+        cols['seq'] = cache.seq
+        cols['pos'] = pos
+        cols['slot'] = (P + np.arange(n, dtype=np.int64)) % S
+        cols['ctx_lo'] = 0 if cache.window is None else np.maximum(0, pos - cache.window + 1)
+        cols['ctx_hi'] = P - 1
+        cols['tree_base'] = P % S
+        cols['tree_count'] = n
+        cols['tree_mask'] = masks
         flags = self._lib.SP_F_LOGITS | (self._lib.SP_F_GRAPH if graph else 0)
-        return e.run(cols, flags, logits_out=logits_out, want_ids=True)
+        if not ids and logits_out is None:
+            raise ValueError('ids=False needs logits_out')
+        return e.run(cols, flags, logits_out=logits_out, want_ids=ids)
 
     def commit(self, cache, tree: FlatTree, path_nodes):
         """Keep the root and the accepted path nodes (in order) in the cache: their K/V move to consecutive slots
@@ -326,11 +348,16 @@ class TreeVerifier:
         V = p_logits.shape[1]
         md = max(1, tree.max_depth)
         # one host->device copy from a reused pinned buffer: float64 uniforms first (8-byte aligned), then the int32
-        # tree arrays (the call is synchronous, so the buffer is free again when it returns)
-        ints = [tree.token, tree.trial_start, tree.n_trials, tree.trials if len(tree.trials) else [0]]
+        # tree arrays (concatenated once per tree; the call is synchronous, so the buffer is free again when it returns)
+        acc = getattr(tree, '_acc', None)
+        if acc is None:
+            ints = [tree.token, tree.trial_start, tree.n_trials, tree.trials if len(tree.trials) else [0]]
+            sizes = [len(x) for x in ints]
+            acc = tree._acc = (np.concatenate([np.asarray(x, dtype=np.int32) for x in ints]),
+                               [int(o) for o in np.cumsum([0] + sizes[:-1])])
+        flat, rel = acc
         nu = len(u)
-        sizes = [len(x) for x in ints]
-        total = nu * 2 + sum(sizes)
+        total = nu * 2 + len(flat)
         stage = self._stage.get(dev)
         if stage is None or stage[0].numel() < total:
             cap = max(total, 4096)
@@ -339,11 +366,8 @@ class TreeVerifier:
         pinned, buf = stage
         host = pinned.numpy()
         host[:nu * 2] = np.asarray(u, dtype=np.float64).view(np.int32)
-        off, offs = nu * 2, []
-        for x, n in zip(ints, sizes):
-            host[off:off + n] = x
-            offs.append(off)
-            off += n
+        host[nu * 2:total] = flat
+        offs = [nu * 2 + o for o in rel]
         buf[:total].copy_(pinned[:total], non_blocking=True)
         out = self._out.get((dev, md))
         if out is None:
@@ -515,7 +539,7 @@ def speculative_generate(target, drafter, prompt, steps, n_branches=8, depth=4, 
         branches, rows, used = drafter.propose(dcache, pending, n_branches, depth, temperature, u)
         tree = flatten(committed[-1], branches)
         p = torch.empty((tree.size, target.vocab), dtype=torch.float32, device=target.device)
-        verifier.forward(tcache, tree, logits_out=p)
+        verifier.forward(tcache, tree, logits_out=p, ids=False)
         q = q_rows_for_tree(tree, rows, target.vocab, target.device)
         path, final, _, bonus = verifier.accept(p, q, tree, u[used:], temperature)
         acc_tokens = [tree.token[n] for n in path]
