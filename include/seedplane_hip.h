@@ -64,8 +64,11 @@ enum {
     SP_F_GRAPH = 4,       /* capture the step into a hipGraph on first use and replay it afterwards  */
     SP_F_PERSISTENT = 8,  /* one decode column without a tree: run the whole step as one persistent   */
                           /* cooperative kernel when the model fits it (else the kernel chain runs)  */
-    SP_F_UNFUSED = 16     /* one column: run every RMSNorm and attention combine as a kernel of its   */
+    SP_F_UNFUSED = 16,    /* one column: run every RMSNorm and attention combine as a kernel of its   */
                           /* own instead of inside the next GEMV (same results; for checking)        */
+    SP_F_FEED = 32        /* column b's token is the argmax id of column b of the last SP_F_ARGMAX   */
+                          /* call (on the device; the token field is ignored), so a greedy loop     */
+                          /* needs no host round trip per step                                       */
 };
 
 typedef struct sp_model_desc {
@@ -138,6 +141,12 @@ int sp_engine_logits(sp_engine *e, float **logits_dev);
  * the slot copies of copy_slots (qwen_vk.cpp:441-451): for every layer copies K/V of slot src[i] to dst[i] of
  * sequence `seq`, in order i = 0..n-1 (tree compaction after acceptance). */
 int sp_engine_kv_move(sp_engine *e, int32_t seq, int32_t n, const int32_t *src_slots, const int32_t *dst_slots);
+
+/* Replaces the per-token host read of the greedy id in Qwen2Engine.generate (qwen_engine.py:158-166): enqueue a copy of
+ * the last SP_F_ARGMAX call's ids (n <= its column count) to host memory on the engine's stream and return without
+ * waiting; `host` holds them after the stream synchronises (sp_engine_sync).  Pinned host memory keeps the copy
+ * asynchronous. */
+int sp_engine_copy_ids(sp_engine *e, int32_t n, int32_t *host);
 
 /* Wait for all work queued by the engine. */
 int sp_engine_sync(sp_engine *e);

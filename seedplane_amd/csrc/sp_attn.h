@@ -30,11 +30,12 @@ __device__ __forceinline__ float packed_elem(const uint8_t *w, const f16 *sz, in
     }
 }
 
-// x[b][k] = E[token_b][k] (fp32).  Replaces F.embedding (qwen_engine.py:117) / embed.comp.
+// x[b][k] = E[token_b][k] (fp32).  Replaces F.embedding (qwen_engine.py:117) / embed.comp.  With `feed` the token
+// of column b is feed[b] (the previous step's argmax of that column, kept on the device), clamped to the vocabulary.
 template <int FMT>
 __global__ void __launch_bounds__(256) k_embed(const uint8_t *w, const f16 *sz, int nkt, const sp_token *toks,
-                                               int H, float *x, int ldx) {
-    const int b = blockIdx.x, tok = toks[b].token;
+                                               int H, float *x, int ldx, const int *feed, int vocab) {
+    const int b = blockIdx.x, tok = feed ? min(max(feed[b], 0), vocab - 1) : toks[b].token;
     for (int k = threadIdx.x; k < H; k += blockDim.x) x[(size_t)b * ldx + k] = packed_elem<FMT>(w, sz, nkt, tok, k);
 }
 

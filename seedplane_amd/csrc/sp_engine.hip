@@ -345,8 +345,9 @@ void launch_attn_dec(int HD, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 
 }
 
 template <int FMT>
-void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x, hipStream_t st) {
-    hipLaunchKernelGGL((k_embed<FMT>), dim3(n), dim3(256), 0, st, m.w, m.sz, m.nkt, toks, H, x, H);
+void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x, hipStream_t st, const int *feed,
+                  int vocab) {
+    hipLaunchKernelGGL((k_embed<FMT>), dim3(n), dim3(256), 0, st, m.w, m.sz, m.nkt, toks, H, x, H, feed, vocab);
 }
 
 }  // namespace
@@ -381,6 +382,7 @@ struct sp_engine {
     f16 *xn = nullptr, *attn = nullptr, *act = nullptr;
     float *am_v = nullptr;
     int *am_i = nullptr, *am_out = nullptr;
+    int argmax_cols = 0;         // columns whose argmax ids am_out holds (the last SP_F_ARGMAX call)
     // column descriptors of a call: tokens, attention groups, chunk counts, uploaded together from a pinned staging
     // buffer (one copy per call); `upload_done` marks the copy so the staging buffer is not rewritten before it ran
     sp_token *dtoks = nullptr;
@@ -485,6 +487,8 @@ void sp_engine::alloc_activations() {
     am_v = dev_alloc<float>((size_t)maxT * ARGMAX_BLOCKS);
     am_i = dev_alloc<int>((size_t)maxT * ARGMAX_BLOCKS);
     am_out = dev_alloc<int>(maxT);
+    HIPCHK(hipMemset(am_out, 0, maxT * sizeof(int)));
+    argmax_cols = 0;
     // [tokens][groups][chunk counts], each part 16-byte aligned
     const size_t tb = ((size_t)maxT * sizeof(sp_token) + 15) & ~(size_t)15;
     const size_t gb = ((size_t)maxT * sizeof(AttnGroup) + 15) & ~(size_t)15;
@@ -768,10 +772,11 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
     const int nchunk = ap.nchunk;
     const int H = d.hidden, I = d.intermediate, NH = d.n_heads, NKV = d.n_kv_heads, HD = d.head_dim;
     hipStream_t st = stream;
+    const int *feed = (flags & SP_F_FEED) ? am_out : nullptr;   // tokens = the previous step's argmax ids
     switch (embed.fmt) {
-        case 1: launch_embed<1>(embed, dtoks, n, H, x, st); break;
-        case 2: launch_embed<2>(embed, dtoks, n, H, x, st); break;
-        default: launch_embed<3>(embed, dtoks, n, H, x, st); break;
+        case 1: launch_embed<1>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
+        case 2: launch_embed<2>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
+        default: launch_embed<3>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
     }
     const bool logits_on = flags & SP_F_LOGITS;
     const size_t ps = gpart_stride;
@@ -1028,9 +1033,12 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
                     "a layer's weights are not loaded");
         require(!(argmax_host && !(flags & SP_F_ARGMAX)), SP_EINVAL, "argmax_host needs SP_F_ARGMAX");
         require(!((flags & SP_F_ARGMAX) && !(flags & SP_F_LOGITS)), SP_EINVAL, "SP_F_ARGMAX needs SP_F_LOGITS");
+        const bool feed = flags & SP_F_FEED;
+        require(!feed || n <= e->argmax_cols, SP_ESTATE,
+                "SP_F_FEED needs a previous SP_F_ARGMAX call over at least as many columns");
         for (int i = 0; i < n; ++i) {
             const sp_token &t = toks[i];
-            require(t.token >= 0 && t.token < d.vocab, SP_EINVAL, "token id out of range");
+            require(feed || (t.token >= 0 && t.token < d.vocab), SP_EINVAL, "token id out of range");
             require(t.seq >= 0 && t.seq < e->n_seq, SP_EINVAL, "sequence index out of range");
             require(t.slot >= 0 && t.slot < e->n_slots, SP_EINVAL, "slot out of range");
             require(t.pos >= 0, SP_EINVAL, "position must be non-negative");
@@ -1042,8 +1050,8 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             require(nlin + t.tree_count >= 1, SP_EINVAL, "a column must see at least one key");
         }
         const bool use_graph = flags & SP_F_GRAPH;
-        const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX | SP_F_UNFUSED);
-        if (n == 1 && (flags & SP_F_PERSISTENT)) {
+        const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX | SP_F_UNFUSED | SP_F_FEED);
+        if (n == 1 && (flags & SP_F_PERSISTENT) && !feed) {
             if (e->persistent_step(toks[0], sflags, logits_dev, argmax_host)) {
                 e->last_path = 1;
                 return;
@@ -1089,6 +1097,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         } else {
             e->step(n, sflags, ap);
         }
+        if (sflags & SP_F_ARGMAX) e->argmax_cols = n;
         if (logits_dev && (flags & SP_F_LOGITS))
             HIPCHK(hipMemcpyAsync(logits_dev, e->logits, (size_t)n * d.vocab * sizeof(float), hipMemcpyDeviceToDevice, e->stream));
         if (argmax_host) {
@@ -1135,6 +1144,15 @@ int sp_engine_kv_move(sp_engine *e, int32_t seq, int32_t n, const int32_t *src, 
                            e->d.n_kv_heads, e->n_slots, e->d.head_dim, e->d_move, e->d_move + n, n);
         HIPCHK(hipGetLastError());
         HIPCHK(hipStreamSynchronize(e->stream));
+    });
+}
+
+int sp_engine_copy_ids(sp_engine *e, int32_t n, int32_t *host) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        require(host != nullptr, SP_EINVAL, "host is NULL");
+        require(n >= 1 && n <= e->argmax_cols, SP_EINVAL, "n must be in [1, columns of the last SP_F_ARGMAX call]");
+        HIPCHK(hipMemcpyAsync(host, e->am_out, n * sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
     });
 }
 

@@ -336,6 +336,54 @@ class Qwen2Engine:
             c.length += 1
         return ids
 
+    @torch.inference_mode()
+    def decode_greedy(self, tokens, caches, steps, eos_token_id=None, burst=32, graph=True):
+        """Greedy decode of up to `steps` tokens per cache, step i + 1 taking step i's argmax on the device
+        (SP_F_FEED): no host round trip per step; the ids come back through a pinned buffer every `burst` steps.
+        tokens: the next input token of each cache.  Returns one id list per cache (the ids decode() would return
+        step by step).  With eos_token_id a sequence's list ends at its first eos, decoding stops once every
+        sequence has one, and each cache is rolled back to just after its eos (positions decoded past it are
+        dropped, as the reference rolls back by assigning `length`)."""
+        n = len(tokens)
+        if n != len(caches) or n == 0:
+            raise ValueError('one token per cache')
+        if steps <= 0:
+            return [[] for _ in range(n)]
+        for c in caches:
+            self._check_cache(c)
+            if c.window is None and c.length + steps > c.capacity:
+                raise ValueError(f'KV cache capacity {c.capacity} exceeded')
+        burst = max(1, min(int(burst), steps))
+        ring = torch.empty((burst, n), dtype=torch.int32, pin_memory=True)
+        base = ring.data_ptr()
+        start = [c.length for c in caches]
+        out = [[] for _ in range(n)]
+        done = [False] * n
+        flags = _lib.SP_F_LOGITS | _lib.SP_F_ARGMAX | (_lib.SP_F_GRAPH if graph else 0)
+        step = 0
+        while step < steps and not all(done):
+            k = min(burst, steps - step)
+            for j in range(k):
+                feed = step + j > 0
+                cols = [self._column(-1 if feed else int(t), c, c.length, c.length) for t, c in zip(tokens, caches)]
+                self.run(cols, flags | (_lib.SP_F_FEED if feed else 0))
+                _lib.check(self.lib.sp_engine_copy_ids(self.h, n, ctypes.c_void_p(base + 4 * n * j)), self.h)
+                for c in caches:
+                    c.length += 1
+            _lib.check(self.lib.sp_engine_sync(self.h), self.h)
+            ids = ring[:k].numpy()
+            for j in range(k):
+                for b in range(n):
+                    if not done[b]:
+                        t = int(ids[j, b])
+                        out[b].append(t)
+                        done[b] = eos_token_id is not None and t == eos_token_id
+            step += k
+        if eos_token_id is not None:
+            for b, c in enumerate(caches):
+                c.length = start[b] + len(out[b])
+        return out
+
     # ------------------------------------------------------------------------------------------ sampling / loops
     @staticmethod
     def sample(logits, temperature=0.0, top_k=0, top_p=1.0, generator=None):
@@ -361,11 +409,17 @@ class Qwen2Engine:
         cache = self.new_cache(len(prompt_ids) + max_new_tokens, window=window)
         if temperature <= 0:
             token = self._prefill_greedy(prompt_ids, cache)
-            for i in range(max_new_tokens):
-                yield token
-                if token == eos_token_id or i + 1 == max_new_tokens:
-                    break
-                token = int(self.decode([token], [cache])[0])
+            yield token
+            left = max_new_tokens - 1
+            # later tokens in bursts, the ids fed back on the GPU (decode_greedy); the first burst is short so the
+            # first tokens arrive early
+            burst = 8
+            while left > 0 and token != eos_token_id:
+                ids = self.decode_greedy([token], [cache], min(burst, left), eos_token_id=eos_token_id, burst=burst)[0]
+                for token in ids:
+                    yield token
+                left -= len(ids)
+                burst = min(64, burst * 2)
             return
         logits, cache = self.forward(prompt_ids, cache)
         gen = torch.Generator(device=self.device).manual_seed(seed)
@@ -419,18 +473,13 @@ class Qwen2Engine:
             self.reserve(max(len(prompts), self._pool_n), max(need, self._pool_slots))
         caches = [self.new_cache(len(p) + max_new_tokens, window=window) for p in prompts]
         tok = self.prefill(prompts, caches)
-        out = [[t] for t in tok]
+        out = [[int(t)] for t in tok]
         live = [i for i in range(len(prompts)) if tok[i] != eos_token_id]
-        for _ in range(max_new_tokens - 1):
-            if not live:
-                break
-            ids = self.decode([out[i][-1] for i in live], [caches[i] for i in live], graph=graph)
-            nl = []
-            for i, t in zip(live, ids):
-                out[i].append(int(t))
-                if int(t) != eos_token_id:
-                    nl.append(i)
-            live = nl
+        if live and max_new_tokens > 1:
+            ids = self.decode_greedy([out[i][-1] for i in live], [caches[i] for i in live], max_new_tokens - 1,
+                                     eos_token_id=eos_token_id, graph=graph)
+            for i, seq in zip(live, ids):
+                out[i] += seq
         return out
 
 
