@@ -532,6 +532,25 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
     int maxcols = 1;
     for (auto &g : p.groups) { p.mq = p.mq || g.ncols > 1; maxcols = std::max(maxcols, g.ncols); }
     const int G = d.n_heads / d.n_kv_heads;
+    bool dec_ok = true, force = false;
+#ifdef SP_GEMV_TUNE
+    dec_ok = g_tune_attn[0] >= 0;
+    force = g_tune_attn[0] > 0;
+#endif
+    // blocks per kv head and column: decode key splits of dec_keys_per_block() keys, chunk-kernel blocks of ATT_CH
+    long dec_work = 0, chunk_work = 0;
+    bool dec_cols = G <= 8 && dec_ok;
+    for (int c = 0; c < n; ++c) {
+        dec_cols = dec_cols && t[c].tree_count == 0 && nlin_of(t[c]) >= 1;
+        dec_work += (long)(nlin_of(t[c]) + dec_keys_per_block() - 1) / dec_keys_per_block() * d.n_kv_heads;
+        chunk_work += (long)(nlin_of(t[c]) + ATT_CH - 1) / ATT_CH * d.n_kv_heads;
+    }
+    // several plain columns whose 64-key chunks fill the chip but whose decode splits would not give each CU a few
+    // blocks: the multi-query kernel (MFMA scores for all query heads of a kv head) is the fastest there.  Measured per
+    // step: 16 x 1024 keys, 2 kv heads (512 chunks, 128 splits) multi-query 2.3% faster than the chunk kernel;
+    // 32 x 8192 keys, 4 kv heads (4096 splits) the decode kernel 2.8% faster; 16 ragged prompts of 16-128 keys
+    // (about 64 chunks) the chunk kernel with the rotation fused 7% faster.
+    if (n > 1 && dec_cols && chunk_work >= 256 && dec_work < 1024 && !force) p.mq = true;
     p.splits = (maxcols * G + 63) / 64;
     p.colnc.assign(n, 0);
     int mx = 1;
@@ -548,24 +567,10 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
         }
     }
     p.nchunk = graph ? max_nchunk : mx;
-    bool dec_ok = true;
-#ifdef SP_GEMV_TUNE
-    dec_ok = g_tune_attn[0] >= 0;
-#endif
-    if (!p.mq && d.n_heads / d.n_kv_heads <= 8 && dec_ok) {
+    if (!p.mq && dec_cols) {
         // the MFMA decode kernel pays off once its key splits fill the chip (long contexts, large batches); short
         // ranges stay on the 64-key chunk kernel, which spreads them over more CUs
-        p.dec = true;
-        long work = 0;
-        for (int c = 0; c < n; ++c) {
-            p.dec = p.dec && t[c].tree_count == 0 && nlin_of(t[c]) >= 1;
-            work += (long)(nlin_of(t[c]) + dec_keys_per_block() - 1) / dec_keys_per_block() * d.n_kv_heads;
-        }
-        bool force = false;
-#ifdef SP_GEMV_TUNE
-        force = g_tune_attn[0] > 0;
-#endif
-        if (work < 256 && !force) p.dec = false;
+        p.dec = dec_work >= 256 || force;
     }
     if (!p.mq && !p.dec) {
         // every column a plain ring range of its own sequence: no column sees another column's new key, so each
