@@ -145,12 +145,14 @@ __global__ void __launch_bounds__(ROPE_THREADS) k_rope_kv(RopeArgs a) {
 // ---------------------------------------------------------------------------------------------------------------
 // Split-K GQA attention.  One block per (chunk of CH visible keys, kv head, column); the G query heads of the kv
 // head share the K/V chunk staged in LDS.  Visible keys of a column: ring positions [ctx_lo, ctx_hi] then the tree
-// block (slots tree_base + j, bit j of tree_mask).  Each block records {m, l, acc[HD]} per query head; k_attn_combine
-// merges them with exp(m - M) weights.  Replaces the SDPA call with its causal/slot mask (qwen_engine.py:126-135)
+// block (slots tree_base + j, bit j of tree_mask).  Each block records {m, l, o[HD]} per query head (o = acc / l, the
+// chunk's own normalised output); k_attn_combine merges them with l exp(m - M) weights.  Replaces the SDPA call with its causal/slot mask (qwen_engine.py:126-135)
 // and attn_part.comp / attn_combine.comp.
 constexpr int ATT_CH = 64;
-// One partial record per (column, head, chunk): m and l as fp32, then acc[HD] as fp16 (half the bytes of an fp32
-// record; the rounding is below the fp16 rounding of the merged output).  Length in floats:
+// One partial record per (column, head, chunk): m and l as fp32, then o[HD] = acc / l as fp16 (half the bytes of an
+// fp32 record; o is a convex combination of the chunk's fp16 values, so it never exceeds the fp16 range, which the
+// unnormalised acc (up to l x max |v|) could; the rounding is below the fp16 rounding of the merged output).  Length
+// in floats:
 __host__ __device__ constexpr int part_floats(int HD) { return 2 + HD / 2; }
 struct AttnArgs {
     const float *q;        // [n][NH*HD]
@@ -238,8 +240,9 @@ __global__ void __launch_bounds__(64 * G) k_attn_part(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < DPL; ++i) o[i] += p * (float)v_s[j][lane + 64 * i];
     }
+    const float il = l > 0.f ? 1.f / l : 0.f;         // acc / l: bounded by max |v|, so fp16 holds it
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) ((f16 *)(out + 2))[lane + 64 * i] = (f16)o[i];
+    for (int i = 0; i < DPL; ++i) ((f16 *)(out + 2))[lane + 64 * i] = (f16)(o[i] * il);
     if (lane == 0) { out[0] = m; out[1] = l; }
 }
 
@@ -382,8 +385,9 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
 #pragma unroll
         for (int i = 0; i < DPL; ++i) o[i] += p * (float)v_s[j][lane + 64 * i];
     }
+    const float il = l > 0.f ? 1.f / l : 0.f;         // acc / l: bounded by max |v|, so fp16 holds it
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) ((f16 *)(out + 2))[lane + 64 * i] = (f16)o[i];
+    for (int i = 0; i < DPL; ++i) ((f16 *)(out + 2))[lane + 64 * i] = (f16)(o[i] * il);
     if (lane == 0) { out[0] = m; out[1] = l; }
 }
 
@@ -392,7 +396,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
 // K and V loads before the first use (one memory round trip per block).  Per sub-chunk of DEC_KC keys: S = Q K^T on
 // MFMA (rows = the G query heads of the kv head, K fragments straight from the cache), online softmax per row, P and
 // V^T staged in the wave's own LDS region, O += P V on MFMA.  The wave states are merged in wave order; a column
-// whose keys fit one split gets its fp16 attention row directly, otherwise each split writes {m, l, acc} in
+// whose keys fit one split gets its fp16 attention row directly, otherwise each split writes {m, l, acc / l} in
 // k_attn_part's layout and k_attn_combine merges the splits.
 constexpr int DEC_KC = 32;
 template <int HD, int NWV, int SUB>
@@ -529,13 +533,13 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
             out[act_off(b, (kvh * G + h) * HD + d, ldo, mtp)] = (f16)(acc / L);
         } else {
             float *pp = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nchunk + split) * part_floats(HD);
-            ((f16 *)(pp + 2))[d] = (f16)acc;
+            ((f16 *)(pp + 2))[d] = (f16)(L > 0.f ? acc / L : 0.f);
             if (d == 0) { pp[0] = M; pp[1] = L; }
         }
     }
 }
 
-// out[b][h*HD + d] (fp16) = sum_c acc_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}; one block (HD threads) per
+// out[b][h*HD + d] (fp16) = sum_c o_c[d] l_c e^{m_c - M} / sum_c l_c e^{m_c - M}; one block (HD threads) per
 // (head, column), chunk statistics loaded in parallel.
 // The chunk outputs are read in batches of CMB_BATCH with every load of a batch in flight together (the first batch
 // before the weights are known); the accumulation runs over the chunks in ascending order.
@@ -568,9 +572,9 @@ __global__ void __launch_bounds__(128) k_attn_combine(const float *part, const i
     for (int i = 1; i < (nt + 63) / 64; ++i) M = fmaxf(M, red[i]);
     float lsum = 0.f;
     for (int c = tid; c < nc; c += nt) {
-        const float wc = w_s[c] == -INFINITY ? 0.f : expf(w_s[c] - M);
+        const float wc = w_s[c] == -INFINITY ? 0.f : expf(w_s[c] - M) * l_s[c];
         w_s[c] = wc;
-        lsum += wc * l_s[c];
+        lsum += wc;
     }
     __syncthreads();
     const float L = block_sum_dpp(lsum, red + 8);
@@ -874,8 +878,9 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
             const int col = row / G, h = row - col * G;
             float *out = a.part + (((size_t)(gr.first_col + col) * a.NH + kvh * G + h) * a.nchunk + c) * part_floats(HD);
             f16 *oh = (f16 *)(out + 2);
+            const float il = lrow[j] > 0.f ? 1.f / lrow[j] : 0.f;
 #pragma unroll
-            for (int dt = 0; dt < HD / 16; ++dt) oh[16 * dt + r16] = (f16)o[dt][j];
+            for (int dt = 0; dt < HD / 16; ++dt) oh[16 * dt + r16] = (f16)(o[dt][j] * il);
             if (r16 == 0) { out[0] = mrow[j]; out[1] = lrow[j]; }
         }
     }

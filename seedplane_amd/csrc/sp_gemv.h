@@ -125,7 +125,7 @@ struct ProArgs {
     const float *w;
     float eps;
     int H;
-    // PRO_COMB: act = the attention partials [NH][nchunk][HD + 2] of column 0 merged as k_attn_combine merges them
+    // PRO_COMB: act = the attention partials [NH][nchunk][part_floats(HD)] of column 0 merged as k_attn_combine merges them
     const float *apart;
     const int *colnc;
     int NH, HD, nchunk;
@@ -230,9 +230,9 @@ __device__ __forceinline__ void pro_comb(const ProArgs &p, f16 *act, int klo, in
         for (int i = 1; i < gnw; ++i) M = fmaxf(M, red[i]);
         float lsum = 0.f;
         for (int c = gt; c < nc; c += HD) {
-            const float wc = w_s[c] == -INFINITY ? 0.f : expf(w_s[c] - M);
+            const float wc = w_s[c] == -INFINITY ? 0.f : expf(w_s[c] - M) * l_s[c];
             w_s[c] = wc;
-            lsum += wc * l_s[c];
+            lsum += wc;
         }
         __syncthreads();
         lsum = wave_sum_dpp(lsum);

@@ -1,7 +1,9 @@
-"""The two decode attention kernels against each other on the same cache state: a batch of 32 long-context columns
-(whose key splits fill the chip, so the step runs the MFMA decode kernel with split-K partials and the combine)
-against the same columns decoded one at a time (64-key chunk kernel, which the oracle tests pin).  Logits within the
-fp16-class tolerance, greedy ids identical where the top-2 margin exceeds it."""
+"""The batch decode attention kernels against the single-column one on the same cache state: a batch of 32 columns
+against the same columns decoded one at a time (64-key chunk kernel with RoPE fused, which the oracle tests pin).
+At 1100 positions (18 chunks, 5 decode splits per column and kv head) the batch runs the multi-query MFMA kernel,
+one group per column; at 4100 positions (17 decode splits, 1088 over the batch) the MFMA decode kernel with split-K
+partials and the combine.  Logits within the fp16-class tolerance, greedy ids identical where the top-2 margin
+exceeds it."""
 import pytest
 import torch
 
@@ -16,13 +18,13 @@ TOL = 2e-2
 
 
 @pytest.mark.parametrize('shape', ['small-hd64', 'qwen2-1.5b-hd128'])
-@pytest.mark.parametrize('window', [None, 1024])
-def test_batch_decode_kernel_matches_chunk_kernel(gpu_device, shape, window):
+@pytest.mark.parametrize('window,ctx', [(None, 1100), (1024, 1100), (None, 4100)])
+def test_batch_decode_kernel_matches_chunk_kernel(gpu_device, shape, window, ctx):
     if shape == 'small-hd64':
-        cfg, w = make_weights(small_cfg(), 'q8', seed=21)
+        cfg, w = make_weights(small_cfg(max_position_embeddings=8192), 'q8', seed=21)
     else:
         cfg, w = make_weights(preset('qwen2-1.5b', num_hidden_layers=2, vocab_size=4096), 'q8', seed=22)
-    B, ctx = 32, 1100
+    B = 32
     print(f'attention paths {shape} window={window}: {B} columns x {ctx} positions', flush=True)
     eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=B)
     eng.reserve(B, eng.slots_for(ctx + 8, window))
