@@ -391,6 +391,7 @@ struct sp_engine {
     char *d_upload = nullptr, *h_upload = nullptr;
     size_t upload_bytes = 0;
     hipEvent_t upload_done = nullptr;
+    int *h_ids = nullptr;        // pinned landing buffer of the greedy ids a call returns to the host
 
     // KV ring
     int n_seq = 0, n_slots = 0;
@@ -458,8 +459,9 @@ void sp_engine::free_all() {
     dev_free(pk.d_plans); dev_free(pk.d_lp); dev_free(pk.d_aux); dev_free(pk.ll); dev_free(pk.status);
     pk = Persistent{};
     if (h_upload) (void)hipHostFree(h_upload);
+    if (h_ids) (void)hipHostFree(h_ids);
     if (upload_done) (void)hipEventDestroy(upload_done);
-    h_upload = nullptr; upload_done = nullptr; d_upload = nullptr;
+    h_upload = nullptr; h_ids = nullptr; upload_done = nullptr; d_upload = nullptr;
     dtoks = nullptr; dgroups = nullptr; dcolnc = nullptr;
     if (own_stream && stream) (void)hipStreamDestroy(stream);
     if (capture_stream) (void)hipStreamDestroy(capture_stream);
@@ -498,6 +500,7 @@ void sp_engine::alloc_activations() {
     dgroups = (AttnGroup *)(d_upload + tb);
     dcolnc = (int *)(d_upload + tb + gb);
     HIPCHK(hipHostMalloc((void **)&h_upload, upload_bytes, hipHostMallocDefault));
+    HIPCHK(hipHostMalloc((void **)&h_ids, (size_t)maxT * sizeof(int), hipHostMallocDefault));
     HIPCHK(hipEventCreateWithFlags(&upload_done, hipEventDisableTiming));
     d_move = dev_alloc<int>(2 * 64);
     HIPCHK(hipMemset(xn, 0, tpad * kmax * sizeof(f16)));
@@ -1106,8 +1109,10 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         if (logits_dev && (flags & SP_F_LOGITS))
             HIPCHK(hipMemcpyAsync(logits_dev, e->logits, (size_t)n * d.vocab * sizeof(float), hipMemcpyDeviceToDevice, e->stream));
         if (argmax_host) {
-            HIPCHK(hipMemcpyAsync(argmax_host, e->am_out, n * sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
+            // through pinned memory: a device-to-host copy into pageable memory is staged by the runtime
+            HIPCHK(hipMemcpyAsync(e->h_ids, e->am_out, n * sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
             HIPCHK(hipStreamSynchronize(e->stream));
+            std::memcpy(argmax_host, e->h_ids, n * sizeof(int32_t));
         }
     });
 }
@@ -1365,8 +1370,12 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         // the kernel checks every node / trial / token index it follows before using it (err = 2 if one is bad)
         hipStream_t st = (hipStream_t)stream;
         // exchange words + error word, one set per device, zeroed once; tags never repeat within 2^20 launches, so
-        // neither needs clearing between launches (the kernel writes every entry of out_dev itself)
-        static std::map<int, std::pair<unsigned long long *, unsigned *>> scratch_of;
+        // neither needs clearing between launches (the kernel writes every entry of out_dev itself).  The error word
+        // and the result come back through a pinned block (device-to-host copies into pageable memory are staged
+        // by the runtime and cost tens of microseconds each); out_host may be any host memory.
+        struct AccScratch { unsigned long long *xbuf; unsigned *err; int32_t *pin; };
+        constexpr int PIN_OUT = 16;                      // out at int 16 of the pinned block, the error word at 0
+        static std::map<int, AccScratch> scratch_of;
         static unsigned launches = 0;
         int dev = 0;
         HIPCHK(hipGetDevice(&dev));
@@ -1375,19 +1384,23 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
             unsigned long long *xb = dev_alloc<unsigned long long>(4 * ACC_NB * 4);
             unsigned *er = dev_alloc<unsigned>(1);
             HIPCHK(hipMemset(xb, 0, 4 * ACC_NB * 4 * sizeof(unsigned long long)));
-            it = scratch_of.emplace(dev, std::make_pair(xb, er)).first;
+            int32_t *pin = nullptr;
+            HIPCHK(hipHostMalloc((void **)&pin, (PIN_OUT + 64 + 4) * sizeof(int32_t), hipHostMallocDefault));
+            it = scratch_of.emplace(dev, AccScratch{xb, er, pin}).first;
         }
+        const AccScratch &sc = it->second;
         launches = launches % 0xFFFFFu + 1;
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token_dev, trial_start_dev, n_trials_dev, trials_dev, u_dev,
-                     n_u, 1.0 / temperature, it->second.first, it->second.second, launches << 12, n_nodes,
-                     n_trials_total, out_dev, max_depth};
+                     n_u, 1.0 / temperature, sc.xbuf, sc.err, launches << 12, n_nodes, n_trials_total, out_dev,
+                     max_depth};
         void *args[] = {&a};
         HIPCHK(hipLaunchCooperativeKernel((const void *)k_accept_tree, dim3(ACC_NB), dim3(ACC_T), args, 0, st));
-        unsigned err = 0;
-        HIPCHK(hipMemcpyAsync(&err, it->second.second, sizeof(unsigned), hipMemcpyDeviceToHost, st));
+        HIPCHK(hipMemcpyAsync(sc.pin, sc.err, sizeof(unsigned), hipMemcpyDeviceToHost, st));
         if (out_host)
-            HIPCHK(hipMemcpyAsync(out_host, out_dev, (max_depth + 4) * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+            HIPCHK(hipMemcpyAsync(sc.pin + PIN_OUT, out_dev, (max_depth + 4) * sizeof(int32_t), hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
+        const unsigned err = (unsigned)sc.pin[0];
+        if (out_host) std::memcpy(out_host, sc.pin + PIN_OUT, (max_depth + 4) * sizeof(int32_t));
         const unsigned code = (err & ~0xfffu) == (launches << 12) ? err & 0xfffu : 0u;
         require(code != 2, SP_EINVAL, "malformed tree: node, trial or token index out of range");
         require(code == 0, SP_EHIP, "acceptance exchange timed out");
