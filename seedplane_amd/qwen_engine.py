@@ -26,6 +26,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from . import native_bundle
 
 GROUP = 32
 
@@ -64,7 +65,11 @@ class Qwen2Engine:
     """Inference-only Qwen2/Qwen2.5 runtime with a persistent HBM KV cache (reference: qwen_engine.py:32-166)."""
 
     def __init__(self, bundle=None, device='cuda', dtype=None, max_tokens=64, config=None, tensors=None):
-        if tensors is None:
+        if tensors is None and native_bundle.is_bundle(bundle):
+            # seedplane-bundle/2 directory (seedplane.json + weights.spw, SHA-256 checked)
+            self.bundle = Path(bundle)
+            self.config, tensors = native_bundle.load(self.bundle)
+        elif tensors is None:
             self.bundle = Path(bundle)
             self.config = json.loads((self.bundle / 'config.json').read_text())
         else:
