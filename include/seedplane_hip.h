@@ -207,6 +207,16 @@ int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_d
 int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32_t *row_dev, const double *u_dev,
                  int32_t n, double temperature, int32_t *out_dev, void *hip_stream);
 
+/* Replaces Qwen2Engine.sample with top_k / top_p (qwen_engine.py:149-156) and the native Sampler::distribution +
+ * draw (native/vulkan_decode/sampler.hpp:22-57, 93-97) on the GPU: z = fp32(logits / T); top_k > 0 (and < vocab)
+ * keeps z >= the k-th largest z (ties kept); top_p < 1 keeps the prefix of the z-descending order (ties by index)
+ * whose exclusive cumulative mass is <= top_p of the kept mass; out_dev[s] = the inverse-CDF draw over what is kept
+ * with uniform u_dev[s] (masses are 64-bit fixed point, exp(z - z_max) * 2^40, so every sum is exact).  One block
+ * per draw; all pointers are device memory.  Errors: NULL pointers, bad sizes, temperature <= 0, top_p <= 0. */
+int sp_op_sample_filtered(const float *logits_dev, int32_t vocab, int32_t ld, const int32_t *row_dev,
+                          const double *u_dev, int32_t n, double temperature, int32_t top_k, double top_p,
+                          int32_t *out_dev, void *hip_stream);
+
 /* No counterpart in the reference, whose verifier is greedy only (seedplane/speculative.py:55-92; README.md:69):
  * speculative acceptance over a draft tree with residual resampling.  Node 0 is the root (the last committed
  * token).  The trials of node i are trials_dev[trial_start[i] .. trial_start[i] + n_trials[i]): the child each

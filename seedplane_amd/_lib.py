@@ -70,6 +70,8 @@ SIGNATURES = {
     'sp_op_gemv': (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
     'sp_op_sample': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_int32, ctypes.c_double, c_void_p,
                              c_void_p]),
+    'sp_op_sample_filtered': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_int32, ctypes.c_double,
+                                      c_int32, ctypes.c_double, c_void_p, c_void_p]),
     'sp_op_accept_tree': (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_int32, c_void_p, c_int32, ctypes.c_double, c_int32, c_void_p, c_void_p,
                                   c_void_p, c_void_p]),

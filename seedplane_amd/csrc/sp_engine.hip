@@ -1352,6 +1352,20 @@ int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32
     });
 }
 
+int sp_op_sample_filtered(const float *logits_dev, int32_t vocab, int32_t ld, const int32_t *row_dev,
+                          const double *u_dev, int32_t n, double temperature, int32_t top_k, double top_p,
+                          int32_t *out_dev, void *stream) {
+    return guarded(nullptr, [&] {
+        require(logits_dev && row_dev && u_dev && out_dev, SP_EINVAL, "NULL pointer");
+        require(vocab >= 1 && ld >= vocab && n >= 1 && n <= 65535, SP_EINVAL, "bad sizes");
+        require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
+        require(top_p > 0.0, SP_EINVAL, "top_p must be positive");
+        hipLaunchKernelGGL(k_sample_filtered, dim3(n), dim3(FS_THREADS), 0, (hipStream_t)stream, logits_dev, vocab, ld,
+                           row_dev, u_dev, (float)temperature, top_k, top_p, out_dev);
+        HIPCHK(hipGetLastError());
+    });
+}
+
 int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld, int32_t n_nodes,
                       const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
                       const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,

@@ -432,3 +432,203 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         if (final_tok >= 0) a.out[a.max_depth + 1] = final_tok;   // only the block owning the draw has it
     }
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Filtered sampling: temperature, top-k and top-p (nucleus) exactly as Qwen2Engine.sample defines them
+// (qwen_engine.py:146-156; native Sampler::distribution, sampler.hpp:22-57), one block of FS_THREADS per draw.
+//   z_i   = fp32(l_i / T);  the order is z descending, ties by ascending index (the native sampler's comparator);
+//   top-k (0 < k < V): keep z_i >= the k-th largest z (ties at the cutoff kept);
+//   mass  m_i = floor(exp(z_i - z_max) * 2^40) as a 64-bit integer (fp64 exp; z_max = the row maximum, so m <= 2^40
+//         and a row sum stays below 2^58): sums are exact and independent of order, so the kernel needs no fixed
+//         summation tree; the 2^-40 quantum is far below any probability the cut or the draw can resolve;
+//   top-p (p < 1): with F the total mass of the kept tokens, keep the sorted prefix whose exclusive cumulative mass
+//         is <= floor(p * F) (first index whose inclusive mass exceeds that, and everything before it);
+//   draw: target = floor(u * K) (clamped below K) over the kept mass K; the token is the first in sorted order whose
+//         inclusive cumulative mass exceeds the target (inverse CDF, Sampler::draw, sampler.hpp:93-97).
+// Selections in sorted order never sort: a radix descent over the 32-bit order key (8 bits per level, LDS histograms
+// of counts and 64-bit masses restricted to the candidates) finds the bin holding the k-th token / the target mass;
+// at the last level the bin is one z value, whose tokens (equal masses) are ordered by index.
+constexpr int FS_THREADS = 1024;
+
+__device__ __forceinline__ uint32_t fs_key(float z) {      // monotone: larger z, larger key
+    const uint32_t b = __float_as_uint(z);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float fs_unkey(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+__device__ __forceinline__ unsigned long long fs_mass(float z, float zmax) {
+    return (unsigned long long)(exp((double)z - (double)zmax) * 1099511627776.0);    // 2^40
+}
+
+struct FsShared {
+    unsigned long long hmass[256];
+    unsigned int hcnt[256];
+    unsigned long long red64[FS_THREADS / 64];
+    unsigned int redu[FS_THREADS / 64];
+    unsigned int sel_bin;
+    unsigned long long above;
+    unsigned int scan[FS_THREADS];
+};
+
+// Block sum of a 64-bit integer (exact, any order).
+__device__ __forceinline__ unsigned long long fs_block_sum(unsigned long long v, FsShared &sh) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh.red64[w] = v;
+    __syncthreads();
+    unsigned long long t = 0;
+    for (int i = 0; i < FS_THREADS / 64; ++i) t += sh.red64[i];
+    return t;
+}
+
+// First token (z descending, index ascending) among the candidates (key >= kmin) whose inclusive cumulative mass
+// exceeds `target`.  Returns its key; *above_out = the mass of every candidate before the key's tie group,
+// *rank_out = the token's rank inside its tie group (index order).  The caller guarantees target < total mass.
+__device__ uint32_t fs_select_mass(const float *row, int V, float T, float zmax, uint32_t kmin,
+                                   unsigned long long target, FsShared &sh, unsigned long long *above_out,
+                                   unsigned long long *rank_out) {
+    uint32_t prefix = 0, mask = 0;
+    unsigned long long above = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = threadIdx.x; b < 256; b += FS_THREADS) { sh.hmass[b] = 0; sh.hcnt[b] = 0; }
+        __syncthreads();
+        for (int i = threadIdx.x; i < V; i += FS_THREADS) {
+            const float z = __fdiv_rn(row[i], T);
+            const uint32_t k = fs_key(z);
+            if (k >= kmin && (k & mask) == prefix) {
+                const int b = (k >> shift) & 255;
+                atomicAdd(&sh.hmass[b], fs_mass(z, zmax));
+                atomicAdd(&sh.hcnt[b], 1u);
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int chosen = -1, last_nz = -1;
+            unsigned long long a = above;
+            for (int b = 255; b >= 0; --b) {
+                if (sh.hcnt[b] == 0) continue;
+                if (a + sh.hmass[b] > target) { chosen = b; break; }
+                a += sh.hmass[b];
+                last_nz = b;
+            }
+            if (chosen < 0) {            // cannot happen for target < total; keep the last candidate bin
+                chosen = last_nz;
+                a -= sh.hmass[last_nz < 0 ? 0 : last_nz];
+            }
+            sh.sel_bin = (unsigned)chosen;
+            sh.above = a;
+        }
+        __syncthreads();
+        prefix |= sh.sel_bin << shift;
+        mask |= 255u << shift;
+        above = sh.above;
+        __syncthreads();
+    }
+    const unsigned long long m = fs_mass(fs_unkey(prefix), zmax);
+    *above_out = above;
+    *rank_out = m > 0 ? (target - above) / m : 0;
+    return prefix;
+}
+
+// Index of the rank-th token (index order) whose key equals `key` (a block-wide scan over contiguous chunks).
+__device__ int fs_index_of(const float *row, int V, float T, uint32_t key, unsigned long long rank, FsShared &sh) {
+    const int C = (V + FS_THREADS - 1) / FS_THREADS, lo = threadIdx.x * C, hi = min(V, lo + C);
+    unsigned int cnt = 0;
+    for (int i = lo; i < hi; ++i) cnt += fs_key(__fdiv_rn(row[i], T)) == key;
+    sh.scan[threadIdx.x] = cnt;
+    __syncthreads();
+    if (threadIdx.x == 0) {                 // exclusive prefix over the threads, in order
+        unsigned int s = 0;
+        for (int t = 0; t < FS_THREADS; ++t) { const unsigned int c = sh.scan[t]; sh.scan[t] = s; s += c; }
+    }
+    __syncthreads();
+    const unsigned long long before = sh.scan[threadIdx.x];
+    __shared__ int found;
+    if (threadIdx.x == 0) found = -1;
+    __syncthreads();
+    if (rank >= before && rank < before + cnt) {
+        unsigned long long r = rank - before;
+        for (int i = lo; i < hi; ++i)
+            if (fs_key(__fdiv_rn(row[i], T)) == key) {
+                if (r == 0) { found = i; break; }
+                --r;
+            }
+    }
+    __syncthreads();
+    return found;
+}
+
+// out[s] = filtered draw from row rows[s] with uniform u[s]; top_k <= 0 or >= V: no top-k; top_p >= 1: no top-p.
+__global__ void __launch_bounds__(FS_THREADS) k_sample_filtered(const float *logits, int V, int ld, const int *rows,
+                                                               const double *u, float T, int top_k, double top_p,
+                                                               int *out) {
+    __shared__ FsShared sh;
+    const int s = blockIdx.x;
+    const float *row = logits + (size_t)rows[s] * ld;
+    // ---- maximum z (its key)
+    uint32_t kmax = 0;
+    for (int i = threadIdx.x; i < V; i += FS_THREADS) kmax = max(kmax, fs_key(__fdiv_rn(row[i], T)));
+    for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+    if ((threadIdx.x & 63) == 0) sh.redu[threadIdx.x >> 6] = kmax;
+    __syncthreads();
+    kmax = 0;
+    for (int i = 0; i < FS_THREADS / 64; ++i) kmax = max(kmax, sh.redu[i]);
+    const float zmax = fs_unkey(kmax);
+    // ---- top-k cutoff: the k-th largest key by a radix descent on counts (ties at the cutoff kept)
+    uint32_t kmin = 0;
+    if (top_k > 0 && top_k < V) {
+        uint32_t prefix = 0, mask = 0;
+        unsigned int rem = (unsigned)top_k;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int b = threadIdx.x; b < 256; b += FS_THREADS) sh.hcnt[b] = 0;
+            __syncthreads();
+            for (int i = threadIdx.x; i < V; i += FS_THREADS) {
+                const uint32_t k = fs_key(__fdiv_rn(row[i], T));
+                if ((k & mask) == prefix) atomicAdd(&sh.hcnt[(k >> shift) & 255], 1u);
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                unsigned int a = 0;
+                int b = 255;
+                for (; b > 0; --b) {
+                    if (a + sh.hcnt[b] >= rem) break;
+                    a += sh.hcnt[b];
+                }
+                sh.sel_bin = (unsigned)b;
+                sh.redu[0] = rem - a;
+            }
+            __syncthreads();
+            prefix |= sh.sel_bin << shift;
+            mask |= 255u << shift;
+            rem = sh.redu[0];
+            __syncthreads();
+        }
+        kmin = prefix;
+    }
+    // ---- total candidate mass
+    unsigned long long F = 0;
+    for (int i = threadIdx.x; i < V; i += FS_THREADS) {
+        const float z = __fdiv_rn(row[i], T);
+        if (fs_key(z) >= kmin) F += fs_mass(z, zmax);
+    }
+    F = fs_block_sum(F, sh);
+    // ---- top-p: kept mass K = inclusive mass of the first token whose inclusive mass exceeds floor(p * F)
+    unsigned long long K = F;
+    if (top_p < 1.0) {
+        const unsigned long long tp = (unsigned long long)(top_p * (double)F);
+        if (tp < F) {
+            unsigned long long above, rank;
+            const uint32_t key = fs_select_mass(row, V, T, zmax, kmin, tp, sh, &above, &rank);
+            K = above + (rank + 1) * fs_mass(fs_unkey(key), zmax);
+        }
+    }
+    // ---- the draw
+    unsigned long long tgt = (unsigned long long)(u[s] * (double)K);
+    if (tgt >= K) tgt = K - 1;
+    unsigned long long above, rank;
+    const uint32_t key = fs_select_mass(row, V, T, zmax, kmin, tgt, sh, &above, &rank);
+    const int tok = fs_index_of(row, V, T, key, rank, sh);
+    if (threadIdx.x == 0) out[s] = tok;
+}

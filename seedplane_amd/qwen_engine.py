@@ -426,14 +426,36 @@ class Qwen2Engine:
                 left -= len(ids)
                 burst = min(64, burst * 2)
             return
+        # T > 0: each token is drawn on the GPU (sp_op_sample_filtered: temperature, top-k, top-p, inverse CDF) with
+        # the counter-based uniform u(seed, step); the reference draws from the same distribution with
+        # torch.multinomial and a torch.Generator(seed), so the random streams differ
+        from .speculative import uniforms
         logits, cache = self.forward(prompt_ids, cache)
-        gen = torch.Generator(device=self.device).manual_seed(seed)
-        for _ in range(max_new_tokens):
-            token = self.sample(logits[-1], temperature, top_k, top_p, gen)
+        row = torch.zeros(1, dtype=torch.int32, device=self.device)
+        for step in range(max_new_tokens):
+            token = self.sample_gpu(logits, [0], uniforms(seed, step, 1), temperature, top_k, top_p, row)[0]
             yield token
             if token == eos_token_id:
                 break
             logits, cache = self.forward([token], cache)
+
+    def sample_gpu(self, logits, rows, u, temperature, top_k=0, top_p=1.0, rows_dev=None):
+        """Filtered draws on the GPU: token s from softmax(logits[rows[s]] / T) after top-k / top-p, by inverse CDF
+        with uniform u[s] (sp_op_sample_filtered).  `logits` is a 2-D fp32 CUDA tensor; returns a list of ids."""
+        if temperature <= 0:
+            raise ValueError('temperature must be positive (T <= 0 is the greedy argmax)')
+        if logits.dim() != 2 or logits.dtype != torch.float32 or logits.device.type != 'cuda':
+            raise ValueError('logits must be a 2-D fp32 GPU tensor')
+        dev = logits.device
+        r = rows_dev if rows_dev is not None else torch.tensor(list(rows), dtype=torch.int32, device=dev)
+        ud = torch.as_tensor(np.asarray(u, dtype=np.float64)).to(dev, non_blocking=False)
+        out = torch.empty(len(ud), dtype=torch.int32, device=dev)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        _lib.check(self.lib.sp_op_sample_filtered(ctypes.c_void_p(logits.data_ptr()), logits.shape[1],
+                                                  logits.stride(0), ctypes.c_void_p(r.data_ptr()),
+                                                  ctypes.c_void_p(ud.data_ptr()), len(ud), float(temperature),
+                                                  int(top_k), float(top_p), ctypes.c_void_p(out.data_ptr()), stream))
+        return out.cpu().tolist()
 
     def _prefill_greedy(self, prompt_ids, cache):
         ids = [int(t) for t in prompt_ids]
