@@ -18,8 +18,10 @@ Text needs the bundle's tokenizer.json (the HF `tokenizers` library reads it, as
 file).  Without it, generation from token ids still works: tokens are recorded in `last_tokens` and no text is
 yielded; tokenize / detokenize / chat raise RuntimeError.
 
-The attention is full over `ctx` positions.  The reference's shard-window boundary modes (--mode rebuild / shadow /
-reuse, qwen_vk.cpp:686-690) are not part of this engine; asking for one raises ValueError.
+The attention is full over `ctx` positions unless a shard-window mode is asked for (qwen_vk.cpp:686-690): 'rebuild' /
+'rebuild-batch' and 'shadow' / 'shadow-batch' run the exact boundary policies of seedplane_amd.engine.ShardedSession
+with the bundle's plan (seedplane.json) or the default ShardPlan; the approximate 'reuse' mode raises ValueError.
+Sampling at temperature > 0 (top-k / top-p) draws on the GPU with counter-based uniforms u(seed, draw counter).
 """
 import ctypes.util
 import json
@@ -87,10 +89,12 @@ class NativeEngine:
         from .qwen_engine import Qwen2Engine
         path = find_engine(engine)
         if mode is not None and mode != 'full':
-            if mode in _MODES:
-                raise ValueError(f'mode {mode!r} is not available in this engine: it attends over the full context '
-                                 f'(pass full=True or mode=None)')
-            raise ValueError(f'bad mode {mode!r}')
+            if mode == 'reuse':
+                raise ValueError("mode 'reuse' (approximate halo reuse) is not available in this engine: use "
+                                 "'rebuild' or 'shadow' (exact), or full attention")
+            if mode not in _MODES:
+                raise ValueError(f'bad mode {mode!r}')
+        sharded = mode not in (None, 'full') and not full
         if extra_args:
             raise ValueError(f'unknown engine arguments {list(extra_args)}')
         if _lib._lib is None:
@@ -117,10 +121,25 @@ class NativeEngine:
         self.im_end_id = self.tok.token_to_id('<|im_end|>') if self.tok is not None else None
         self._seq, self._done, self._cache = [], 0, None
         self._closed = False
-        self.engine.reserve(1, self.positions)
-        self.info = {'ready': True, 'device': torch.cuda.get_device_name(self.engine.device), 'mode': 'full',
-                     'plan': {'shard': self.positions, 'halo': 0, 'sinks': 0}, 'positions': self.positions,
-                     'window_slots': self.positions}
+        self._draws = 0                  # uniforms drawn so far (the counter of u(seed, counter))
+        self._shard = None
+        if sharded:
+            from .engine import ShardPlan, ShardedSession
+            from . import native_bundle
+            plan = (native_bundle.read_manifest(self.bundle)['plan'] if native_bundle.is_bundle(self.bundle)
+                    else {'shard': 512, 'halo': 256, 'sinks': 4})
+            self._plan = ShardPlan(int(plan['shard']), int(plan['halo']), int(plan['sinks']))
+            self._shard_mode = 'rebuild' if mode.startswith('rebuild') else 'shadow'
+            self._shard = ShardedSession(self.engine, self._plan, self._shard_mode)
+            window = self._shard.capacity
+            plan_info = {'shard': self._plan.shard, 'halo': self._plan.halo, 'sinks': self._plan.sinks}
+        else:
+            self.engine.reserve(1, self.positions)
+            window = self.positions
+            plan_info = {'shard': self.positions, 'halo': 0, 'sinks': 0}
+        self.info = {'ready': True, 'device': torch.cuda.get_device_name(self.engine.device),
+                     'mode': mode if sharded else 'full', 'plan': plan_info, 'positions': self.positions,
+                     'window_slots': window}
         self.last = None
         self.last_tokens = []
 
@@ -152,6 +171,8 @@ class NativeEngine:
             raise RuntimeError('engine exited: closed')
 
     def _session_cache(self):
+        if self._shard is not None:
+            return None
         if self._cache is None:
             self._cache = self.engine.new_cache(self.positions)
             self._done = 0
@@ -179,7 +200,7 @@ class NativeEngine:
                'decode_s': 0.0, 'decode_tok_s': 0.0, 'position': 0}
         dec = _TextStream(self.tok)
         greedy = sp['temperature'] <= 0
-        gen = None if greedy else torch.Generator(device=eng.device).manual_seed(int(sp['seed']))
+        sh = self._shard
         t0 = time.perf_counter()
         try:
             pending = self._seq[self._done:]
@@ -187,7 +208,10 @@ class NativeEngine:
                 raise RuntimeError('nothing to continue from: the session is empty')
             if len(self._seq) > self.positions:
                 raise _ContextFull()
-            if greedy:
+            if sh is not None:
+                logits = sh.feed(pending)[None]
+                nxt = int(torch.argmax(logits[0])) if greedy else None
+            elif greedy:
                 nxt = int(eng.prefill([pending], [cache])[0])
                 logits = None
             else:
@@ -197,7 +221,7 @@ class NativeEngine:
             res['prefill_s'] = time.perf_counter() - t0
             t0 = time.perf_counter()
             while True:
-                t = nxt if greedy else eng.sample(logits[-1], sp['temperature'], sp['top_k'], sp['top_p'], gen)
+                t = nxt if greedy else self._draw(logits, sp)
                 self._seq.append(int(t))
                 res['generated'] += 1
                 self.last_tokens.append(int(t))
@@ -212,7 +236,10 @@ class NativeEngine:
                     break
                 if len(self._seq) > self.positions:
                     raise _ContextFull()
-                if greedy:
+                if sh is not None:
+                    logits = sh.step(int(t))[None]
+                    nxt = int(torch.argmax(logits[0])) if greedy else None
+                elif greedy:
                     nxt = int(eng.decode([int(t)], [cache])[0])
                 else:
                     logits, _ = eng.forward([int(t)], cache)
@@ -255,9 +282,20 @@ class NativeEngine:
         self._live()
         return {'position': len(self._seq), 'processed': self._done, 'tokens': list(self._seq)}
 
+    def _draw(self, logits, sp):
+        """One GPU draw from the last logits row (temperature, top-k, top-p) with the next seeded uniform."""
+        from .speculative import uniforms
+        u = uniforms(int(sp['seed']), self._draws, 1)
+        self._draws += 1
+        return self.engine.sample_gpu(logits[-1:], [0], u, sp['temperature'], sp['top_k'], sp['top_p'])[0]
+
     def reset(self):
         self._live()
         self._seq, self._done = [], 0
+        if self._shard is not None:
+            from .engine import ShardedSession
+            self._shard = None                     # release the old windows before the new session takes slots
+            self._shard = ShardedSession(self.engine, self._plan, self._shard_mode)
         if self._cache is not None:
             self._cache.length = 0
 

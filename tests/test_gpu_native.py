@@ -109,3 +109,21 @@ def test_tokenizer_chat_and_errors(gpu_device, tmp_path):
             list(eng.generate(ids=[cfg['vocab_size'] + 5]))
     with pytest.raises(RuntimeError):
         eng.state()                                         # closed
+
+
+@pytest.mark.parametrize('mode', ['shadow-batch', 'rebuild'])
+def test_sharded_modes_follow_the_bundle_plan(gpu_device, tmp_path, mode):
+    from seedplane_amd import native_bundle
+    from seedplane_amd.engine import ShardPlan, ShardedSession
+    d, cfg, _ = _bundle(tmp_path)
+    sp = native_bundle.convert(d, tmp_path / 'b.sp', shard=8, halo=4, sinks=2)
+    prompt = random_prompt(13, cfg['vocab_size'] - len(SPECIAL), seed=4)
+    plain = Qwen2Engine(tmp_path / 'b.sp', max_tokens=16)
+    ref = list(ShardedSession(plain, ShardPlan(8, 4, 2), mode.split('-')[0]).generate(prompt, max_new_tokens=10))
+    with NativeEngine(tmp_path / 'b.sp', mode=mode, max_new_tokens=10, ctx=256) as eng:
+        assert eng.info['mode'] == mode and eng.info['plan'] == sp['plan'] and eng.info['window_slots'] == 14
+        list(eng.generate(ids=prompt, stop=[]))
+        assert eng.last_tokens == ref
+        eng.reset()
+        list(eng.generate(ids=prompt, stop=[]))
+        assert eng.last_tokens == ref
