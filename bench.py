@@ -145,6 +145,31 @@ def verify_cost(eng, cfg, prefix=2048, n_branches=8, depth=4, reps=20):
             'mfma_frac_f16': round(flops / t_verify / PEAK_F16, 4)}
 
 
+def sampling_cost(eng, V, rows=16, reps=20):
+    """GPU filtered draws (temperature 0.8, top-k / top-p) over `rows` fp32 logits rows of the full vocabulary:
+    microseconds per launch of `rows` draws (HIP events on the launching stream) and per draw, for each filter."""
+    import numpy as np
+    import torch
+    from seedplane_amd.speculative import uniforms
+    g = torch.Generator(device='cuda').manual_seed(0)
+    lg = torch.randn((rows, V), generator=g, device='cuda') * 3.0
+    rid = torch.arange(rows, dtype=torch.int32, device='cuda')
+    res = {}
+    for name, k, p in (('top_k50_top_p0.9', 50, 0.9), ('top_p0.9', 0, 0.9), ('temperature_only', 0, 1.0)):
+        u = uniforms(1, 0, rows)
+        eng.sample_gpu(lg, None, u, 0.8, k, p, rows_dev=rid)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        sync()
+        e0.record()
+        for i in range(reps):
+            eng.sample_gpu(lg, None, uniforms(1, i, rows), 0.8, k, p, rows_dev=rid)
+        e1.record()
+        sync()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        res[name] = {'us_per_launch': round(us, 1), 'draws_per_launch': rows}
+    return res
+
+
 TRAFFIC_FILE = ROOT / 'profiles' / 'k_gemv_q8_gate_up_traffic.md'
 
 
@@ -245,6 +270,9 @@ def workload_c3(args, out):
         verify = verify_cost(eng, cfg)
         log(f'verify: {verify}')
 
+    sampling = sampling_cost(eng, cfg['vocab_size'])
+    log(f'sampling: {sampling}')
+
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
@@ -260,7 +288,7 @@ def workload_c3(args, out):
                            'layers': cfg['num_hidden_layers'], 'hidden': cfg['hidden_size'],
                            'vocab': cfg['vocab_size'], 'window': W, 'prompt': args.prompt},
                 'hbm_frac_step': round(step_bytes * tok_s / PEAK_HBM, 4), 'bytes_per_token': step_bytes,
-                'bs16': bs16, 'verify': verify, 'roofline': roofline, 'cpu_baseline': cpu})
+                'bs16': bs16, 'verify': verify, 'sampling': sampling, 'roofline': roofline, 'cpu_baseline': cpu})
 
 
 def workload_verify(args, out):

@@ -471,6 +471,84 @@ struct FsShared {
     unsigned int scan[FS_THREADS];
 };
 
+// Histogram add with the wave's lanes combined per bin first: most keys of a row share their top bits, and 64 lanes
+// adding to one LDS word serialise.  Up to FS_AGG distinct bins of the wave are combined (one atomic per bin, from
+// the lowest active lane); lanes left after that add on their own.  Integer sums: the result is order-independent.
+constexpr int FS_AGG = 1;
+constexpr int FS_U = 16;             // elements per thread whose loads are issued together in every pass
+template <bool MASS>
+__device__ __forceinline__ void fs_hist_add(FsShared &sh, bool act, int bin, unsigned long long mass) {
+    const int lane = threadIdx.x & 63;
+    for (int it = 0; it < FS_AGG; ++it) {
+        const unsigned long long pend = __ballot(act);
+        if (pend == 0) return;
+        const int leader = __ffsll((long long)pend) - 1;
+        const int lb = __shfl(bin, leader);
+        const bool mine = act && bin == lb;
+        const unsigned long long mm = __ballot(mine);
+        if constexpr (MASS) {
+            unsigned long long v = mine ? mass : 0ull;
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+            if (lane == leader) atomicAdd(&sh.hmass[lb], v);
+        }
+        if (lane == leader) atomicAdd(&sh.hcnt[lb], (unsigned)__popcll(mm));
+        act = act && !mine;
+    }
+    if (act) {
+        if constexpr (MASS) atomicAdd(&sh.hmass[bin], mass);
+        atomicAdd(&sh.hcnt[bin], 1u);
+    }
+}
+
+// Inclusive prefix sums over the 64 lanes of a wave.
+template <typename I>
+__device__ __forceinline__ I fs_wave_scan(I v) {
+    const int lane = threadIdx.x & 63;
+    for (int o = 1; o < 64; o <<= 1) {
+        const I t = __shfl_up(v, o);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+// Bin choice of one radix level, by wave 0 (bins in descending order, 4 per lane: lane l holds 255 - 4l - j).
+// MASS: the first bin at which above + (mass of the bins before it, inclusive) exceeds `target`; sh.above = the mass
+// before that bin.  !MASS: the first bin at which the running count reaches `rem`; sh.redu[0] = rem minus the count
+// before it.  Same choice as walking the bins one by one from 255 down.
+template <bool MASS>
+__device__ __forceinline__ void fs_choose_bin(FsShared &sh, unsigned long long above, unsigned long long target,
+                                              unsigned int rem) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    unsigned long long v[4], ls = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int b = 255 - 4 * lane - j;
+        v[j] = MASS ? sh.hmass[b] : (unsigned long long)sh.hcnt[b];
+        ls += v[j];
+    }
+    const unsigned long long incl = fs_wave_scan<unsigned long long>(ls);
+    const bool hit = MASS ? above + incl > target : incl >= (unsigned long long)rem;
+    const unsigned long long m = __ballot(hit);
+    const int L = m ? __ffsll((long long)m) - 1 : 63;
+    if (lane == L) {
+        unsigned long long a = (MASS ? above : 0ull) + (incl - ls);
+        int chosen = 255 - 4 * lane - 3;
+        bool found = false;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (found) continue;
+            const bool take = MASS ? a + v[j] > target : a + v[j] >= (unsigned long long)rem;
+            if (take) { chosen = 255 - 4 * lane - j; found = true; }
+            else a += v[j];
+        }
+        if (!found) a -= v[3];     // walked past the lane's last bin: that bin is the choice (the serial walk ends there)
+        sh.sel_bin = (unsigned)chosen;
+        if (MASS) sh.above = a;
+        else sh.redu[0] = rem - (unsigned)a;
+    }
+}
+
 // Block sum of a 64-bit integer (exact, any order).
 __device__ __forceinline__ unsigned long long fs_block_sum(unsigned long long v, FsShared &sh) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -494,32 +572,24 @@ __device__ uint32_t fs_select_mass(const float *row, int V, float T, float zmax,
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (int b = threadIdx.x; b < 256; b += FS_THREADS) { sh.hmass[b] = 0; sh.hcnt[b] = 0; }
         __syncthreads();
-        for (int i = threadIdx.x; i < V; i += FS_THREADS) {
-            const float z = __fdiv_rn(row[i], T);
-            const uint32_t k = fs_key(z);
-            if (k >= kmin && (k & mask) == prefix) {
-                const int b = (k >> shift) & 255;
-                atomicAdd(&sh.hmass[b], fs_mass(z, zmax));
-                atomicAdd(&sh.hcnt[b], 1u);
+        for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {    // block-uniform trip count: whole waves vote
+            float lv[FS_U];
+#pragma unroll
+            for (int u = 0; u < FS_U; ++u) {
+                const int i = i0 + u * FS_THREADS + threadIdx.x;
+                lv[u] = i < V ? row[i] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < FS_U; ++u) {
+                const int i = i0 + u * FS_THREADS + threadIdx.x;
+                const float z = __fdiv_rn(lv[u], T);
+                const uint32_t k = fs_key(z);
+                const bool act = i < V && k >= kmin && (k & mask) == prefix;
+                fs_hist_add<true>(sh, act, (k >> shift) & 255, act ? fs_mass(z, zmax) : 0ull);
             }
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            int chosen = -1, last_nz = -1;
-            unsigned long long a = above;
-            for (int b = 255; b >= 0; --b) {
-                if (sh.hcnt[b] == 0) continue;
-                if (a + sh.hmass[b] > target) { chosen = b; break; }
-                a += sh.hmass[b];
-                last_nz = b;
-            }
-            if (chosen < 0) {            // cannot happen for target < total; keep the last candidate bin
-                chosen = last_nz;
-                a -= sh.hmass[last_nz < 0 ? 0 : last_nz];
-            }
-            sh.sel_bin = (unsigned)chosen;
-            sh.above = a;
-        }
+        fs_choose_bin<true>(sh, above, target, 0u);
         __syncthreads();
         prefix |= sh.sel_bin << shift;
         mask |= 255u << shift;
@@ -537,14 +607,13 @@ __device__ int fs_index_of(const float *row, int V, float T, uint32_t key, unsig
     const int C = (V + FS_THREADS - 1) / FS_THREADS, lo = threadIdx.x * C, hi = min(V, lo + C);
     unsigned int cnt = 0;
     for (int i = lo; i < hi; ++i) cnt += fs_key(__fdiv_rn(row[i], T)) == key;
-    sh.scan[threadIdx.x] = cnt;
+    // exclusive prefix of the counts over the threads, in thread order: wave scans, then the earlier waves' totals
+    const unsigned int incl = fs_wave_scan<unsigned int>(cnt);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 63) sh.scan[w] = incl;
     __syncthreads();
-    if (threadIdx.x == 0) {                 // exclusive prefix over the threads, in order
-        unsigned int s = 0;
-        for (int t = 0; t < FS_THREADS; ++t) { const unsigned int c = sh.scan[t]; sh.scan[t] = s; s += c; }
-    }
-    __syncthreads();
-    const unsigned long long before = sh.scan[threadIdx.x];
+    unsigned long long before = incl - cnt;
+    for (int j = 0; j < w; ++j) before += sh.scan[j];
     __shared__ int found;
     if (threadIdx.x == 0) found = -1;
     __syncthreads();
@@ -569,7 +638,16 @@ __global__ void __launch_bounds__(FS_THREADS) k_sample_filtered(const float *log
     const float *row = logits + (size_t)rows[s] * ld;
     // ---- maximum z (its key)
     uint32_t kmax = 0;
-    for (int i = threadIdx.x; i < V; i += FS_THREADS) kmax = max(kmax, fs_key(__fdiv_rn(row[i], T)));
+    for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {
+        float lv[FS_U];
+#pragma unroll
+        for (int u = 0; u < FS_U; ++u) {
+            const int i = i0 + u * FS_THREADS + threadIdx.x;
+            lv[u] = i < V ? row[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < FS_U; ++u) kmax = max(kmax, fs_key(__fdiv_rn(lv[u], T)));
+    }
     for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
     if ((threadIdx.x & 63) == 0) sh.redu[threadIdx.x >> 6] = kmax;
     __syncthreads();
@@ -584,21 +662,22 @@ __global__ void __launch_bounds__(FS_THREADS) k_sample_filtered(const float *log
         for (int shift = 24; shift >= 0; shift -= 8) {
             for (int b = threadIdx.x; b < 256; b += FS_THREADS) sh.hcnt[b] = 0;
             __syncthreads();
-            for (int i = threadIdx.x; i < V; i += FS_THREADS) {
-                const uint32_t k = fs_key(__fdiv_rn(row[i], T));
-                if ((k & mask) == prefix) atomicAdd(&sh.hcnt[(k >> shift) & 255], 1u);
+            for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {
+                float lv[FS_U];
+#pragma unroll
+                for (int u = 0; u < FS_U; ++u) {
+                    const int i = i0 + u * FS_THREADS + threadIdx.x;
+                    lv[u] = i < V ? row[i] : 0.f;
+                }
+#pragma unroll
+                for (int u = 0; u < FS_U; ++u) {
+                    const int i = i0 + u * FS_THREADS + threadIdx.x;
+                    const uint32_t k = fs_key(__fdiv_rn(lv[u], T));
+                    fs_hist_add<false>(sh, i < V && (k & mask) == prefix, (k >> shift) & 255, 0ull);
+                }
             }
             __syncthreads();
-            if (threadIdx.x == 0) {
-                unsigned int a = 0;
-                int b = 255;
-                for (; b > 0; --b) {
-                    if (a + sh.hcnt[b] >= rem) break;
-                    a += sh.hcnt[b];
-                }
-                sh.sel_bin = (unsigned)b;
-                sh.redu[0] = rem - a;
-            }
+            fs_choose_bin<false>(sh, 0ull, 0ull, rem);
             __syncthreads();
             prefix |= sh.sel_bin << shift;
             mask |= 255u << shift;
@@ -609,9 +688,18 @@ __global__ void __launch_bounds__(FS_THREADS) k_sample_filtered(const float *log
     }
     // ---- total candidate mass
     unsigned long long F = 0;
-    for (int i = threadIdx.x; i < V; i += FS_THREADS) {
-        const float z = __fdiv_rn(row[i], T);
-        if (fs_key(z) >= kmin) F += fs_mass(z, zmax);
+    for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {
+        float lv[FS_U];
+#pragma unroll
+        for (int u = 0; u < FS_U; ++u) {
+            const int i = i0 + u * FS_THREADS + threadIdx.x;
+            lv[u] = i < V ? row[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < FS_U; ++u) {
+            const float z = __fdiv_rn(lv[u], T);
+            if (fs_key(z) >= kmin) F += fs_mass(z, zmax);
+        }
     }
     F = fs_block_sum(F, sh);
     // ---- top-p: kept mass K = inclusive mass of the first token whose inclusive mass exceeds floor(p * F)
