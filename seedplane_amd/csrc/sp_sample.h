@@ -464,6 +464,8 @@ __device__ __forceinline__ unsigned long long fs_mass(float z, float zmax) {
 struct FsShared {
     unsigned long long hmass[256];
     unsigned int hcnt[256];
+    unsigned long long h1mass[256];     // first-level (top 8 key bits) histogram of the candidates, built once
+    unsigned int h1cnt[256];
     unsigned long long red64[FS_THREADS / 64];
     unsigned int redu[FS_THREADS / 64];
     unsigned int sel_bin;
@@ -570,9 +572,12 @@ __device__ uint32_t fs_select_mass(const float *row, int V, float T, float zmax,
     uint32_t prefix = 0, mask = 0;
     unsigned long long above = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int b = threadIdx.x; b < 256; b += FS_THREADS) { sh.hmass[b] = 0; sh.hcnt[b] = 0; }
+        for (int b = threadIdx.x; b < 256; b += FS_THREADS) {
+            sh.hmass[b] = shift == 24 ? sh.h1mass[b] : 0ull;
+            sh.hcnt[b] = shift == 24 ? sh.h1cnt[b] : 0u;
+        }
         __syncthreads();
-        for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {    // block-uniform trip count: whole waves vote
+        for (int i0 = 0; shift < 24 && i0 < V; i0 += FS_THREADS * FS_U) {   // block-uniform: whole waves vote
             float lv[FS_U];
 #pragma unroll
             for (int u = 0; u < FS_U; ++u) {
@@ -686,20 +691,31 @@ __global__ void __launch_bounds__(FS_THREADS) k_sample_filtered(const float *log
         }
         kmin = prefix;
     }
-    // ---- total candidate mass
-    unsigned long long F = 0;
+    // ---- first-level histogram of the candidates (count and mass per top key byte); F = the total mass
+    for (int b = threadIdx.x; b < 256; b += FS_THREADS) { sh.hmass[b] = 0; sh.hcnt[b] = 0; }
+    __syncthreads();
     for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {
         float lv[FS_U];
 #pragma unroll
         for (int u = 0; u < FS_U; ++u) {
             const int i = i0 + u * FS_THREADS + threadIdx.x;
-            lv[u] = i < V ? row[i] : -INFINITY;
+            lv[u] = i < V ? row[i] : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < FS_U; ++u) {
+            const int i = i0 + u * FS_THREADS + threadIdx.x;
             const float z = __fdiv_rn(lv[u], T);
-            if (fs_key(z) >= kmin) F += fs_mass(z, zmax);
+            const uint32_t k = fs_key(z);
+            const bool act = i < V && k >= kmin;
+            fs_hist_add<true>(sh, act, k >> 24, act ? fs_mass(z, zmax) : 0ull);
         }
+    }
+    __syncthreads();
+    unsigned long long F = 0;
+    for (int b = threadIdx.x; b < 256; b += FS_THREADS) {
+        sh.h1mass[b] = sh.hmass[b];
+        sh.h1cnt[b] = sh.hcnt[b];
+        F += sh.hmass[b];
     }
     F = fs_block_sum(F, sh);
     // ---- top-p: kept mass K = inclusive mass of the first token whose inclusive mass exceeds floor(p * F)
