@@ -464,6 +464,7 @@ __device__ __forceinline__ unsigned long long fs_mass(float z, float zmax) {
 struct FsShared {
     unsigned long long hmass[256];
     unsigned int hcnt[256];
+    unsigned int hidx[256];             // last level: the smallest index in each bin
     unsigned long long h1mass[256];     // first-level (top 8 key bits) histogram of the candidates, built once
     unsigned int h1cnt[256];
     unsigned long long red64[FS_THREADS / 64];
@@ -568,13 +569,14 @@ __device__ __forceinline__ unsigned long long fs_block_sum(unsigned long long v,
 // *rank_out = the token's rank inside its tie group (index order).  The caller guarantees target < total mass.
 __device__ uint32_t fs_select_mass(const float *row, int V, float T, float zmax, uint32_t kmin,
                                    unsigned long long target, FsShared &sh, unsigned long long *above_out,
-                                   unsigned long long *rank_out) {
+                                   unsigned long long *rank_out, int *first_out = nullptr) {
     uint32_t prefix = 0, mask = 0;
     unsigned long long above = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (int b = threadIdx.x; b < 256; b += FS_THREADS) {
             sh.hmass[b] = shift == 24 ? sh.h1mass[b] : 0ull;
             sh.hcnt[b] = shift == 24 ? sh.h1cnt[b] : 0u;
+            sh.hidx[b] = 0xffffffffu;
         }
         __syncthreads();
         for (int i0 = 0; shift < 24 && i0 < V; i0 += FS_THREADS * FS_U) {   // block-uniform: whole waves vote
@@ -591,6 +593,7 @@ __device__ uint32_t fs_select_mass(const float *row, int V, float T, float zmax,
                 const uint32_t k = fs_key(z);
                 const bool act = i < V && k >= kmin && (k & mask) == prefix;
                 fs_hist_add<true>(sh, act, (k >> shift) & 255, act ? fs_mass(z, zmax) : 0ull);
+                if (shift == 0 && act) atomicMin(&sh.hidx[k & 255], (unsigned)i);
             }
         }
         __syncthreads();
@@ -602,6 +605,7 @@ __device__ uint32_t fs_select_mass(const float *row, int V, float T, float zmax,
         __syncthreads();
     }
     const unsigned long long m = fs_mass(fs_unkey(prefix), zmax);
+    if (first_out) *first_out = (int)sh.hidx[prefix & 255];    // the tie group's smallest index
     *above_out = above;
     *rank_out = m > 0 ? (target - above) / m : 0;
     return prefix;
@@ -732,7 +736,9 @@ __global__ void __launch_bounds__(FS_THREADS) k_sample_filtered(const float *log
     unsigned long long tgt = (unsigned long long)(u[s] * (double)K);
     if (tgt >= K) tgt = K - 1;
     unsigned long long above, rank;
-    const uint32_t key = fs_select_mass(row, V, T, zmax, kmin, tgt, sh, &above, &rank);
-    const int tok = fs_index_of(row, V, T, key, rank, sh);
+    int first = -1;
+    const uint32_t key = fs_select_mass(row, V, T, zmax, kmin, tgt, sh, &above, &rank, &first);
+    // rank 0 (always, unless the drawn z value is shared by several tokens) is the group's smallest index
+    const int tok = rank == 0 ? first : fs_index_of(row, V, T, key, rank, sh);
     if (threadIdx.x == 0) out[s] = tok;
 }
