@@ -122,6 +122,14 @@ int sp_engine_load(sp_engine *e, int32_t kind, int32_t layer, int32_t fmt, int32
  * every layer (layout [layer][seq][kv_head][slot][head_dim]).  Re-reserving frees the previous cache. */
 int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots);
 
+/* Replaces the independence of the reference's per-cache tensors (Qwen2Engine.new_cache allocates a fresh KVCache
+ * per call and never touches the others, qwen_engine.py:82-85): grows the pool to n_seq x n_slots (neither smaller
+ * than now) while keeping the live sequences.  For kept sequence keep_seq[i] of length keep_len[i], positions
+ * [max(0, len - old n_slots), len) move from slot p mod old n_slots to slot p mod n_slots, in every layer; other
+ * sequences start empty.  On failure the old pool is untouched.  Synchronous. */
+int sp_engine_kv_grow(sp_engine *e, int32_t n_seq, int32_t n_slots, int32_t n_keep, const int32_t *keep_seq,
+                      const int32_t *keep_len);
+
 /* Replaces Qwen2Engine.forward (qwen_engine.py:105-144) and the recorded one-token / K/V-batch command buffers
  * (qwen_vk.cpp:374-437).  Runs `n` columns (any mix of sequences) through every layer.  Without SP_F_LOGITS the
  * call is K/V-only: the last layer stops after writing its K/V (qwen_vk.cpp:426).  logits_dev, when not NULL,

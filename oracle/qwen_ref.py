@@ -6,7 +6,15 @@ needs to be checked against:
     reference's `arange(start+q) <= slots` mask (qwen_engine.py:131-135) in `forward`;
   * an optional sliding window: query at cache position p sees positions (p - W, p] (the Hugging Face rule,
     transformers masking_utils sliding_window_overlay: kv_idx > q_idx - sliding_window);
-  * weights of any synthetic recipe, dequantized to fp32 once at load (oracle/quant_ref.py).
+  * weights of any synthetic recipe, dequantized to fp32 once at load (oracle/quant_ref.py);
+  * a storage precision (`storage`):
+      None   -- fp32 everywhere: the reference at dtype=float32, its CPU default (qwen_engine.py:39-41);
+      'fp16' -- the reference at dtype=float16, its GPU default (qwen_engine.py:39-41): weights, residual stream,
+                projections, RoPE cos/sin, K/V cache and attention output are fp16 tensors, the norms compute in fp32
+                and cast their output (qwen_engine.py:90-92), logits are cast to fp32 (:143).  Emulated as fp32
+                arithmetic rounded to fp16 after every reference op (what fp16 GEMMs with fp32 accumulation give);
+      'hip'  -- fp16 where the HIP engine stores fp16 (normalised GEMV inputs, K/V cache, attention output, SwiGLU
+                activation), fp32 elsewhere (residual stream, projection outputs, RoPE, logits).
 The cache here is never a ring: it holds every position, and the window is applied through the mask.
 """
 import math
@@ -29,8 +37,11 @@ class RefCache:
 
 
 class RefQwen2:
-    def __init__(self, cfg, tensors):
+    def __init__(self, cfg, tensors, storage=None):
         """qwen_engine.py:35-80: config fields, inv_freq, fused qkv / gate_up packing, fp32 norms."""
+        if storage not in (None, 'fp16', 'hip'):
+            raise ValueError(f'unknown storage {storage!r}')
+        self.storage = storage
         self.cfg = cfg
         self.n_layers = cfg['num_hidden_layers']
         self.n_heads = cfg['num_attention_heads']
@@ -41,6 +52,8 @@ class RefQwen2:
         self.inv_freq = 1.0 / (theta ** (torch.arange(0, self.head_dim, 2).float() / self.head_dim))
         self.eps = cfg.get('rms_norm_eps', 1e-6)
         w = dequant_all(cfg, tensors)
+        if storage == 'fp16':          # the reference casts every loaded tensor to dtype (qwen_engine.py:59)
+            w = {k: v.half().float() for k, v in w.items()}
         self.embed = w['model.embed_tokens.weight']
         self.head = w.get('lm_head.weight', self.embed)
         self.final_norm = w['model.norm.weight'].float()
@@ -62,11 +75,15 @@ class RefQwen2:
     def new_cache(self, capacity):
         return RefCache(self.n_layers, capacity, self.n_kv_heads, self.head_dim)
 
+    def _r(self, t, *kinds):
+        """Round `t` to fp16 when the storage mode stores this tensor kind in fp16."""
+        return t.half().float() if self.storage in kinds else t
+
     def _norm(self, x, weight):
         """qwen_engine.py:90-92: fp32 x * rsqrt(mean(x^2) + eps), times the weight before the cast."""
         xf = x.float()
         z = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return z * weight
+        return self._r(z * weight, 'fp16', 'hip')
 
     @staticmethod
     def _rotate_half(x):
@@ -78,8 +95,9 @@ class RefQwen2:
         """qwen_engine.py:99-103: phase = outer(float(pos), inv_freq), duplicated over both halves."""
         phase = torch.outer(positions.float(), self.inv_freq)
         phase = torch.cat((phase, phase), dim=-1)[None, :, None, :]
-        cos, sin = phase.cos(), phase.sin()
-        return q * cos + self._rotate_half(q) * sin, k * cos + self._rotate_half(k) * sin
+        cos, sin = self._r(phase.cos(), 'fp16'), self._r(phase.sin(), 'fp16')
+        r = lambda t: self._r(t, 'fp16')
+        return (r(r(q * cos) + r(self._rotate_half(q) * sin)), r(r(k * cos) + r(self._rotate_half(k) * sin)))
 
     @torch.inference_mode()
     def forward_masked(self, ids, cache, positions, allowed, all_logits=True):
@@ -91,30 +109,32 @@ class RefQwen2:
             raise ValueError(f'KV cache capacity {cache.capacity} exceeded')
         positions = torch.as_tensor(positions, dtype=torch.long).flatten()
         H, NH, NKV, HD = self.hidden, self.n_heads, self.n_kv_heads, self.head_dim
+        r16 = lambda t: self._r(t, 'fp16')          # the reference's fp16 tensors
         x = F.embedding(ids, self.embed)[None]
         for l, ly in enumerate(self.layers):
             residual = x
             h = self._norm(x, ly['in_norm'])
-            qkv = F.linear(h, ly['qkv_w'], ly['qkv_b'])
+            qkv = r16(F.linear(h, ly['qkv_w'], ly['qkv_b']))
             q, k, v = qkv.split((H, NKV * HD, NKV * HD), dim=-1)
             q = q.view(1, qlen, NH, HD)
             k = k.view(1, qlen, NKV, HD)
             v = v.view(1, qlen, NKV, HD)
             q, k = self._rope(q, k, positions)
-            cache.keys[l][:, start:start + qlen].copy_(k)
-            cache.values[l][:, start:start + qlen].copy_(v)
+            cache.keys[l][:, start:start + qlen].copy_(self._r(k, 'hip'))
+            cache.values[l][:, start:start + qlen].copy_(self._r(v, 'hip'))
             kk = cache.keys[l][:, :start + qlen].repeat_interleave(NH // NKV, dim=2)
             vv = cache.values[l][:, :start + qlen].repeat_interleave(NH // NKV, dim=2)
             qt, kt, vt = (z.transpose(1, 2) for z in (q, kk, vv))
-            attn = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=allowed)
-            x = residual + F.linear(attn.transpose(1, 2).reshape(1, qlen, H), ly['o_w'])
+            attn = self._r(F.scaled_dot_product_attention(qt, kt, vt, attn_mask=allowed), 'fp16', 'hip')
+            x = r16(residual + r16(F.linear(attn.transpose(1, 2).reshape(1, qlen, H), ly['o_w'])))
             residual = x
             h = self._norm(x, ly['post_norm'])
-            gate, up = F.linear(h, ly['gate_up_w']).chunk(2, dim=-1)
-            x = residual + F.linear(F.silu(gate) * up, ly['down_w'])
+            gate, up = r16(F.linear(h, ly['gate_up_w'])).chunk(2, dim=-1)
+            act = self._r(r16(r16(F.silu(gate)) * up), 'hip')
+            x = r16(residual + r16(F.linear(act, ly['down_w'])))
         cache.length += qlen
         x = self._norm(x, self.final_norm)
-        logits = F.linear(x if all_logits else x[:, -1:], self.head).float()[0]
+        logits = r16(F.linear(x if all_logits else x[:, -1:], self.head)).float()[0]
         return logits
 
     def forward(self, input_ids, cache, all_logits=False, positions=None, window=None):

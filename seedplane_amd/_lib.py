@@ -49,6 +49,7 @@ SIGNATURES = {
     'sp_engine_set_stream': (c_int, [c_void_p, c_void_p]),
     'sp_engine_load': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     'sp_engine_kv_reserve': (c_int, [c_void_p, c_int32, c_int32]),
+    'sp_engine_kv_grow': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     'sp_engine_forward': (c_int, [c_void_p, c_int32, ctypes.POINTER(Token), c_int32, c_void_p, c_void_p]),
     'sp_engine_logits': (c_int, [c_void_p, ctypes.POINTER(c_void_p)]),
     'sp_engine_kv_move': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),

@@ -636,6 +636,23 @@ __global__ void __launch_bounds__(128) k_kv_move(f16 *const *kl, f16 *const *vl,
     }
 }
 
+// Growth of the KV pool with live sequences kept: for kept sequence i (keep[3i] = sequence, keep[3i+1] = first position,
+// keep[3i+2] = position count) every position p moves from slot p mod old_slots of the old pool to slot p mod new_slots
+// of the new one, for one layer's K and V.  Sixteen bytes per thread; blockIdx.y = kept index * NKV + kv head.
+__global__ void __launch_bounds__(256) k_kv_regrid(const f16 *ko, const f16 *vo, f16 *kn, f16 *vn, const int *keep,
+                                                   int NKV, int HD, int old_slots, int new_slots) {
+    const int ki = blockIdx.y / NKV, kvh = blockIdx.y % NKV;
+    const int seq = keep[3 * ki], p0 = keep[3 * ki + 1], np = keep[3 * ki + 2];
+    const int per_pos = HD / 8;
+    const size_t ob = ((size_t)seq * NKV + kvh) * old_slots, nb = ((size_t)seq * NKV + kvh) * new_slots;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < np * per_pos; i += gridDim.x * blockDim.x) {
+        const int p = p0 + i / per_pos, c = (i % per_pos) * 8;
+        const size_t so = (ob + p % old_slots) * HD + c, dO = (nb + p % new_slots) * HD + c;
+        *(uint4 *)(kn + dO) = *(const uint4 *)(ko + so);
+        *(uint4 *)(vn + dO) = *(const uint4 *)(vo + so);
+    }
+}
+
 // Seeded fill of K/V slots (benchmark stand-in for a long prefill): value = scale * (2 * hash01 - 1).
 __global__ void __launch_bounds__(256) k_kv_fill(f16 *const *kl, f16 *const *vl, int seq, int NKV, int n_slots, int HD,
                                                  int first, int n, uint64_t seed, float scale) {

@@ -996,35 +996,121 @@ int sp_engine_load(sp_engine *e, int32_t kind, int32_t layer, int32_t fmt, int32
     });
 }
 
+namespace {
+// A zeroed K/V pool for n_seq x n_slots in every layer (nothing of the engine's state changes; on failure the new
+// allocations are released and the exception propagates).
+void alloc_pool(const sp_engine *e, int n_seq, int n_slots, std::vector<f16 *> &k, std::vector<f16 *> &v, uint64_t &bytes) {
+    k.assign(e->d.n_layers, nullptr);
+    v.assign(e->d.n_layers, nullptr);
+    bytes = 0;
+    const size_t per = (size_t)n_seq * e->d.n_kv_heads * n_slots * e->d.head_dim;
+    try {
+        for (int l = 0; l < e->d.n_layers; ++l) {
+            k[l] = dev_alloc<f16>(per, &bytes);
+            v[l] = dev_alloc<f16>(per, &bytes);
+            HIPCHK(hipMemsetAsync(k[l], 0, per * sizeof(f16), e->stream));
+            HIPCHK(hipMemsetAsync(v[l], 0, per * sizeof(f16), e->stream));
+        }
+    } catch (...) {
+        for (auto p : k) dev_free(p);
+        for (auto p : v) dev_free(p);
+        k.clear(); v.clear();
+        throw;
+    }
+}
+
+// Makes (k, v) the engine's pool: frees the old one, sizes the attention partials for n_slots and drops the recorded
+// graphs and persistent tables (they hold the old addresses).  The stream must be idle.
+void install_pool(sp_engine *e, int n_seq, int n_slots, std::vector<f16 *> &k, std::vector<f16 *> &v, uint64_t bytes) {
+    for (auto p : e->kc) dev_free(p);
+    for (auto p : e->vc) dev_free(p);
+    e->kc.swap(k);
+    e->vc.swap(v);
+    k.clear(); v.clear();
+    e->kv_bytes = bytes;
+    dev_free(e->attn_part); e->attn_part = nullptr;
+    e->n_seq = 0; e->n_slots = 0;
+    if (!e->d_kl) e->d_kl = dev_alloc<f16 *>(e->d.n_layers);
+    if (!e->d_vl) e->d_vl = dev_alloc<f16 *>(e->d.n_layers);
+    HIPCHK(hipMemcpy(e->d_kl, e->kc.data(), e->d.n_layers * sizeof(f16 *), hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(e->d_vl, e->vc.data(), e->d.n_layers * sizeof(f16 *), hipMemcpyHostToDevice));
+    e->max_nchunk = (n_slots + 64 + ATT_CH - 1) / ATT_CH;
+    e->attn_part = dev_alloc<float>((size_t)e->maxT * e->d.n_heads * e->max_nchunk * part_floats(e->d.head_dim));
+    e->n_seq = n_seq; e->n_slots = n_slots;
+    for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
+    e->graphs.clear();
+    e->pk.tried = false;
+}
+}  // namespace
+
 int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots) {
     if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
     return guarded(e, [&] {
         require(n_seq >= 1 && n_slots >= 1, SP_EINVAL, "n_seq and n_slots must be positive");
         require((n_slots + 64 + ATT_CH - 1) / ATT_CH <= ATT_MAX_CHUNKS, SP_EINVAL, "n_slots too large for the attention combine");
         HIPCHK(hipStreamSynchronize(e->stream));
+        // the old pool goes first, so a re-reservation never needs both at once
         for (auto p : e->kc) dev_free(p);
         for (auto p : e->vc) dev_free(p);
-        e->kc.assign(e->d.n_layers, nullptr);
-        e->vc.assign(e->d.n_layers, nullptr);
+        e->kc.clear(); e->vc.clear();
         e->kv_bytes = 0;
         e->n_seq = 0; e->n_slots = 0;
-        dev_free(e->attn_part); e->attn_part = nullptr;
-        const size_t per = (size_t)n_seq * e->d.n_kv_heads * n_slots * e->d.head_dim;
-        for (int l = 0; l < e->d.n_layers; ++l) {
-            e->kc[l] = dev_alloc<f16>(per, &e->kv_bytes);
-            e->vc[l] = dev_alloc<f16>(per, &e->kv_bytes);
-            HIPCHK(hipMemset(e->kc[l], 0, per * sizeof(f16)));
-            HIPCHK(hipMemset(e->vc[l], 0, per * sizeof(f16)));
+        std::vector<f16 *> k, v;
+        uint64_t bytes = 0;
+        alloc_pool(e, n_seq, n_slots, k, v, bytes);
+        install_pool(e, n_seq, n_slots, k, v, bytes);
+        HIPCHK(hipStreamSynchronize(e->stream));
+    });
+}
+
+int sp_engine_kv_grow(sp_engine *e, int32_t n_seq, int32_t n_slots, int32_t n_keep, const int32_t *keep_seq,
+                      const int32_t *keep_len) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        require(e->n_seq > 0, SP_ESTATE, "KV cache not reserved");
+        require(n_seq >= e->n_seq && n_slots >= e->n_slots, SP_EINVAL, "a grown pool must not be smaller in either dimension");
+        require((n_slots + 64 + ATT_CH - 1) / ATT_CH <= ATT_MAX_CHUNKS, SP_EINVAL, "n_slots too large for the attention combine");
+        require(n_keep >= 0 && n_keep <= e->n_seq, SP_EINVAL, "n_keep must be in [0, n_seq of the current pool]");
+        require(n_keep == 0 || (keep_seq && keep_len), SP_EINVAL, "keep arrays are NULL");
+        std::vector<int> keep(3 * (size_t)std::max(n_keep, 1));
+        std::vector<char> seen(e->n_seq, 0);
+        int most = 0;
+        for (int i = 0; i < n_keep; ++i) {
+            require(keep_seq[i] >= 0 && keep_seq[i] < e->n_seq && !seen[keep_seq[i]], SP_EINVAL,
+                    "kept sequences must be distinct indices of the current pool");
+            require(keep_len[i] >= 0, SP_EINVAL, "kept lengths must be non-negative");
+            seen[keep_seq[i]] = 1;
+            const int np = std::min(keep_len[i], e->n_slots);     // the ring holds the last n_slots positions
+            keep[3 * i] = keep_seq[i];
+            keep[3 * i + 1] = keep_len[i] - np;
+            keep[3 * i + 2] = np;
+            most = std::max(most, np);
         }
-        if (!e->d_kl) e->d_kl = dev_alloc<f16 *>(e->d.n_layers);
-        if (!e->d_vl) e->d_vl = dev_alloc<f16 *>(e->d.n_layers);
-        HIPCHK(hipMemcpy(e->d_kl, e->kc.data(), e->d.n_layers * sizeof(f16 *), hipMemcpyHostToDevice));
-        HIPCHK(hipMemcpy(e->d_vl, e->vc.data(), e->d.n_layers * sizeof(f16 *), hipMemcpyHostToDevice));
-        e->n_seq = n_seq; e->n_slots = n_slots;
-        e->max_nchunk = (n_slots + 64 + ATT_CH - 1) / ATT_CH;
-        e->attn_part = dev_alloc<float>((size_t)e->maxT * e->d.n_heads * e->max_nchunk * part_floats(e->d.head_dim));
-        for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
-        e->graphs.clear();
+        HIPCHK(hipStreamSynchronize(e->stream));
+        std::vector<f16 *> k, v;
+        uint64_t bytes = 0;
+        alloc_pool(e, n_seq, n_slots, k, v, bytes);
+        int *dkeep = nullptr;
+        try {
+            if (n_keep > 0 && most > 0) {
+                dkeep = dev_alloc<int>(keep.size());
+                HIPCHK(hipMemcpyAsync(dkeep, keep.data(), keep.size() * sizeof(int), hipMemcpyHostToDevice, e->stream));
+                const int per = most * (e->d.head_dim / 8);
+                const dim3 grid((per + 255) / 256 < 512 ? (per + 255) / 256 : 512, n_keep * e->d.n_kv_heads);
+                for (int l = 0; l < e->d.n_layers; ++l)
+                    hipLaunchKernelGGL(k_kv_regrid, grid, dim3(256), 0, e->stream, e->kc[l], e->vc[l], k[l], v[l], dkeep,
+                                       e->d.n_kv_heads, e->d.head_dim, e->n_slots, n_slots);
+                HIPCHK(hipGetLastError());
+            }
+            HIPCHK(hipStreamSynchronize(e->stream));
+        } catch (...) {
+            dev_free(dkeep);
+            for (auto p : k) dev_free(p);
+            for (auto p : v) dev_free(p);
+            throw;
+        }
+        dev_free(dkeep);
+        install_pool(e, n_seq, n_slots, k, v, bytes);
     });
 }
 

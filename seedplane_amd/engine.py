@@ -74,10 +74,10 @@ class ShardedSession:
         self.capacity = plan.sinks + plan.halo + plan.shard
         if self.capacity > engine.config['max_position_embeddings']:
             raise ValueError(f'sinks + halo + shard = {self.capacity} exceeds the model\'s positions')
-        # two window caches live at once (the current one and the next); growing the pool later would invalidate
-        # them, so it is sized here (which, like any reservation, invalidates caches made before the session)
+        # two window caches live at once (the current one and the next); the pool is grown for them here (growth
+        # keeps every live cache of the engine)
         if engine._pool_slots < self.capacity or len(engine._free) < 2:
-            engine.reserve(max(engine._pool_n, 2), max(engine._pool_slots, self.capacity))
+            engine.grow(engine._pool_n + max(0, 2 - len(engine._free)), self.capacity)
         self.seq = []                 # every token processed so far (index = original position)
         self.cur = engine.new_cache(self.capacity)
         self.shadow = None            # the next window's cache while the halo of the next shard is decoded

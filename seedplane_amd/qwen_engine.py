@@ -130,6 +130,7 @@ class Qwen2Engine:
         self._pool_slots = 0
         self._epoch = 0
         self._free = []
+        self._live = weakref.WeakValueDictionary()     # sequence index -> its live cache
         self._logits_buf = None
 
     # ------------------------------------------------------------------------------------------ loading
@@ -224,20 +225,43 @@ class Qwen2Engine:
         self._pool_n, self._pool_slots = int(n_seq), int(n_slots)
         self._epoch += 1
         self._free = list(range(self._pool_n))[::-1]
+        self._live = weakref.WeakValueDictionary()
+
+    def grow(self, n_seq, n_slots):
+        """Grow the HBM KV pool to at least n_seq sequences x n_slots slots, keeping every live cache: its K/V moves
+        to the new pool (ring slot p mod n_slots) and it stays usable, as the reference's caches are independent of
+        each other (qwen_engine.py:82-85)."""
+        n_seq, n_slots = max(int(n_seq), self._pool_n), max(int(n_slots), self._pool_slots)
+        if self._pool_n == 0:
+            self.reserve(n_seq, n_slots)
+            return
+        if n_seq == self._pool_n and n_slots == self._pool_slots:
+            return
+        live = [(s, c) for s, c in list(self._live.items()) if c.epoch == self._epoch]
+        seqs = np.array([s for s, _ in live], dtype=np.int32)
+        lens = np.array([c.length for _, c in live], dtype=np.int32)
+        _lib.check(self.lib.sp_engine_kv_grow(self.h, n_seq, n_slots, len(live), _ptr(seqs), _ptr(lens)), self.h)
+        self._free = list(range(n_seq - 1, self._pool_n - 1, -1)) + self._free
+        self._pool_n, self._pool_slots = n_seq, n_slots
 
     def slots_for(self, capacity, window=None):
         return capacity if window is None else int(window) + self.max_tokens
 
     def new_cache(self, capacity=4096, window=None):
+        """A fresh, empty cache (reference: qwen_engine.py:82-85).  When the pool lacks a free sequence or enough
+        slots it grows, keeping every live cache."""
         capacity = min(capacity, self.config['max_position_embeddings'])
         if capacity < 1:
             raise ValueError('cache capacity must be positive')
         if window is not None and window < 1:
             raise ValueError('window must be positive')
         need = self.slots_for(capacity, window)
-        if need > self._pool_slots or not self._free:
-            self.reserve(max(self._pool_n, 1) if self._free else self._pool_n + 1, max(need, self._pool_slots))
+        if self._pool_n == 0:
+            self.reserve(1, need)
+        elif need > self._pool_slots or not self._free:
+            self.grow(self._pool_n if self._free else 2 * self._pool_n, need)
         cache = KVCache([], [], 0, capacity, window, self._free.pop(), self._epoch)
+        self._live[cache.seq] = cache
         weakref.finalize(cache, self._release, cache.seq, cache.epoch)
         return cache
 
@@ -446,9 +470,23 @@ class Qwen2Engine:
             raise ValueError('temperature must be positive (T <= 0 is the greedy argmax)')
         if logits.dim() != 2 or logits.dtype != torch.float32 or logits.device.type != 'cuda':
             raise ValueError('logits must be a 2-D fp32 GPU tensor')
+        if logits.stride(1) != 1:
+            raise ValueError('logits rows must be contiguous (stride 1 along the vocabulary)')
+        u = np.asarray(u, dtype=np.float64).ravel()
+        if rows_dev is None:
+            # the kernel reads row rows[s] for every draw s: check every index before the launch
+            rows = [int(r) for r in rows]
+            if len(rows) != len(u):
+                raise ValueError('rows and u must have the same length')
+            if any(r < 0 or r >= logits.shape[0] for r in rows):
+                raise ValueError('a row index is outside the logits')
+        elif (rows_dev.dtype != torch.int32 or rows_dev.device != logits.device or rows_dev.dim() != 1
+              or rows_dev.numel() != len(u)):
+            # a device row list is the caller's to keep in range (it is not read back to the host)
+            raise ValueError('rows_dev must be a 1-D int32 tensor on the logits device with one entry per draw')
         dev = logits.device
-        r = rows_dev if rows_dev is not None else torch.tensor(list(rows), dtype=torch.int32, device=dev)
-        ud = torch.as_tensor(np.asarray(u, dtype=np.float64)).to(dev, non_blocking=False)
+        r = rows_dev if rows_dev is not None else torch.tensor(rows, dtype=torch.int32, device=dev)
+        ud = torch.as_tensor(u).to(dev, non_blocking=False)
         out = torch.empty(len(ud), dtype=torch.int32, device=dev)
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         _lib.check(self.lib.sp_op_sample_filtered(ctypes.c_void_p(logits.data_ptr()), logits.shape[1],
@@ -496,8 +534,10 @@ class Qwen2Engine:
     def generate_batch(self, prompts, max_new_tokens=32, eos_token_id=None, window=None, graph=True):
         """Greedy decode of independent requests as one batch (ragged prompt lengths).  Returns token lists."""
         need = max(self.slots_for(len(p) + max_new_tokens, window) for p in prompts)
-        if len(self._free) < len(prompts) or need > self._pool_slots:
-            self.reserve(max(len(prompts), self._pool_n), max(need, self._pool_slots))
+        if self._pool_n == 0:
+            self.reserve(len(prompts), need)
+        elif len(self._free) < len(prompts) or need > self._pool_slots:
+            self.grow(self._pool_n + max(0, len(prompts) - len(self._free)), need)
         caches = [self.new_cache(len(p) + max_new_tokens, window=window) for p in prompts]
         tok = self.prefill(prompts, caches)
         out = [[int(t)] for t in tok]

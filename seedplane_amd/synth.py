@@ -95,8 +95,9 @@ def norm_names(cfg):
     return names
 
 
-def make_weights(cfg, recipe, seed=0, threads=16):
-    """Return (config, tensors) for `recipe` in {'f32', 'f16', 'q8', 'q4'}; tensors are CPU torch tensors."""
+def make_weights(cfg, recipe, seed=0, threads=16, scale_std=0.002):
+    """Return (config, tensors) for `recipe` in {'f32', 'f16', 'q8', 'q4'}; tensors are CPU torch tensors.
+    `scale_std`: the standard deviation of the |N(0, s)| block scales of 'q8' / 'q4' (0.002 in the recipes above)."""
     cfg = dict(cfg)
     f = _Filler(seed, threads)
     w = {}
@@ -113,11 +114,11 @@ def make_weights(cfg, recipe, seed=0, threads=16):
             w[name + '.weight'] = f.normal((n, k), 0.02, torch.float16)
         elif recipe == 'q8':
             w[name + '.qweight'] = f.randint((n, k), -127, 128, torch.int8)
-            w[name + '.scales'] = f.abs_normal((n, k // GROUP), 0.002, torch.float16)
+            w[name + '.scales'] = f.abs_normal((n, k // GROUP), scale_std, torch.float16)
         elif recipe == 'q4':
             packed = f.randint((n, k // 2), 0, 256, torch.uint8)   # two uniform nibbles per byte
             w[name + '.qweight'] = packed
-            w[name + '.scales'] = f.abs_normal((n, k // GROUP), 0.002, torch.float16)
+            w[name + '.scales'] = f.abs_normal((n, k // GROUP), scale_std, torch.float16)
             w[name + '.qzeros'] = f.uniform((n, k // GROUP), 7.0, 8.0, torch.float16)
         else:
             raise ValueError(f'unknown recipe {recipe}')

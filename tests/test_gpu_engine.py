@@ -128,3 +128,31 @@ def test_graph_replay_matches_eager(small):
         graphed = eng.generate_batch(prompts, max_new_tokens=8, graph=True)
         assert graphed == eager
         assert eng.generate_batch(prompts, max_new_tokens=3, graph=False) == [e[:3] for e in eager]
+
+
+def test_new_cache_growth_keeps_live_caches(small):
+    # the reference's caches are independent tensors (qwen_engine.py:82-85): making more caches, with more slots,
+    # must not disturb one that is in use
+    fmt, cfg, eng, ref = small
+    print(f'cache growth {fmt}', flush=True)
+    ids = random_prompt(40, cfg['vocab_size'], seed=31)
+    a = eng.new_cache(48)
+    w = eng.new_cache(4096, window=8)
+    eng.forward(ids[:20], a)
+    eng.forward(ids[:20], w)
+    n0, s0 = eng._pool_n, eng._pool_slots
+    more = []
+    while eng._pool_n == n0:                                  # more sequences than the pool holds: it grows...
+        more.append(eng.new_cache(16))
+    more.append(eng.new_cache(s0 + 200))                      # ... and then in slots (every ring slot moves)
+    assert eng._pool_slots > s0
+    assert a.epoch == eng._epoch and w.epoch == eng._epoch
+    lg, _ = eng.forward(ids[20:], a, all_logits=True)
+    lw, _ = eng.forward(ids[20:], w, all_logits=True)
+    rl = ref.forward(ids, ref.new_cache(40), all_logits=True)[20:]
+    rw = ref.forward(ids, ref.new_cache(40), all_logits=True, window=8)[20:]
+    assert max_rel(lg, rl) < TOL
+    assert max_rel(lw, rw) < TOL
+    for c in more:                                            # the new caches work too
+        out, _ = eng.forward(ids[:3], c)
+        assert torch.isfinite(out).all()

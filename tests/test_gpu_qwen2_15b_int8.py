@@ -1,0 +1,171 @@
+"""Oracle parity of the HIP engine at the full Qwen2-1.5B shape (28 layers, hidden 1536, 12 / 2 heads, head_dim 128,
+GQA group 6, SwiGLU 8960, tied 151936-row head) with int8 block-32 weights (codes U[-127, 127], fp16 block scales):
+  * batch 1 over a 1024-position sliding window, the context past the window and past the 1088-slot ring: decode logits
+    of every step and the greedy ids vs the oracle (reference qwen_engine.py:105-166; window rule of transformers'
+    sliding window);
+  * 16 sequences of 1030-1165 positions decoded as one batch, each against its own oracle run;
+  * the 1 + 8 x 4 draft tree over a 2048-position prefix with a Qwen2-0.5B fp16 drafter: tree-masked logits vs the
+    oracle's forward_masked with the ancestor mask, greedy ids per node, then the acceptance walk on those logits vs
+    the oracle walk (bit-exact, every decision outside rounding of its threshold).
+These run with block scales |N(0, 0.0005)|.  With the benchmark's |N(0, 0.002)| the model is so sensitive to rounding
+that fp16 storage alone moves its logits by more than the fp16 bar: the reference's own fp16 path (qwen_engine.py:39-41,
+dtype float16) lies about 0.1 max-rel from its fp32 path.  For that recipe the test below requires the HIP engine to be
+no further from the fp32 oracle than the reference's fp16 path is.
+The sequences share a 1024-token prefix that the oracle runs once; its cache is cloned per sequence."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import speculative_ref as sref
+from oracle.qwen_ref import RefQwen2, tree_attention_mask
+from seedplane_amd.presets import preset
+from seedplane_amd.qwen_engine import Qwen2Engine
+from seedplane_amd.speculative import TreeDrafter, TreeVerifier, flatten, q_rows_for_tree, uniforms
+from seedplane_amd.synth import make_weights, random_prompt
+from oracle.qwen_ref import max_rel
+from tests.parity import TOL, check_greedy, check_rows, clone_cache
+
+pytestmark = pytest.mark.gpu
+
+W = 1024            # sliding window
+PREFIX = 1024       # shared prompt prefix
+MARGIN = 1e-12
+
+
+@pytest.fixture(scope='module')
+def m15(gpu_device):
+    print('qwen2-1.5b int8: weights, engine, oracle prefix', flush=True)
+    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0, scale_std=0.0005)
+    eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    ref = RefQwen2(cfg, w)
+    del w
+    prefix = random_prompt(PREFIX, cfg['vocab_size'], seed=1)
+    rc = ref.new_cache(PREFIX)
+    ref.forward(prefix, rc, window=W)        # every position < W: the window changes nothing here
+    yield cfg, eng, ref, prefix, rc
+
+
+def test_bs1_windowed_decode_past_the_wrap(m15):
+    cfg, eng, ref, prefix, rc = m15
+    V, steps = cfg['vocab_size'], 16
+    suffix = random_prompt(76, V, seed=2)
+    prompt = prefix + suffix                 # 1100 positions: past the window and the 1024 + 64 slot ring
+    print('1.5b bs1: prefill + decode', flush=True)
+    cache = eng.new_cache(4096, window=W)
+    lg, cache = eng.forward(prompt, cache)
+    rows = torch.empty((steps, V), dtype=torch.float32, device=eng.device)
+    rows[0].copy_(lg[0])
+    toks = [int(lg[0].argmax())]
+    for s in range(1, steps):
+        toks.append(int(eng.decode([toks[-1]], [cache], logits_out=rows[s:s + 1])[0]))
+    assert list(eng.generate(prompt, steps, window=W)) == toks      # device-side feed: same ids
+    print('1.5b bs1: oracle', flush=True)
+    oc = clone_cache(ref, rc, len(prompt) + steps)
+    ref_rows = torch.cat([ref.forward(suffix, oc, window=W)[-1:],
+                          ref.forward(toks[:-1], oc, all_logits=True, window=W)])
+    worst = check_rows(rows.cpu(), ref_rows, what='bs1')
+    same = check_greedy(toks, ref_rows, what='bs1')
+    print(f'1.5b bs1: worst max-rel {worst:.2e}, {same}/{steps} ids equal the oracle argmax', flush=True)
+    assert same >= 0.75 * steps          # the margin rule allows close races; most steps are not close
+
+
+def test_bs16_windowed_decode_each_sequence_vs_oracle(m15):
+    cfg, eng, ref, prefix, rc = m15
+    V, B, steps = cfg['vocab_size'], 16, 16
+    lens = [6 + 9 * i for i in range(B)]                 # contexts 1030 .. 1165 positions
+    suffixes = [random_prompt(n, V, seed=100 + i) for i, n in enumerate(lens)]
+    prompts = [prefix + s for s in suffixes]
+    print('1.5b bs16: prefill + decode', flush=True)
+    caches = [eng.new_cache(4096, window=W) for _ in range(B)]
+    first = eng.prefill(prompts, caches)
+    rows = torch.empty((steps, B, V), dtype=torch.float32, device=eng.device)
+    toks = [list(first)]
+    for s in range(steps):
+        toks.append([int(t) for t in eng.decode(toks[-1], caches, logits_out=rows[s])])
+    per_seq = [[toks[s][b] for s in range(steps + 1)] for b in range(B)]
+    assert eng.generate_batch(prompts, steps + 1, window=W) == per_seq      # device-side feed, bursts
+    rows = rows.cpu()
+    worst, same = 0.0, 0
+    for b in range(B):
+        print(f'1.5b bs16: oracle sequence {b} ({len(prompts[b])} positions)', flush=True)
+        oc = clone_cache(ref, rc, len(prompts[b]) + steps + 1)
+        ref_rows = torch.cat([ref.forward(suffixes[b], oc, window=W)[-1:],
+                              ref.forward(per_seq[b][:-1], oc, all_logits=True, window=W)])
+        worst = max(worst, check_rows(rows[:, b], ref_rows[1:], what=f'bs16 seq {b}'))
+        same += check_greedy(per_seq[b], ref_rows, what=f'bs16 seq {b}')
+    print(f'1.5b bs16: worst max-rel {worst:.2e}, {same}/{B * (steps + 1)} ids equal the oracle argmax', flush=True)
+    assert same >= 0.75 * B * (steps + 1)
+
+
+@pytest.fixture(scope='module')
+def drafter(gpu_device):
+    print('qwen2-0.5b fp16 drafter', flush=True)
+    cfg, w = make_weights(preset('qwen2-0.5b'), 'f16', seed=1)
+    return Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+
+
+def test_tree_verify_8x4_over_2048_prefix_vs_oracle(m15, drafter):
+    cfg, eng, ref, prefix, rc = m15
+    V = cfg['vocab_size']
+    more = random_prompt(PREFIX, V, seed=3)
+    ctx, root = prefix + more[:-1], more[-1]         # 2047 cached positions; the root is position 2047
+    P = len(ctx)
+    print('1.5b tree: target prefill, drafter proposal', flush=True)
+    cache = eng.new_cache(P + 64)
+    eng.forward(ctx, cache)
+    dcache = drafter.new_cache(P + 64)
+    u = uniforms(7, 0, 8 * 4 + 64)
+    branches, drows, used = TreeDrafter(drafter).propose(dcache, ctx + [root], 8, 4, 0.8, u)
+    tree = flatten(root, branches)
+    assert tree.size > 8 and tree.max_depth == 4
+    verifier = TreeVerifier(eng)
+    p = torch.empty((tree.size, V), dtype=torch.float32, device=eng.device)
+    ids = verifier.forward(cache, tree, logits_out=p)
+    print(f'1.5b tree: {tree.size} nodes; oracle masked pass', flush=True)
+    oc = clone_cache(ref, rc, P + tree.size)
+    ref.forward(more[:-1], oc)                       # full causal attention over the 2047-position prefix
+    allowed = tree_attention_mask(P, tree.parent)
+    positions = [P + d for d in tree.depth]
+    ref_rows = ref.forward_masked(tree.token, oc, positions, allowed)
+    worst = check_rows(p.cpu(), ref_rows, what='tree')
+    same = check_greedy([int(t) for t in ids], ref_rows, what='tree')
+    print(f'1.5b tree: worst max-rel {worst:.2e}, {same}/{tree.size} node ids equal the oracle argmax', flush=True)
+    q = q_rows_for_tree(tree, drows, V, eng.device)
+    got = verifier.accept(p, q, tree, u[used:], 0.8)
+    t = dict(token=tree.token, trial_start=tree.trial_start, n_trials=tree.n_trials, trials=tree.trials)
+    path, final, n_u, bonus, margin = sref.accept_tree(p.cpu().numpy(), q.cpu().numpy(), t, np.asarray(u[used:]), 0.8,
+                                                       tree.max_depth)
+    assert margin > MARGIN
+    assert (got[0], got[1], got[2], got[3]) == (path, final, n_u, bonus)
+
+
+def test_benchmark_recipe_no_further_from_fp32_than_reference_fp16(gpu_device):
+    """Scales |N(0, 0.002)|: the HIP engine's logits lie no further from the fp32 oracle than the reference's own fp16
+    execution does (per decode step, worst row), and its greedy ids follow the fp32 oracle wherever the top-2 margin
+    exceeds that distance."""
+    print('1.5b benchmark recipe: weights, engine', flush=True)
+    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
+    V, steps = cfg['vocab_size'], 16
+    eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    prompt = random_prompt(1100, V, seed=2)
+    cache = eng.new_cache(4096, window=W)
+    lg, cache = eng.forward(prompt, cache)
+    rows = torch.empty((steps, V), dtype=torch.float32, device=eng.device)
+    rows[0].copy_(lg[0])
+    toks = [int(lg[0].argmax())]
+    for s in range(1, steps):
+        toks.append(int(eng.decode([toks[-1]], [cache], logits_out=rows[s:s + 1])[0]))
+    gpu = rows.cpu()
+    del eng, cache
+    seq = prompt + toks[:-1]
+    out = {}
+    for mode in (None, 'fp16'):
+        print(f'1.5b benchmark recipe: oracle storage={mode}', flush=True)
+        ref = RefQwen2(cfg, w, storage=mode)
+        out[mode] = ref.forward(seq, ref.new_cache(len(seq)), all_logits=True, window=W)[len(prompt) - 1:]
+        del ref
+    e_gpu = max(max_rel(gpu[i], out[None][i]) for i in range(steps))
+    e_f16 = max(max_rel(out['fp16'][i], out[None][i]) for i in range(steps))
+    print(f'1.5b benchmark recipe: HIP vs fp32 {e_gpu:.3e}; reference fp16 path vs fp32 {e_f16:.3e}', flush=True)
+    assert e_gpu <= max(TOL, e_f16)
+    check_greedy(toks, out[None], tol=max(TOL, e_f16), what='benchmark recipe')

@@ -53,6 +53,19 @@ def test_gpu_sample_rejects_bad_arguments(eng):
         eng.sample_gpu(lg, [0], [0.5], 0.0)
     with pytest.raises(ValueError):
         eng.sample_gpu(lg, [0], [0.5], 1.0, 0, 0.0)
+    # every row index is checked on the host before the launch: nothing out of bounds reaches the kernel
+    with pytest.raises(ValueError):
+        eng.sample_gpu(lg, [0], [0.5, 0.5], 1.0)                 # fewer rows than draws
+    with pytest.raises(ValueError):
+        eng.sample_gpu(lg, [2], [0.5], 1.0)                      # row past the end
+    with pytest.raises(ValueError):
+        eng.sample_gpu(lg, [-1], [0.5], 1.0)
+    with pytest.raises(ValueError):
+        eng.sample_gpu(torch.zeros((100, 2), device='cuda').t(), [0], [0.5], 1.0)   # strided rows
+    with pytest.raises(ValueError):
+        eng.sample_gpu(lg, None, [0.5, 0.5], 1.0, rows_dev=torch.zeros(1, dtype=torch.int32, device='cuda'))
+    flat = np.zeros(100, dtype=np.float32)
+    assert eng.sample_gpu(lg, [1, 0], [0.25, 0.75], 1.0) == [sample_filtered(flat, 1.0, 0, 1.0, u) for u in (0.25, 0.75)]
 
 
 def test_generate_with_temperature_uses_gpu_draws(eng):

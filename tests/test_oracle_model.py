@@ -173,3 +173,33 @@ def test_synthetic_recipes_have_the_stated_statistics():
     # determinism
     _, again = make_weights(cfg, 'q8', seed=0)
     assert torch.equal(again['model.layers.1.self_attn.q_proj.qweight'], w8['model.layers.1.self_attn.q_proj.qweight'])
+
+
+def test_storage_modes_round_where_they_say(tiny_f32):
+    # 'fp16' is the reference at dtype float16 (qwen_engine.py:39-41), 'hip' rounds where the HIP engine stores fp16;
+    # both stay within fp16 distance of the fp32 oracle, differ from it, and keep only fp16 values in the K/V cache
+    cfg, w = tiny_f32
+    ids = [1, 2, 3, 4, 5, 6, 7, 49, 0]
+    base = RefQwen2(cfg, w).forward(ids, RefQwen2(cfg, w).new_cache(16), all_logits=True)
+    for mode in ('fp16', 'hip'):
+        ref = RefQwen2(cfg, w, storage=mode)
+        c = ref.new_cache(16)
+        lg = ref.forward(ids, c, all_logits=True)
+        rel = float((lg - base).abs().max() / base.abs().max())
+        assert 0 < rel < 2e-2, (mode, rel)
+        for t in c.keys + c.values:
+            assert torch.equal(t, t.half().float()), mode
+    with pytest.raises(ValueError):
+        RefQwen2(cfg, w, storage='bf16')
+
+
+def test_fp16_storage_matches_transformers_in_fp16(tiny_f32):
+    # an independent fp16 execution of the same model: Transformers' Qwen2 with every tensor in float16
+    cfg, w = tiny_f32
+    ref = RefQwen2(cfg, w, storage='fp16')
+    m = _hf_model(cfg, w).half()
+    ids = [1, 2, 3, 4, 5, 6, 7, 49, 0]
+    with torch.no_grad():
+        hf = m(torch.tensor([ids])).logits[0].float()
+    ours = ref.forward(ids, ref.new_cache(16), all_logits=True)
+    assert float((hf - ours).abs().max() / hf.abs().max()) < 1e-2
