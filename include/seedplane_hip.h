@@ -184,6 +184,13 @@ size_t sp_op_argmax_workspace(int32_t rows, int32_t cols);
 int sp_op_argmax(const float *logits_dev, int32_t rows, int32_t cols, int32_t *out_dev, void *workspace_dev,
                  void *hip_stream);
 
+/* No counterpart in the reference.  sp_op_argmax for callers that cannot allocate (code under HIP graph capture,
+ * serving loops that forbid allocation): the same kernels and ids, with the partials in a device array of the
+ * library's own (256 KiB per GPU, held until the process ends) instead of a workspace.  No hipMalloc / hipFree or
+ * other allocating call is made.  rows <= 512 (SP_EINVAL beyond).  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (on different streams, or from different host threads without ordering) race. */
+int sp_op_argmax_noalloc(const float *logits_dev, int32_t rows, int32_t cols, int32_t *out_dev, void *hip_stream);
+
 /* A packed projection matrix in HBM, for kernel-level tests and roofline measurement of the GEMV alone.
  * Replaces the per-matrix path of F.linear (qwen_engine.py:121,136,138-139,143) and gemv.comp. */
 typedef struct sp_weight sp_weight;

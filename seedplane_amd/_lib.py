@@ -62,6 +62,7 @@ SIGNATURES = {
                                     ctypes.POINTER(c_uint64)]),
     'sp_op_argmax_workspace': (c_size_t, [c_int32, c_int32]),
     'sp_op_argmax': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    'sp_op_argmax_noalloc': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     'sp_weight_create': (c_int, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, ctypes.POINTER(c_void_p)]),
     'sp_weight_destroy': (None, [c_void_p]),
     'sp_weight_bytes': (c_uint64, [c_void_p]),

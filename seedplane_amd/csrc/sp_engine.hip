@@ -11,6 +11,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <mutex>
 #include <tuple>
 #include <type_traits>
 #include <string>
@@ -1346,16 +1347,62 @@ size_t sp_op_argmax_workspace(int32_t rows, int32_t cols) {
     return rows <= 0 ? 0 : (size_t)rows * ARGMAX_BLOCKS * (sizeof(float) + sizeof(int));
 }
 
+}  // extern "C"
+
+namespace {
+// Both argmax entry points: ARGMAX_BLOCKS partial (value, index) pairs per row in `ws` (fp32 values of every row,
+// then int32 indices), then one wave per row merges them.  Every partial is written before it is read, so `ws` needs
+// no clearing.
+void launch_argmax(const float *logits, int rows, int cols, int *out, void *ws, hipStream_t st) {
+    float *pv = (float *)ws;
+    int *pi = (int *)(pv + (size_t)rows * ARGMAX_BLOCKS);
+    hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, rows), dim3(256), 0, st, logits, cols, cols, pv, pi);
+    hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pv, pi, out);
+    HIPCHK(hipGetLastError());
+}
+
+// The partials of sp_op_argmax_noalloc live in this array of the library's own, so that entry point allocates
+// nothing.  In host code `scratch` names a host-side stand-in, not device memory: kernels get the device address that
+// hipGetSymbolAddress returns, looked up once per device with that device current (each GPU holds its own copy at
+// its own address until the process ends).
+constexpr int NOALLOC_ARGMAX_MAX_ROWS = 512;
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)NOALLOC_ARGMAX_MAX_ROWS * ARGMAX_BLOCKS * (sizeof(float) + sizeof(int));
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+std::map<int, void *> g_scratch_of;      // device ordinal -> device address of `scratch` there
+
+void *scratch_on_current_device() {
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch_of.find(dev);
+    if (it != g_scratch_of.end()) return it->second;
+    void *ptr = nullptr;
+    HIPCHK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    require(ptr != nullptr, SP_EHIP, "hipGetSymbolAddress returned no address for the argmax scratch array");
+    g_scratch_of.emplace(dev, ptr);
+    return ptr;
+}
+}  // namespace
+
+extern "C" {
+
 int sp_op_argmax(const float *logits_dev, int32_t rows, int32_t cols, int32_t *out_dev, void *ws, void *stream) {
     return guarded(nullptr, [&] {
         require(logits_dev && out_dev && ws, SP_EINVAL, "NULL pointer");
         require(rows >= 1 && rows <= 65535 && cols >= 1, SP_EINVAL, "rows must be in [1, 65535] and cols positive");
-        float *pv = (float *)ws;
-        int *pi = (int *)(pv + (size_t)rows * ARGMAX_BLOCKS);
-        hipStream_t st = (hipStream_t)stream;
-        hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, rows), dim3(256), 0, st, logits_dev, cols, cols, pv, pi);
-        hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pv, pi, out_dev);
-        HIPCHK(hipGetLastError());
+        launch_argmax(logits_dev, rows, cols, out_dev, ws, (hipStream_t)stream);
+    });
+}
+
+int sp_op_argmax_noalloc(const float *logits_dev, int32_t rows, int32_t cols, int32_t *out_dev, void *stream) {
+    return guarded(nullptr, [&] {
+        require(logits_dev && out_dev, SP_EINVAL, "NULL pointer");
+        require(cols >= 1, SP_EINVAL, "cols must be positive");
+        require(rows >= 1 && rows <= NOALLOC_ARGMAX_MAX_ROWS, SP_EINVAL,
+                "rows must be in [1, 512]: the allocation-free argmax keeps the partials of at most 512 rows");
+        launch_argmax(logits_dev, rows, cols, out_dev, scratch_on_current_device(), (hipStream_t)stream);
     });
 }
 
