@@ -1,84 +1,111 @@
-"""Native SeedPlane bundle (`seedplane-bundle/2` layout) holding engine-ready, optionally quantized tensors.
+"""On-disk bundles in the reference's `seedplane-bundle/2` layout, extended with the quantized matrices the HIP engine
+runs.
 
     python -m seedplane_amd.native_bundle <hf_dir> <out.sp> [--bits 8|4] [--shard 512 --halo 256 --sinks 4]
 
-Same directory layout and manifest schema as the reference converter (seedplane/native_bundle.py:1-137):
+A bundle is a directory (format of the reference converter, seedplane/native_bundle.py:62-137, read by
+native/vulkan_decode/qwen_vk.cpp:63-85):
 
-  seedplane.json  architecture, shard plan, tensor table, SHA-256 of the source files and of weights.spw
-  weights.spw     engine-ready tensors, each at a 256-byte aligned offset: fused QKV (+ bias), gate / up, down, o,
-                  embedding (and head when untied), fp32 norms and biases
-  tokenizer.json  (+ tokenizer_config.json, chat_template.jinja, generation_config.json when present)
+  seedplane.json  format, engine, source files with their SHA-256, shard plan, architecture, the tensor table
+                  (name -> dtype, shape, byte offset, byte count) and the SHA-256 of weights.spw
+  weights.spw     the tensors back to back, each starting at a multiple of 256 bytes: fused QKV weight (+ fp32 bias),
+                  o, gate, up, down, fp32 norms, the embedding (and the head when untied)
+  tokenizer.json  and the other tokenizer / generation files of the checkpoint, copied when present
 
-Extension over the reference: matrices may be stored quantized in the formats the HIP engine runs --
-int8 symmetric in blocks of 32 along K with one fp16 scale per block (`q8`: codes int8 [N, K], scales fp16
-[N, K/32]) or int4 asymmetric in groups of 32 (`q4`: two codes per byte, even k in the low nibble, [N, K/2] uint8;
-fp16 scale and fp16 zero per group), w = (code - zero) * scale.  A source checkpoint that is already quantized this
-way (`quantization_config.quant_method == 'seedplane'`, tensors `<name>.qweight/.scales/.qzeros`) is copied code for
-code; a float checkpoint is rounded to fp16 (reference behaviour) or quantized with `--bits`.
+Float bundles hold fp16 matrices and are `seedplane-bundle/2` exactly as the reference writes them, so either side
+can read the other's.  Quantized bundles hold int8 (blocks of 32 along K, fp16 scale: `<name>` i8 [N, K] +
+`<name>.scales` f16 [N, K/32]) or int4 (groups of 32, two codes per byte with even k in the low nibble, fp16 scale and
+zero: `<name>` u8 [N, K/2] + `.scales` + `.zeros`, w = (code - zero) * scale) matrices; they carry the format string
+`seedplane-bundle/2-quant` and a `quantization` object, so the reference runtime, which checks the format string and
+would read the codes as fp16, refuses them instead.
 
-`load(path)` checks the manifest (format, engine, tensor ranges, SHA-256 of weights.spw unless verify=False) and
-returns a Hugging Face style (config, tensors) pair that `Qwen2Engine` loads; `Qwen2Engine(bundle_dir)` does this by
-itself when the directory holds a seedplane.json.  Only numpy is needed to convert; safetensors are parsed directly.
+The bundle's contents are described once, by `_layout`: the writer walks it to place tensors and the reader walks
+it to split fused matrices back into Hugging Face names.
 """
 import argparse
 import hashlib
 import json
 import shutil
-import struct
 from pathlib import Path
 
 import numpy as np
 
 FORMAT = 'seedplane-bundle/2'
+FORMAT_QUANT = 'seedplane-bundle/2-quant'
 ENGINE = 'seedplane-hip-qwen2/1'
+REFERENCE_ENGINE = 'seedplane-native-qwen2/1'       # float bundles written by the reference converter
 ALIGN = 256
 GROUP = 32
 # sinks + halo + shard must fit one column's attention range: 512 chunks of 64 keys (the split-K attention kernels)
 MAX_WINDOW = 32768
 EXTRA_FILES = ('tokenizer.json', 'tokenizer_config.json', 'chat_template.jinja', 'generation_config.json')
-_NP_DTYPE = {'f16': '<f2', 'f32': '<f4', 'i8': 'i1', 'u8': 'u1'}
-
-
-# ----------------------------------------------------------------------------------------------- source reading
-def read_safetensors(path):
-    """name -> (dtype, shape, raw uint8 view) without loading the file (native_bundle.py:26-32)."""
-    with open(path, 'rb') as f:
-        n = struct.unpack('<Q', f.read(8))[0]
-        header = json.loads(f.read(n))
-    data = np.memmap(path, dtype=np.uint8, mode='r', offset=8 + n)
-    return {k: (v['dtype'], v['shape'], data[v['data_offsets'][0]:v['data_offsets'][1]])
-            for k, v in header.items() if k != '__metadata__'}
-
-
-def as_f32(dtype, raw):
-    """float32 copy of a floating safetensors buffer; BF16 widens exactly (native_bundle.py:35-39)."""
-    if dtype == 'F32':
-        return np.frombuffer(raw, dtype='<f4').copy()
-    if dtype == 'F16':
-        return np.frombuffer(raw, dtype='<f2').astype(np.float32)
-    if dtype == 'BF16':
-        return (np.frombuffer(raw, dtype='<u2').astype(np.uint32) << 16).view(np.float32)
-    raise ValueError(f'unsupported dtype {dtype}')
+DEFAULT_PLAN = {'shard': 512, 'halo': 256, 'sinks': 4}
+_STORE = {'f16': np.dtype('<f2'), 'f32': np.dtype('<f4'), 'i8': np.dtype('i1'), 'u8': np.dtype('u1')}
 
 
 def sha256_file(path, chunk=1 << 24):
-    h = hashlib.sha256()
+    digest = hashlib.sha256()
     with open(path, 'rb') as f:
-        while True:
-            block = f.read(chunk)
-            if not block:
-                break
-            h.update(block)
-    return h.hexdigest()
+        for block in iter(lambda: f.read(chunk), b''):
+            digest.update(block)
+    return digest.hexdigest()
 
 
-def validate_plan(plan):
-    """shard > 0, halo >= 0, sinks >= 0 and the window within MAX_WINDOW (native_bundle.py:56-59)."""
-    s, h, k = plan['shard'], plan['halo'], plan['sinks']
-    if s <= 0 or h < 0 or k < 0:
-        raise ValueError(f'invalid plan {plan}')
-    if s + h + k > MAX_WINDOW:
-        raise ValueError(f'sinks + halo + shard = {s + h + k} exceeds the engine window {MAX_WINDOW}')
+def check_plan(plan):
+    """A shard plan needs shard >= 1, halo >= 0, sinks >= 0, and a window sinks + halo + shard the kernels hold."""
+    shard, halo, sinks = (int(plan[k]) for k in ('shard', 'halo', 'sinks'))
+    if shard < 1:
+        raise ValueError(f'plan {plan}: shard must be at least 1')
+    if halo < 0 or sinks < 0:
+        raise ValueError(f'plan {plan}: halo and sinks must be non-negative')
+    if shard + halo + sinks > MAX_WINDOW:
+        raise ValueError(f'plan {plan}: window sinks + halo + shard = {shard + halo + sinks} is larger than '
+                         f'{MAX_WINDOW} positions')
+
+
+# ----------------------------------------------------------------------------------------------- checkpoint input
+class Checkpoint:
+    """The tensors of a Hugging Face checkpoint directory, memory-mapped.  A safetensors file is an 8-byte
+    little-endian header length, a JSON header (name -> dtype, shape, [begin, end) of the data) and the data."""
+
+    def __init__(self, directory):
+        self.dir = Path(directory)
+        self.files = sorted(self.dir.glob('*.safetensors'))
+        if not self.files:
+            raise FileNotFoundError(f'no safetensors in {self.dir}')
+        self._where = {}
+        for path in self.files:
+            blob = np.memmap(path, dtype=np.uint8, mode='r')
+            head = int.from_bytes(bytes(blob[:8]), 'little')
+            body = 8 + head
+            for name, info in json.loads(bytes(blob[8:body])).items():
+                if name == '__metadata__':
+                    continue
+                if name in self._where:
+                    raise ValueError(f'tensor {name} appears twice in {self.dir}')
+                begin, end = info['data_offsets']
+                self._where[name] = (info['dtype'], tuple(info['shape']), blob[body + begin:body + end])
+
+    def __contains__(self, name):
+        return name in self._where
+
+    def floats(self, name):
+        """float32 values of a floating tensor (BF16 widens exactly: its bits are the top half of an fp32)."""
+        dtype, shape, buf = self._where[name]
+        if dtype == 'BF16':
+            out = (buf.view('<u2').astype(np.uint32) << 16).view(np.float32)
+        elif dtype == 'F16':
+            out = buf.view('<f2').astype(np.float32)
+        elif dtype == 'F32':
+            out = buf.view('<f4').copy()
+        else:
+            raise ValueError(f'{name}: dtype {dtype} is not a float type')
+        return out.reshape(shape)
+
+    def stored(self, name, dtype):
+        """The tensor's bytes viewed as `dtype` (quantized codes, fp16 scales) without conversion."""
+        _, shape, buf = self._where[name]
+        return buf.view(dtype).reshape(shape)
 
 
 # ----------------------------------------------------------------------------------------------- quantizers
@@ -120,124 +147,137 @@ def quantize_q4(w):
     return packed, scale, zero
 
 
+# ----------------------------------------------------------------------------------------------- layout
+def _layout(arch):
+    """Every tensor of a bundle in file order: (bundle name, [(Hugging Face name, rows)], kind).  kind 'matrix':
+    the rows of the named matrices stacked (the engine's fused packing, qwen_engine.py:64-80); 'vector': fp32
+    values, several sources concatenated (the fused QKV bias)."""
+    L, H, I, V = arch['layers'], arch['hidden'], arch['intermediate'], arch['vocab']
+    q_rows, kv_rows = arch['heads'] * arch['head_dim'], arch['kv_heads'] * arch['head_dim']
+    yield 'embed', [('model.embed_tokens', V)], 'matrix'
+    if not arch['tied_embeddings']:
+        yield 'lm_head', [('lm_head', V)], 'matrix'
+    yield 'final_norm', [('model.norm.weight', H)], 'vector'
+    for l in range(L):
+        p = f'model.layers.{l}.'
+        attn = [(p + 'self_attn.q_proj', q_rows), (p + 'self_attn.k_proj', kv_rows), (p + 'self_attn.v_proj', kv_rows)]
+        yield f'{l}.qkv_w', attn, 'matrix'
+        yield f'{l}.qkv_b', [(n + '.bias', r) for n, r in attn], 'vector'
+        yield f'{l}.o_w', [(p + 'self_attn.o_proj', H)], 'matrix'
+        yield f'{l}.gate_w', [(p + 'mlp.gate_proj', I)], 'matrix'
+        yield f'{l}.up_w', [(p + 'mlp.up_proj', I)], 'matrix'
+        yield f'{l}.down_w', [(p + 'mlp.down_proj', H)], 'matrix'
+        yield f'{l}.in_norm', [(p + 'input_layernorm.weight', H)], 'vector'
+        yield f'{l}.post_norm', [(p + 'post_attention_layernorm.weight', H)], 'vector'
+
+
+# the parts of a stored matrix: (bundle suffix, Hugging Face suffix, dtype) per weight format
+_PARTS = {None: [('', '.weight', 'f16')],
+          8: [('', '.qweight', 'i8'), ('.scales', '.scales', 'f16')],
+          4: [('', '.qweight', 'u8'), ('.scales', '.scales', 'f16'), ('.zeros', '.qzeros', 'f16')]}
+
+
+class _WeightsFile:
+    """Appends tensors to weights.spw, each at an ALIGN-byte boundary, hashing every byte written (padding too) and
+    counting the values fp16 cannot hold (overflow) or rounds to zero."""
+
+    def __init__(self, path):
+        self.f = open(path, 'wb')
+        self.sha = hashlib.sha256()
+        self.table = {}
+        self.overflow = self.flushed = 0
+
+    def _emit(self, data):
+        self.f.write(data)
+        self.sha.update(data)
+
+    def add(self, name, values, dtype):
+        if dtype == 'f16' and values.dtype != np.float16:
+            wide = np.asarray(values, dtype=np.float32)
+            values = wide.astype(np.float16)
+            self.overflow += int(np.count_nonzero(np.abs(wide) > 65504))
+            self.flushed += int(np.count_nonzero((values == 0) & (wide != 0)))
+        data = np.ascontiguousarray(values, dtype=_STORE[dtype])
+        self._emit(bytes(-self.f.tell() % ALIGN))
+        self.table[name] = {'dtype': dtype, 'shape': list(data.shape), 'offset': self.f.tell(), 'bytes': data.nbytes}
+        self._emit(data.tobytes())
+
+    def close(self):
+        self.f.close()
+
+
 # ----------------------------------------------------------------------------------------------- convert
+def _arch_of(cfg):
+    L, H = cfg['num_hidden_layers'], cfg['hidden_size']
+    NH, NKV = cfg['num_attention_heads'], cfg['num_key_value_heads']
+    if H % NH or NH % NKV:
+        raise ValueError('invalid Qwen2 head configuration')
+    theta = cfg.get('rope_theta', cfg.get('rope_parameters', {}).get('rope_theta', 10000.0))
+    return {'model_type': 'qwen2', 'layers': L, 'hidden': H, 'heads': NH, 'kv_heads': NKV, 'head_dim': H // NH,
+            'intermediate': cfg['intermediate_size'], 'vocab': cfg['vocab_size'], 'rope_theta': theta,
+            'rms_norm_eps': cfg.get('rms_norm_eps', 1e-6), 'max_positions': cfg.get('max_position_embeddings', 32768),
+            'tied_embeddings': None}
+
+
 def convert(src, out, bits=None, shard=None, halo=None, sinks=None):
-    """Write the bundle for the Hugging Face Qwen2 checkpoint directory `src` into `out`; returns the manifest."""
+    """Write the bundle of the Hugging Face Qwen2 checkpoint directory `src` into `out`; returns the manifest.
+    Float matrices are rounded to fp16, or quantized with bits = 8 / 4; a checkpoint that is already quantized in the
+    engine's formats (quantization_config.quant_method 'seedplane', `<name>.qweight/.scales/.qzeros`) keeps its
+    codes.  The plan and source name of a version-1 seedplane.json in `src` carry over; shard / halo / sinks given
+    here replace the plan's values."""
     src, out = Path(src), Path(out)
     if not src.is_dir():
         raise FileNotFoundError(f'{src} is not a checkpoint directory')
     cfg = json.loads((src / 'config.json').read_text())
     if cfg.get('model_type') != 'qwen2':
         raise ValueError('the native engine currently supports model_type=qwen2 only')
-    v1 = src / 'seedplane.json'
-    v1_meta = json.loads(v1.read_text()) if v1.exists() else {}
-    plan = dict(v1_meta.get('plan', {'shard': 512, 'halo': 256, 'sinks': 4}))
-    for key, val in (('shard', shard), ('halo', halo), ('sinks', sinks)):
-        if val is not None:
-            plan[key] = val
-    validate_plan(plan)
+    old = json.loads((src / 'seedplane.json').read_text()) if (src / 'seedplane.json').exists() else {}
+    plan = {**DEFAULT_PLAN, **old.get('plan', {})}
+    plan.update({k: v for k, v in (('shard', shard), ('halo', halo), ('sinks', sinks)) if v is not None})
+    check_plan(plan)
 
-    L, H = cfg['num_hidden_layers'], cfg['hidden_size']
-    NH, NKV = cfg['num_attention_heads'], cfg['num_key_value_heads']
-    I, V = cfg['intermediate_size'], cfg['vocab_size']
-    if H % NH or NH % NKV:
-        raise ValueError('invalid Qwen2 head configuration')
-    HD = H // NH
-    theta = cfg.get('rope_theta', cfg.get('rope_parameters', {}).get('rope_theta', 10000.0))
-    sq = cfg.get('quantization_config') or {}
-    src_bits = sq.get('bits') if sq.get('quant_method') == 'seedplane' else None
-    if src_bits is not None and bits is not None and bits != src_bits:
-        raise ValueError(f'checkpoint is already {src_bits}-bit; requantization is not supported')
-    bits = src_bits if src_bits is not None else bits
+    qc = cfg.get('quantization_config') or {}
+    held = qc.get('bits') if qc.get('quant_method') == 'seedplane' else None
+    if held is not None and bits not in (None, held):
+        raise ValueError(f'the checkpoint is already {held}-bit; requantizing is not supported')
+    bits = held if held is not None else bits
     if bits not in (None, 8, 4):
         raise ValueError('bits must be 8 or 4')
 
-    files = sorted(src.glob('*.safetensors'))
-    if not files:
-        raise FileNotFoundError(f'no safetensors in {src}')
-    t = {}
-    for f in files:
-        for name, v in read_safetensors(f).items():
-            if name in t:
-                raise ValueError(f'duplicate tensor {name}')
-            t[name] = v
-    get = lambda name: as_f32(t[name][0], t[name][2]).reshape(t[name][1])
-    raw = lambda name, dt: np.frombuffer(t[name][2], dtype=dt).reshape(t[name][1])
-    tied = 'lm_head.weight' not in t and 'lm_head.qweight' not in t
-
+    ck = Checkpoint(src)
+    arch = _arch_of(cfg)
+    arch['tied_embeddings'] = 'lm_head.weight' not in ck and 'lm_head.qweight' not in ck
     out.mkdir(parents=True, exist_ok=True)
-    table, stats, h = {}, {'fp16_overflow': 0, 'fp16_flushed_to_zero': 0}, hashlib.sha256()
-    with open(out / 'weights.spw', 'wb') as w:
-        def put(name, arr, dtype):
-            arr = np.ascontiguousarray(arr)
-            if dtype == 'f16' and arr.dtype != np.float16:
-                a32 = arr.astype(np.float32)
-                data = a32.astype(np.float16)
-                stats['fp16_overflow'] += int((np.abs(a32) > 65504).sum())
-                stats['fp16_flushed_to_zero'] += int(((a32 != 0) & (data == 0)).sum())
+    wf = _WeightsFile(out / 'weights.spw')
+    try:
+        for name, sources, kind in _layout(arch):
+            if kind == 'vector':
+                wf.add(name, np.concatenate([ck.floats(s).reshape(-1) for s, _ in sources]), 'f32')
+            elif held is not None:          # codes, scales (and zeros) exactly as the checkpoint holds them
+                for suffix, hf_suffix, dtype in _PARTS[held]:
+                    wf.add(name + suffix, np.concatenate([ck.stored(s + hf_suffix, _STORE[dtype]) for s, _ in sources]),
+                           dtype)
             else:
-                data = arr.astype(_NP_DTYPE[dtype])
-            pad = (-w.tell()) % ALIGN
-            if pad:
-                w.write(b'\0' * pad)
-                h.update(b'\0' * pad)
-            buf = data.astype(_NP_DTYPE[dtype]).tobytes()
-            table[name] = {'dtype': dtype, 'shape': list(data.shape), 'offset': w.tell(), 'bytes': len(buf)}
-            w.write(buf)
-            h.update(buf)
-
-        def put_matrix(name, parts):
-            """Rows of the HF matrices `parts` concatenated (the engine's fused packing, qwen_engine.py:71-76)."""
-            if src_bits is not None:            # copy the checkpoint's codes
-                put(name, np.concatenate([raw(p + '.qweight', 'i1' if src_bits == 8 else 'u1') for p in parts]),
-                    'i8' if src_bits == 8 else 'u8')
-                put(name + '.scales', np.concatenate([raw(p + '.scales', '<f2') for p in parts]), 'f16')
-                if src_bits == 4:
-                    put(name + '.zeros', np.concatenate([raw(p + '.qzeros', '<f2') for p in parts]), 'f16')
-                return
-            m = np.concatenate([get(p + '.weight') for p in parts])
-            if bits is None:
-                put(name, m, 'f16')
-            elif bits == 8:
-                c, s = quantize_q8(m)
-                put(name, c, 'i8')
-                put(name + '.scales', s, 'f16')
-            else:
-                c, s, z = quantize_q4(m)
-                put(name, c, 'u8')
-                put(name + '.scales', s, 'f16')
-                put(name + '.zeros', z, 'f16')
-
-        put_matrix('embed', ['model.embed_tokens'])
-        if not tied:
-            put_matrix('lm_head', ['lm_head'])
-        put('final_norm', get('model.norm.weight'), 'f32')
-        for l in range(L):
-            p = f'model.layers.{l}.'
-            att = [p + 'self_attn.q_proj', p + 'self_attn.k_proj', p + 'self_attn.v_proj']
-            put_matrix(f'{l}.qkv_w', att)
-            put(f'{l}.qkv_b', np.concatenate([get(n + '.bias') for n in att]), 'f32')
-            put_matrix(f'{l}.o_w', [p + 'self_attn.o_proj'])
-            put_matrix(f'{l}.gate_w', [p + 'mlp.gate_proj'])
-            put_matrix(f'{l}.up_w', [p + 'mlp.up_proj'])
-            put_matrix(f'{l}.down_w', [p + 'mlp.down_proj'])
-            put(f'{l}.in_norm', get(p + 'input_layernorm.weight'), 'f32')
-            put(f'{l}.post_norm', get(p + 'post_attention_layernorm.weight'), 'f32')
-
-    for name in EXTRA_FILES:
-        if (src / name).exists():
-            shutil.copyfile(src / name, out / name)
+                rows = np.concatenate([ck.floats(s + '.weight') for s, _ in sources])
+                parts = (rows,) if bits is None else quantize_q8(rows) if bits == 8 else quantize_q4(rows)
+                for (suffix, _, dtype), values in zip(_PARTS[bits], parts):
+                    wf.add(name + suffix, values, dtype)
+    finally:
+        wf.close()
+    for extra in EXTRA_FILES:
+        if (src / extra).exists():
+            shutil.copyfile(src / extra, out / extra)
     manifest = {
-        'format': FORMAT, 'engine': ENGINE,
-        'source': v1_meta.get('source', str(src)),
-        'source_files': {f.name: sha256_file(f) for f in files},
+        'format': FORMAT if bits is None else FORMAT_QUANT,
+        'engine': ENGINE,
+        'source': old.get('source', str(src)),
+        'source_files': {f.name: sha256_file(f) for f in ck.files},
         'plan': plan,
-        'arch': {'model_type': 'qwen2', 'layers': L, 'hidden': H, 'heads': NH, 'kv_heads': NKV, 'head_dim': HD,
-                 'intermediate': I, 'vocab': V, 'rope_theta': theta, 'rms_norm_eps': cfg.get('rms_norm_eps', 1e-6),
-                 'max_positions': cfg.get('max_position_embeddings', 32768), 'tied_embeddings': tied},
+        'arch': arch,
         'quantization': None if bits is None else {'method': 'seedplane', 'bits': bits, 'group_size': GROUP},
-        'weights': {'file': 'weights.spw', 'sha256': h.hexdigest(), 'align': ALIGN, **stats},
-        'tensors': table,
+        'weights': {'file': 'weights.spw', 'sha256': wf.sha.hexdigest(), 'align': ALIGN,
+                    'fp16_overflow': wf.overflow, 'fp16_flushed_to_zero': wf.flushed},
+        'tensors': wf.table,
         'note': 'weights converted (fp16 rounding or seedplane int8/int4 quantization), never retrained',
     }
     (out / 'seedplane.json').write_text(json.dumps(manifest, indent=1))
@@ -246,98 +286,88 @@ def convert(src, out, bits=None, shard=None, halo=None, sinks=None):
 
 # ----------------------------------------------------------------------------------------------- load
 def is_bundle(path):
-    return (Path(path) / 'seedplane.json').is_file()
+    return path is not None and (Path(path) / 'seedplane.json').is_file()
 
 
 def read_manifest(path):
+    """The bundle's manifest after its identity checks: `seedplane-bundle/2` from this build or from the reference
+    converter (fp16 / fp32 tensors only), or `seedplane-bundle/2-quant` from this build; a valid shard plan."""
     p = Path(path) / 'seedplane.json'
     if not p.is_file():
         raise FileNotFoundError(f'{path} has no seedplane.json')
     m = json.loads(p.read_text())
-    if m.get('format') != FORMAT:
-        raise ValueError(f'unsupported bundle format {m.get("format")!r} (expected {FORMAT})')
-    if m.get('engine') != ENGINE:
-        raise ValueError(f'bundle was written for engine {m.get("engine")!r}, not {ENGINE}')
-    validate_plan(m['plan'])
+    fmt, engine = m.get('format'), m.get('engine')
+    if fmt == FORMAT:
+        if engine not in (ENGINE, REFERENCE_ENGINE):
+            raise ValueError(f'{FORMAT} bundle of unknown engine {engine!r}')
+        odd = sorted({t.get('dtype') for t in m.get('tensors', {}).values()} - {'f16', 'f32'})
+        if odd:
+            raise ValueError(f'a {FORMAT} bundle holds fp16 / fp32 tensors only, not {odd}')
+    elif fmt == FORMAT_QUANT:
+        if engine != ENGINE:
+            raise ValueError(f'{FORMAT_QUANT} bundle of unknown engine {engine!r}')
+    else:
+        raise ValueError(f'unsupported bundle format {fmt!r} (expected {FORMAT} or {FORMAT_QUANT})')
+    check_plan(m['plan'])
     return m
 
 
 def load(path, verify=True):
-    """(config, tensors) of a bundle: config in Hugging Face config.json form (with the seedplane
-    quantization_config when quantized), tensors as CPU torch tensors under Hugging Face names (fused matrices are
-    split back into row views).  With verify, weights.spw must match the manifest's SHA-256."""
+    """(config, tensors) of a bundle: a Hugging Face style config.json dictionary (with the seedplane
+    quantization_config when quantized) and CPU torch tensors under Hugging Face names (fused matrices split back
+    into row views).  With verify, weights.spw must match the manifest's SHA-256."""
     import torch
     path = Path(path)
     m = read_manifest(path)
-    wf = path / m['weights']['file']
-    if not wf.is_file():
-        raise FileNotFoundError(f'{wf} is missing')
-    if verify and sha256_file(wf) != m['weights']['sha256']:
-        raise ValueError(f'{wf} does not match the SHA-256 in seedplane.json')
-    size = wf.stat().st_size
-    blob = np.memmap(wf, dtype=np.uint8, mode='c')
-    a = m['arch']
-
-    def tensor(name):
-        e = m['tensors'].get(name)
-        if e is None:
-            raise ValueError(f'bundle has no tensor {name}')
-        if e['dtype'] not in _NP_DTYPE or e['offset'] % ALIGN or e['offset'] + e['bytes'] > size:
-            raise ValueError(f'bad table entry for {name}: {e}')
-        arr = blob[e['offset']:e['offset'] + e['bytes']].view(_NP_DTYPE[e['dtype']]).reshape(e['shape'])
-        if arr.nbytes != e['bytes']:
-            raise ValueError(f'bad table entry for {name}: {e}')
-        return torch.from_numpy(arr)
-
+    wpath = path / m['weights']['file']
+    if not wpath.is_file():
+        raise FileNotFoundError(f'{wpath} is missing')
+    if verify and sha256_file(wpath) != m['weights']['sha256']:
+        raise ValueError(f'{wpath} does not match the SHA-256 in seedplane.json')
+    blob = np.memmap(wpath, dtype=np.uint8, mode='c')
+    table, arch = m['tensors'], m['arch']
     q = m.get('quantization')
     bits = q['bits'] if q else None
 
-    def matrix(out, name, parts):
-        """Split the fused matrix `name` into the HF matrices `parts` = [(hf_name, rows)]."""
-        mats = [tensor(name)] + ([tensor(name + '.scales')] if bits else []) + \
-               ([tensor(name + '.zeros')] if bits == 4 else [])
-        suffix = ['.weight'] if bits is None else ['.qweight', '.scales'] + (['.qzeros'] if bits == 4 else [])
-        r0 = 0
-        for hf, rows in parts:
-            for t, sfx in zip(mats, suffix):
-                out[hf + sfx] = t[r0:r0 + rows]
-            r0 += rows
-        if r0 != mats[0].shape[0]:
-            raise ValueError(f'{name} has {mats[0].shape[0]} rows, expected {r0}')
+    def tensor(name):
+        e = table.get(name)
+        if e is None:
+            raise ValueError(f'bundle has no tensor {name}')
+        dt = _STORE.get(e['dtype'])
+        if (dt is None or e['offset'] % ALIGN or e['offset'] + e['bytes'] > blob.size
+                or e['bytes'] != int(np.prod(e['shape'])) * dt.itemsize):
+            raise ValueError(f'bad table entry for {name}: {e}')
+        return torch.from_numpy(blob[e['offset']:e['offset'] + e['bytes']].view(dt).reshape(e['shape']))
 
-    L, H, NH, NKV, HD = a['layers'], a['hidden'], a['heads'], a['kv_heads'], a['head_dim']
-    I, V = a['intermediate'], a['vocab']
     w = {}
-    matrix(w, 'embed', [('model.embed_tokens', V)])
-    if not a['tied_embeddings']:
-        matrix(w, 'lm_head', [('lm_head', V)])
-    w['model.norm.weight'] = tensor('final_norm')
-    for l in range(L):
-        p = f'model.layers.{l}.'
-        att = [(p + 'self_attn.q_proj', NH * HD), (p + 'self_attn.k_proj', NKV * HD), (p + 'self_attn.v_proj', NKV * HD)]
-        matrix(w, f'{l}.qkv_w', att)
-        b = tensor(f'{l}.qkv_b')
-        r0 = 0
-        for hf, rows in att:
-            w[hf + '.bias'] = b[r0:r0 + rows]
-            r0 += rows
-        matrix(w, f'{l}.o_w', [(p + 'self_attn.o_proj', H)])
-        matrix(w, f'{l}.gate_w', [(p + 'mlp.gate_proj', I)])
-        matrix(w, f'{l}.up_w', [(p + 'mlp.up_proj', I)])
-        matrix(w, f'{l}.down_w', [(p + 'mlp.down_proj', H)])
-        w[p + 'input_layernorm.weight'] = tensor(f'{l}.in_norm')
-        w[p + 'post_attention_layernorm.weight'] = tensor(f'{l}.post_norm')
-    cfg = {'model_type': 'qwen2', 'num_hidden_layers': L, 'hidden_size': H, 'num_attention_heads': NH,
-           'num_key_value_heads': NKV, 'intermediate_size': I, 'vocab_size': V, 'rope_theta': a['rope_theta'],
-           'rms_norm_eps': a['rms_norm_eps'], 'max_position_embeddings': a['max_positions'],
-           'tie_word_embeddings': a['tied_embeddings']}
+    for name, sources, kind in _layout(arch):
+        if kind == 'vector':
+            flat, at = tensor(name), 0
+            for hf, n in sources:
+                w[hf] = flat[at:at + n]
+                at += n
+            if at != flat.shape[0]:
+                raise ValueError(f'{name} holds {flat.shape[0]} values, expected {at}')
+            continue
+        for suffix, hf_suffix, _ in _PARTS[bits]:
+            whole, at = tensor(name + suffix), 0
+            for hf, rows in sources:
+                w[hf + hf_suffix] = whole[at:at + rows]
+                at += rows
+            if at != whole.shape[0]:
+                raise ValueError(f'{name}{suffix} has {whole.shape[0]} rows, expected {at}')
+    cfg = {'model_type': 'qwen2', 'num_hidden_layers': arch['layers'], 'hidden_size': arch['hidden'],
+           'num_attention_heads': arch['heads'], 'num_key_value_heads': arch['kv_heads'],
+           'intermediate_size': arch['intermediate'], 'vocab_size': arch['vocab'], 'rope_theta': arch['rope_theta'],
+           'rms_norm_eps': arch['rms_norm_eps'], 'max_position_embeddings': arch['max_positions'],
+           'tie_word_embeddings': arch['tied_embeddings']}
     if bits:
         cfg['quantization_config'] = {'quant_method': 'seedplane', 'bits': bits, 'group_size': q['group_size']}
     return cfg, w
 
 
 def main():
-    ap = argparse.ArgumentParser(description='convert a Qwen2 checkpoint into a seedplane-bundle/2 directory')
+    ap = argparse.ArgumentParser(description='convert a Qwen2 checkpoint into a seedplane bundle directory')
     ap.add_argument('src')
     ap.add_argument('out')
     ap.add_argument('--bits', type=int, choices=[8, 4], default=None)

@@ -14,25 +14,10 @@ from seedplane_amd.synth import make_weights, write_bundle
 
 
 def tiny_qwen2(directory, seed=0):
-    """2-layer Qwen2 (head_dim 64) in BF16 safetensors, the reference test model (tests/test_core.py:146-165)."""
-    from safetensors.torch import save_file
-    L, H, NH, NKV, HD, I, V = 2, 128, 2, 1, 64, 256, 50
-    (Path(directory) / 'config.json').write_text(json.dumps({
-        'model_type': 'qwen2', 'num_hidden_layers': L, 'num_attention_heads': NH, 'num_key_value_heads': NKV,
-        'hidden_size': H, 'intermediate_size': I, 'vocab_size': V, 'max_position_embeddings': 512,
-        'rope_theta': 1e6, 'rms_norm_eps': 1e-6}))
-    g = torch.Generator().manual_seed(seed)
-    r = lambda *shape: torch.randn(*shape, generator=g) * 0.05
-    w = {'model.embed_tokens.weight': r(V, H) * 20, 'model.norm.weight': torch.ones(H)}
-    for l in range(L):
-        p = f'model.layers.{l}.'
-        w.update({p + 'input_layernorm.weight': torch.ones(H), p + 'post_attention_layernorm.weight': torch.ones(H),
-                  p + 'self_attn.q_proj.weight': r(H, H), p + 'self_attn.q_proj.bias': r(H),
-                  p + 'self_attn.k_proj.weight': r(NKV * HD, H), p + 'self_attn.k_proj.bias': r(NKV * HD),
-                  p + 'self_attn.v_proj.weight': r(NKV * HD, H), p + 'self_attn.v_proj.bias': r(NKV * HD),
-                  p + 'self_attn.o_proj.weight': r(H, H), p + 'mlp.gate_proj.weight': r(I, H),
-                  p + 'mlp.up_proj.weight': r(I, H), p + 'mlp.down_proj.weight': r(H, I)})
-    save_file({k: v.to(torch.bfloat16) for k, v in w.items()}, str(Path(directory) / 'model.safetensors'))
+    """The 2-layer test model of the reference (L 2, H 128, 2 / 1 heads, head_dim 64, I 256, V 50; randn * 0.05,
+    embedding x 20, unit norms) written as a BF16 safetensors checkpoint.  Returns the fp32 tensors."""
+    cfg, w = make_weights(preset('tiny'), 'f32', seed=seed)
+    write_bundle(directory, cfg, {k: v.to(torch.bfloat16) for k, v in w.items()})
     return w
 
 
@@ -164,3 +149,39 @@ def test_load_rejects_tampered_or_foreign_bundles(tmp_path):
         native_bundle.load(out)
     with pytest.raises(FileNotFoundError):
         native_bundle.load(tmp_path / 'nothing')
+
+
+def test_reference_float_bundles_load_and_quantized_bundles_fail_closed(tmp_path):
+    # the reference converter writes engine 'seedplane-native-qwen2/1' with the same tensor table: it loads here.  A
+    # quantized bundle carries a format string the reference runtime refuses (qwen_vk.cpp:68 checks it), and a
+    # seedplane-bundle/2 holding integer codes is rejected here
+    tiny_qwen2(tmp_path)
+    out = tmp_path / 'f.sp'
+    native_bundle.convert(tmp_path, out)
+    man = json.loads((out / 'seedplane.json').read_text())
+    (out / 'seedplane.json').write_text(json.dumps(dict(man, engine='seedplane-native-qwen2/1')))
+    cfg, t = native_bundle.load(out)
+    assert cfg['num_hidden_layers'] == 2 and t['model.embed_tokens.weight'].dtype == torch.float16
+    (out / 'seedplane.json').write_text(json.dumps(dict(man, engine='someone-else/1')))
+    with pytest.raises(ValueError, match='engine'):
+        native_bundle.load(out)
+    q = native_bundle.convert(tmp_path, tmp_path / 'q.sp', bits=8)
+    assert q['format'] == 'seedplane-bundle/2-quant' and q['format'] != 'seedplane-bundle/2'
+    qman = json.loads((tmp_path / 'q.sp' / 'seedplane.json').read_text())
+    (tmp_path / 'q.sp' / 'seedplane.json').write_text(json.dumps(dict(qman, format='seedplane-bundle/2')))
+    with pytest.raises(ValueError, match='fp16 / fp32'):
+        native_bundle.load(tmp_path / 'q.sp')
+
+
+def test_fused_rows_split_back_to_checkpoint_tensors(tmp_path):
+    # every Hugging Face tensor comes back from the bundle (fp16-rounded), fused matrices and the fused bias included
+    w = tiny_qwen2(tmp_path)
+    native_bundle.convert(tmp_path, tmp_path / 'b.sp')
+    cfg, t = native_bundle.load(tmp_path / 'b.sp')
+    assert set(t) == set(w)
+    for k, v in w.items():
+        want = v.to(torch.bfloat16).float()
+        got = t[k].float()
+        if v.dim() == 2:
+            want = want.half().float()
+        assert torch.equal(got, want), k
