@@ -14,8 +14,13 @@ The JSON line also carries:
                  (8 branches x 4 tokens) plus the acceptance kernel, divided by one decode step at that prefix
   roofline       the dominant kernel (the SwiGLU gate_up GEMV, the largest launch of the step), HIP-event timed
   cpu_baseline   the CPU oracle (fp32, dequantised weights) on a bounded sample of the same workload
-Other workloads (--workload): 'c2' 0.5B fp16 16-request burst, 'c5' 7B int4 batch 32 at 8k context, 'spec' the full
-speculative loop with a 0.5B fp16 drafter.
+  latency        per-token latency quantiles with one host synchronisation per token, the decode / draw split of a
+                 T > 0 token, and dispatches_per_token (kernels of the replayed step graph)
+  burst16_05b    Qwen2-0.5B fp16, 16 ragged requests x 32 tokens decoded as one batch
+  spec           the full speculative loop (0.5B fp16 drafter, 8 x 4 drafts, T 0.8) on the 1.5B int8 target
+  batch32_7b     Qwen2-7B int4, batch 32 at 8192 positions of fp16 KV each
+                 (each of the three with tok/s, hbm_frac_step and its dominant kernel's launch time and roofline)
+The same three run alone as --workload c2 / spec / c5.
 """
 import argparse
 import json
@@ -171,18 +176,73 @@ def sampling_cost(eng, V, rows=16, reps=20):
 
 
 TRAFFIC_FILE = ROOT / 'profiles' / 'k_gemv_q8_gate_up_traffic.md'
+GEMV_SOURCES = ('sp_gemv.h', 'sp_device.h', 'sp_pack.h')
+
+
+def gemv_source_hash():
+    """First 16 hex digits of the SHA-256 over the GEMV kernel's sources (kernel, device helpers, tile packing)."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in GEMV_SOURCES:
+        h.update((ROOT / 'seedplane_amd' / 'csrc' / name).read_bytes())
+    return h.hexdigest()[:16]
 
 
 def measured_traffic():
     """HBM bytes per gate_up launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter
-    scaled by what it reads for a plain copy of known size), or None when that summary is absent."""
+    scaled by what it reads for a plain copy of known size), and whether it applies: the summary records the hash of
+    the kernel sources it was measured on, and a summary of other sources is reported as stale (traffic null)."""
+    fields = {}
     try:
         for line in TRAFFIC_FILE.read_text().splitlines():
-            if line.startswith('traffic_bytes_per_launch:'):
-                return int(line.split(':')[1])
+            if ':' in line and line.split(':')[0] in ('traffic_bytes_per_launch', 'kernel_source_sha16'):
+                k, v = line.split(':', 1)
+                fields[k] = v.strip()
     except OSError:
-        pass
-    return None
+        return None, 'no traffic summary'
+    if 'traffic_bytes_per_launch' not in fields:
+        return None, 'no traffic summary'
+    if fields.get('kernel_source_sha16') != gemv_source_hash():
+        return None, 'traffic summary measured on other kernel sources (stale)'
+    return int(fields['traffic_bytes_per_launch']), f'{TRAFFIC_FILE.relative_to(ROOT)} (rocprofv3 --pmc, scaled)'
+
+
+def token_latency(eng, cache, token, n=64, warm=4):
+    """Per-token latency as a caller sees it that needs each id before the next step (one host synchronisation per
+    token, the reference's session loop, native/vulkan_decode/qwen_vk.cpp:883-897): quantiles over n tokens, the
+    kernels one step launches (the replayed graph's kernel nodes), and the split of a T > 0 token into the decode step
+    and the GPU draw (top-k 50 / top-p 0.9 at T = 0.8 over the step's logits row, HIP events)."""
+    import torch
+    from seedplane_amd.speculative import uniforms
+    lat = []
+    for i in range(n + warm):
+        t0 = time.perf_counter()
+        token = int(eng.decode([token], [cache], graph=True)[0])
+        if i >= warm:
+            lat.append(time.perf_counter() - t0)
+    dispatches = eng.last_dispatches
+    row = torch.empty((1, eng.vocab), dtype=torch.float32, device=eng.device)
+    eng.decode([token], [cache], logits_out=row, graph=True)
+    rid = torch.zeros(1, dtype=torch.int32, device=eng.device)
+    eng.sample_gpu(row, None, uniforms(2, 0, 1), 0.8, 50, 0.9, rows_dev=rid)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    sync()
+    e0.record()
+    for i in range(20):
+        eng.sample_gpu(row, None, uniforms(2, i, 1), 0.8, 50, 0.9, rows_dev=rid)
+    e1.record()
+    sync()
+    srt = sorted(lat)
+    q = lambda f: round(1e3 * srt[min(len(srt) - 1, int(f * (len(srt) - 1) + 0.5))], 4)
+    return {'p50_ms': q(0.5), 'p95_ms': q(0.95), 'p99_ms': q(0.99), 'max_ms': round(1e3 * srt[-1], 4),
+            'step_ms_mean': round(1e3 * sum(lat) / len(lat), 4), 'sample_ms_mean': round(e0.elapsed_time(e1) / 20, 4),
+            'tokens': n, 'sync': 'one host synchronisation per token'}, dispatches
+
+
+def kernel_frac(name, us, nbytes):
+    """A dominant kernel's measured launch time and its fraction of the HBM roofline for its algorithmic bytes."""
+    return {'kernel': name, 'avg_launch_us': round(us, 3), 'bytes_per_launch': nbytes,
+            'achieved_gbs': round(nbytes / (us * 1e-6) / 1e9, 1), 'frac': round(nbytes / (us * 1e-6) / PEAK_HBM, 4)}
 
 
 def gemv_roofline(eng):
@@ -192,8 +252,9 @@ def gemv_roofline(eng):
     us, gbytes = eng.time_gemv(_lib.SP_T_GATE_UP, layer=-1, n_cols=1, iters=280)
     achieved = gbytes / (us * 1e-6) / 1e9
     log(f'gate_up GEMV: {us:.2f} us/launch, {achieved:.0f} GB/s')
+    traffic, source = measured_traffic()
     return {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM / 1e9, 'unit': 'GB/s',
-            'frac': round(achieved * 1e9 / PEAK_HBM, 4), 'traffic': measured_traffic(),
+            'frac': round(achieved * 1e9 / PEAK_HBM, 4), 'traffic': traffic, 'traffic_source': source,
             'kernel': 'k_gemv<Q8, 1 m-tile, gate+up pair> (SwiGLU gate_up, 17920x1536 int8 + scales)',
             'bytes_per_launch': gbytes, 'avg_launch_us': round(us, 3)}
 
@@ -246,6 +307,8 @@ def workload_c3(args, out):
     tok_s = args.steps / dt
     step_bytes = wbytes + kv_bytes(cfg, min(W, cache.length))
     log(f'bs1: {tok_s:.1f} tok/s, {dt / args.steps * 1e3:.3f} ms/token, {step_bytes / 1e9:.3f} GB/token')
+    latency, dispatches = token_latency(eng, cache, toks[0])
+    log(f'latency: {latency}, {dispatches} kernels per step')
 
     roofline = gemv_roofline(eng)
 
@@ -273,6 +336,16 @@ def workload_c3(args, out):
     sampling = sampling_cost(eng, cfg['vocab_size'])
     log(f'sampling: {sampling}')
 
+    extra = {}
+    if not args.no_extra:
+        extra['burst16_05b'], drafter = run_c2(return_engine=True)
+        log(f"burst16_05b: {extra['burst16_05b']}")
+        extra['spec'] = run_spec(eng, cfg, drafter)
+        log(f"spec: {extra['spec']}")
+        del drafter
+        extra['batch32_7b'] = run_c5(128)
+        log(f"batch32_7b: {extra['batch32_7b']}")
+
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
@@ -288,7 +361,9 @@ def workload_c3(args, out):
                            'layers': cfg['num_hidden_layers'], 'hidden': cfg['hidden_size'],
                            'vocab': cfg['vocab_size'], 'window': W, 'prompt': args.prompt},
                 'hbm_frac_step': round(step_bytes * tok_s / PEAK_HBM, 4), 'bytes_per_token': step_bytes,
-                'bs16': bs16, 'verify': verify, 'sampling': sampling, 'roofline': roofline, 'cpu_baseline': cpu})
+                'latency': latency, 'dispatches_per_token': dispatches,
+                'bs16': bs16, 'verify': verify, 'sampling': sampling, **extra, 'roofline': roofline,
+                'cpu_baseline': cpu})
 
 
 def workload_verify(args, out):
@@ -303,14 +378,17 @@ def workload_verify(args, out):
                 'value': v['verify_over_decode'], 'unit': 'ratio', 'higher_is_better': False, 'verify': v})
 
 
-def workload_c2(args, out):
-    """0.5B fp16, 16 requests x 32 greedy tokens, prompts 16-128 ids, decoded as one batch (decode-only timing)."""
+def run_c2(return_engine=False):
+    """Qwen2-0.5B fp16, 16 requests x 32 greedy tokens, prompts of 16-128 ids, decoded as one batch (decode-only
+    timing; the K/V-only prefill is outside it).  Dominant kernel: the 16-column SwiGLU gate_up GEMV."""
     import torch
+    from seedplane_amd import _lib
     from seedplane_amd.presets import preset
     from seedplane_amd.qwen_engine import Qwen2Engine
     from seedplane_amd.synth import make_weights, random_prompt
     cfg, w = make_weights(preset('qwen2-0.5b'), 'f16', seed=0)
     eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    del w
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(16, 129, (16,), generator=g).tolist()
     prompts = [random_prompt(n, cfg['vocab_size'], seed=200 + i) for i, n in enumerate(lens)]
@@ -323,18 +401,18 @@ def workload_c2(args, out):
     wbytes, _ = eng.weight_bytes()
     mean_ctx = sum(c.length for c in caches) / 16
     step_bytes = wbytes + 16 * kv_bytes(cfg, mean_ctx)
-    out.update({'metric': 'decode tok/s, 16-request burst, Qwen2-0.5B fp16', 'value': round(tok_s, 1),
-                'unit': 'tok/s', 'steps': new - 1, 'warmup': 0, 'ms_per_step': round(dt / (new - 1) * 1e3, 4),
-                'higher_is_better': True, 'dtype': 'fp16 weights/activations/KV, fp32 accumulate',
-                'data': 'synthetic (random-init fp16 weights ~N(0,0.02), uniform random prompts of 16-128 ids)',
-                'config': {'workload': 'Qwen2-0.5B fp16, 16 requests x 32 greedy tokens, ragged prompts, batch 16',
-                           'prompt_lens': lens},
-                'hbm_frac_step': round(step_bytes * (new - 1) / dt / PEAK_HBM, 4)})
+    us, nb = eng.time_gemv(_lib.SP_T_GATE_UP, layer=-1, n_cols=16, iters=240)
+    res = {'workload': 'Qwen2-0.5B fp16, 16 requests x 32 greedy tokens, prompts of 16-128 ids, batch 16',
+           'tok_s': round(tok_s, 1), 'ms_per_step': round(dt / (new - 1) * 1e3, 4),
+           'hbm_frac_step': round(step_bytes * (new - 1) / dt / PEAK_HBM, 4), 'prompt_lens': lens,
+           'dominant_kernel': kernel_frac('k_gemv<F16, 1 m-tile, gate+up pair> 16 columns (9728x896 fp16)', us, nb)}
+    return (res, eng) if return_engine else res
 
 
-def workload_c5(args, out):
-    """7B int4 (g32 scale + zero), batch 32 at 8192 positions of full fp16 KV each, 128 decode steps.  The 8192-token
-    contexts are filled with seeded synthetic K/V (the decode step reads the same bytes)."""
+def run_c5(steps=128):
+    """Qwen2-7B int4 (g32 scale + zero), batch 32 at 8192 positions of full fp16 KV each.  The 8192-token contexts are
+    filled with seeded synthetic K/V (the decode step reads the same bytes).  Dominant kernel: the MFMA decode attention
+    (the K/V of 32 x 8192 positions is 77% of a step's bytes)."""
     from seedplane_amd.presets import preset
     from seedplane_amd.qwen_engine import Qwen2Engine
     from seedplane_amd.synth import make_weights, random_prompt
@@ -343,7 +421,7 @@ def workload_c5(args, out):
     log(f'7B int4 weights generated in {time.perf_counter() - t0:.1f}s')
     eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
     del w
-    ctx, B, steps = 8192, 32, args.steps if args.steps != 256 else 128
+    ctx, B = 8192, 32
     eng.reserve(B, ctx + steps + 8)
     caches = [eng.new_cache(ctx + steps + 8) for _ in range(B)]
     for i, c in enumerate(caches):
@@ -354,40 +432,71 @@ def workload_c5(args, out):
     tok_s = B * steps / dt
     wbytes, _ = eng.weight_bytes()
     step_bytes = wbytes + B * kv_bytes(cfg, ctx + steps // 2)
-    out.update({'metric': 'decode tok/s, Qwen2-7B int4 batch 32 at 8k context', 'value': round(tok_s, 1),
-                'unit': 'tok/s', 'steps': steps, 'warmup': 4, 'ms_per_step': round(dt / steps * 1e3, 4),
-                'higher_is_better': True, 'dtype': 'int4 weights (g32 fp16 scale+zero), fp16 activations/KV',
-                'data': 'synthetic (random-init int4 weights; 8192-position contexts filled with seeded K/V)',
-                'config': {'workload': 'Qwen2-7B int4, batch 32, 8192-token full fp16 KV per request, 128 steps'},
-                'hbm_frac_step': round(step_bytes * steps / dt / PEAK_HBM, 4), 'bytes_per_step': step_bytes})
+    us, nb = eng.time_attention(caches, iters=56)
+    return {'workload': 'Qwen2-7B int4, batch 32, 8192-token full fp16 KV per request',
+            'tok_s': round(tok_s, 1), 'ms_per_step': round(dt / steps * 1e3, 4), 'steps': steps,
+            'hbm_frac_step': round(step_bytes * steps / dt / PEAK_HBM, 4), 'bytes_per_step': step_bytes,
+            'dominant_kernel': kernel_frac('k_attn_dec<128> (32 x ~8260 keys, 4 kv heads, GQA 7)', us, nb)}
 
 
-def workload_spec(args, out):
-    """Full speculative loop: target 1.5B int8, drafter 0.5B fp16, 8 branches x 4 tokens, T = 0.8, 64 steps."""
-    from seedplane_amd.presets import preset
-    from seedplane_amd.qwen_engine import Qwen2Engine
+def run_spec(target, cfg, drafter_engine, steps=32):
+    """The full speculative loop: target 1.5B int8, drafter 0.5B fp16, 8 branches x 4 tokens, T = 0.8, seeded
+    uniforms, over a 2048-token prompt (prefill outside the timing).  Random-init models are unrelated, so few
+    drafts are accepted; the figure is the cost of a step, not a speedup."""
+    from seedplane_amd import _lib
     from seedplane_amd.speculative import SpecStats, TreeDrafter, speculative_generate
-    from seedplane_amd.synth import make_weights, random_prompt
-    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
-    target = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
-    dcfg, dw = make_weights(preset('qwen2-0.5b'), 'f16', seed=1)
-    drafter = TreeDrafter(Qwen2Engine(config=dcfg, tensors=dw, max_tokens=64))
+    from seedplane_amd.synth import random_prompt
+    drafter = TreeDrafter(drafter_engine)
     prompt = random_prompt(2048, cfg['vocab_size'], seed=9)
     stats = SpecStats()
     speculative_generate(target, drafter, prompt, steps=2, seed=0)
     sync()
     t0 = time.perf_counter()
-    toks = speculative_generate(target, drafter, prompt, steps=64, seed=1, stats=stats)
+    toks = speculative_generate(target, drafter, prompt, steps=steps, seed=1, stats=stats)
     sync()
     dt = time.perf_counter() - t0
-    out.update({'metric': 'speculative tree decode tok/s (8x4 drafts, T=0.8)', 'value': round(len(toks) / dt, 2),
-                'unit': 'tok/s', 'steps': 64, 'warmup': 2, 'ms_per_step': round(dt / 64 * 1e3, 3),
-                'higher_is_better': True, 'dtype': 'target int8 / drafter fp16, fp32 logits, fp64 acceptance',
+    us, nb = target.time_gemv(_lib.SP_T_GATE_UP, layer=-1, n_cols=33, iters=140)
+    return {'workload': 'target Qwen2-1.5B int8, drafter Qwen2-0.5B fp16, 8 branches x 4, T 0.8, 2048-token prompt',
+            'tok_s': round(len(toks) / dt, 2), 'ms_per_step': round(dt / steps * 1e3, 3), 'steps': steps,
+            'accepted_per_step': round(stats.accepted / stats.steps, 3),
+            'emitted_per_step': round(stats.emitted / stats.steps, 3),
+            'dominant_kernel': kernel_frac('k_gemv<Q8, 3 m-tiles, gate+up pair> 33 columns (tree pass)', us, nb)}
+
+
+def workload_c2(args, out):
+    r = run_c2()
+    out.update({'metric': 'decode tok/s, 16-request burst, Qwen2-0.5B fp16', 'value': r['tok_s'], 'unit': 'tok/s',
+                'steps': 31, 'warmup': 0, 'ms_per_step': r['ms_per_step'], 'higher_is_better': True,
+                'dtype': 'fp16 weights/activations/KV, fp32 accumulate',
+                'data': 'synthetic (random-init fp16 weights ~N(0,0.02), uniform random prompts of 16-128 ids)',
+                'config': {'workload': r['workload'], 'prompt_lens': r['prompt_lens']},
+                'hbm_frac_step': r['hbm_frac_step'], 'dominant_kernel': r['dominant_kernel']})
+
+
+def workload_c5(args, out):
+    steps = args.steps if args.steps != 256 else 128
+    r = run_c5(steps)
+    out.update({'metric': 'decode tok/s, Qwen2-7B int4 batch 32 at 8k context', 'value': r['tok_s'], 'unit': 'tok/s',
+                'steps': steps, 'warmup': 4, 'ms_per_step': r['ms_per_step'], 'higher_is_better': True,
+                'dtype': 'int4 weights (g32 fp16 scale+zero), fp16 activations/KV',
+                'data': 'synthetic (random-init int4 weights; 8192-position contexts filled with seeded K/V)',
+                'config': {'workload': r['workload']}, 'hbm_frac_step': r['hbm_frac_step'],
+                'bytes_per_step': r['bytes_per_step'], 'dominant_kernel': r['dominant_kernel']})
+
+
+def workload_spec(args, out):
+    from seedplane_amd.presets import preset
+    from seedplane_amd.qwen_engine import Qwen2Engine
+    from seedplane_amd.synth import make_weights
+    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
+    target = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
+    dcfg, dw = make_weights(preset('qwen2-0.5b'), 'f16', seed=1)
+    r = run_spec(target, cfg, Qwen2Engine(config=dcfg, tensors=dw, max_tokens=64), steps=64)
+    out.update({'metric': 'speculative tree decode tok/s (8x4 drafts, T=0.8)', 'value': r['tok_s'], 'unit': 'tok/s',
+                'steps': 64, 'warmup': 2, 'ms_per_step': r['ms_per_step'], 'higher_is_better': True,
+                'dtype': 'target int8 / drafter fp16, fp32 logits, fp64 acceptance',
                 'data': 'synthetic random-init target and drafter (acceptance is near zero for unrelated models)',
-                'config': {'workload': 'target Qwen2-1.5B int8, drafter Qwen2-0.5B fp16, 8 branches x 4, '
-                                       '2048-token prompt, 64 steps (prefill included in neither timing)'},
-                'accepted_per_step': round(stats.accepted / stats.steps, 3),
-                'emitted_per_step': round(stats.emitted / stats.steps, 3)})
+                'config': {'workload': r['workload']}, **{k: r[k] for k in ('accepted_per_step', 'emitted_per_step')}})
 
 
 def main():
@@ -399,6 +508,7 @@ def main():
     ap.add_argument('--no-bs16', action='store_true')
     ap.add_argument('--no-verify', action='store_true')
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-extra', action='store_true', help='skip the 0.5B burst, speculative loop and 7B int4 lines')
     ap.add_argument('--cpu-sample-tokens', type=int, default=6)
     ap.add_argument('--prompt', type=int, default=3840)
     ap.add_argument('--window', type=int, default=1024)

@@ -142,6 +142,11 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
  * 1 = the persistent single-column kernel (SP_F_PERSISTENT accepted), 0 = the kernel chain, -1 = none yet. */
 int sp_engine_last_path(const sp_engine *e);
 
+/* Introspection (no counterpart in the reference; its decode report counts dispatches per token,
+ * native/vulkan_decode/qwen_vk.cpp:866-870): kernels launched by the last sp_engine_forward call when it replayed a
+ * graph (the kernel nodes of the recorded graph), -1 after an eager call. */
+int sp_engine_last_dispatches(const sp_engine *e);
+
 /* Device pointer to the engine's fp32 logits buffer [max_tokens][vocab] holding the last SP_F_LOGITS call. */
 int sp_engine_logits(sp_engine *e, float **logits_dev);
 
@@ -166,6 +171,14 @@ int sp_engine_sync(sp_engine *e);
  * launch reads.  Clobbers the activation buffers (not the KV cache); call between forward passes only. */
 int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_cols, int32_t iters, float *avg_us,
                         uint64_t *bytes);
+
+/* Measurement hook (no counterpart in the reference): launch the attention kernel that a forward call over these n
+ * columns would run (RoPE not fused; q = 0), `iters` times on the engine's stream cycling through the layers, timed
+ * with HIP events.  Returns the average launch duration in microseconds and the K/V bytes one launch reads (each
+ * visible key's fp16 K and V once per kv head; once per group for multi-query groups).  Clobbers the activation
+ * buffers (not the KV cache); call between forward passes only. */
+int sp_engine_time_attention(sp_engine *e, int32_t n, const sp_token *toks, int32_t iters, float *avg_us,
+                             uint64_t *bytes);
 
 /* Benchmark utility (no counterpart in the reference): fill slots [first_slot, first_slot + n) of sequence `seq`
  * in every layer's K and V with seeded pseudo-random fp16 values in [-scale, scale], standing in for a long prefill

@@ -56,6 +56,9 @@ SIGNATURES = {
     'sp_engine_sync': (c_int, [c_void_p]),
     'sp_engine_copy_ids': (c_int, [c_void_p, c_int32, c_void_p]),
     'sp_engine_last_path': (c_int, [c_void_p]),
+    'sp_engine_last_dispatches': (c_int, [c_void_p]),
+    'sp_engine_time_attention': (c_int, [c_void_p, c_int32, ctypes.POINTER(Token), c_int32, ctypes.POINTER(c_float),
+                                         ctypes.POINTER(c_uint64)]),
     'sp_engine_bytes': (c_int, [c_void_p, ctypes.POINTER(c_uint64), ctypes.POINTER(c_uint64)]),
     'sp_engine_kv_fill': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_uint64, c_float]),
     'sp_engine_time_gemv': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(c_float),

@@ -401,6 +401,13 @@ struct sp_engine {
     int *d_move = nullptr;
 
     std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;
+    std::map<std::tuple<int, int, int>, int> graph_kernels;     // kernel nodes of each recorded graph
+    int last_dispatches = -1;                                   // kernels of the last graph replay (-1: eager call)
+    void drop_graphs() {
+        for (auto &kv : graphs) (void)hipGraphExecDestroy(kv.second);
+        graphs.clear();
+        graph_kernels.clear();
+    }
 
     // persistent decode kernel state (built on first use, rebuilt when the KV pool moves)
     struct Persistent {
@@ -437,11 +444,13 @@ struct sp_engine {
     void free_all();
     void alloc_activations();
     void step(int n, int flags, const AttnPlan &ap);
+    void launch_attention(int l, int n, const AttnPlan &ap, int mtp, hipStream_t st);
+    void check_columns(int n, const sp_token *toks, bool feed) const;
+    void upload(int n, const sp_token *toks, const AttnPlan &ap);
 };
 
 void sp_engine::free_all() {
-    for (auto &kv : graphs) (void)hipGraphExecDestroy(kv.second);
-    graphs.clear();
+    drop_graphs();
     for (auto &l : layers) {
         l.qkv.release(); l.o.release(); l.gate_up.release(); l.down.release();
         dev_free(l.qkv_b); dev_free(l.in_norm); dev_free(l.post_norm);
@@ -777,6 +786,56 @@ bool sp_engine::persistent_step(const sp_token &t, int flags, float *logits_dev,
     return true;
 }
 
+// Every column must name a token (unless fed from the last argmax), a reserved sequence and slot, and a visible range
+// the ring holds; a tree block lies inside the ring.
+void sp_engine::check_columns(int n, const sp_token *toks, bool feed) const {
+    for (int i = 0; i < n; ++i) {
+        const sp_token &t = toks[i];
+        require(feed || (t.token >= 0 && t.token < d.vocab), SP_EINVAL, "token id out of range");
+        require(t.seq >= 0 && t.seq < n_seq, SP_EINVAL, "sequence index out of range");
+        require(t.slot >= 0 && t.slot < n_slots, SP_EINVAL, "slot out of range");
+        require(t.pos >= 0, SP_EINVAL, "position must be non-negative");
+        require(t.ctx_lo >= 0, SP_EINVAL, "ctx_lo must be non-negative");
+        const int nlin = t.ctx_hi >= t.ctx_lo ? t.ctx_hi - t.ctx_lo + 1 : 0;
+        require(nlin <= n_slots, SP_ECAPACITY, "visible range exceeds the KV slots");
+        require(t.tree_count >= 0 && t.tree_count <= 64, SP_EINVAL, "tree_count must be in [0, 64]");
+        require(t.tree_count == 0 || (t.tree_base >= 0 && t.tree_base < n_slots), SP_EINVAL, "tree_base out of range");
+        require(nlin + t.tree_count >= 1, SP_EINVAL, "a column must see at least one key");
+    }
+}
+
+// The call's column descriptors, attention groups and chunk counts go up in one copy from the pinned staging buffer.
+void sp_engine::upload(int n, const sp_token *toks, const AttnPlan &ap) {
+    HIPCHK(hipEventSynchronize(upload_done));       // the previous call's copy has read the staging buffer
+    const size_t go = (char *)dgroups - d_upload, co = (char *)dcolnc - d_upload;
+    std::memcpy(h_upload, toks, n * sizeof(sp_token));
+    std::memcpy(h_upload + go, ap.groups.data(), ap.ngroups * sizeof(AttnGroup));
+    std::memcpy(h_upload + co, ap.colnc.data(), n * sizeof(int));
+    HIPCHK(hipMemcpyAsync(d_upload, h_upload, co + n * sizeof(int), hipMemcpyHostToDevice, stream));
+    HIPCHK(hipEventRecord(upload_done, stream));
+}
+
+// The attention kernel of layer l for a plan without the fused RoPE: multi-query groups, MFMA decode splits (written
+// straight to `attn` when one split covers every column) or 64-key chunks, reading q from the q buffer.
+void sp_engine::launch_attention(int l, int n, const AttnPlan &ap, int mtp, hipStream_t st) {
+    const int NH = d.n_heads, NKV = d.n_kv_heads, HD = d.head_dim, G = NH / NKV, nchunk = ap.nchunk;
+    const float scale = 1.0f / std::sqrt((float)HD);
+    if (ap.mq) {
+        AttnMqArgs am{q, kc[l], vc[l], dtoks, dgroups, NH, NKV, HD, n_slots, nchunk, scale, attn_part, ap.splits};
+        dim3 agrid(nchunk, NKV, ap.ngroups * ap.splits);
+        if (HD == 64) launch_attn_mq_hd<64>(G, agrid, st, am);
+        else launch_attn_mq_hd<128>(G, agrid, st, am);
+    } else if (ap.dec) {
+        AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, scale, attn_part};
+        launch_attn_dec(HD, dim3(NKV, n, nchunk), st, aa, attn, NH * HD, ap.dec_direct ? 1 : 0, mtp);
+    } else {
+        AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, scale, attn_part};
+        dim3 agrid(nchunk, NKV, n);
+        if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
+        else launch_attn_hd<128>(G, agrid, st, aa);
+    }
+}
+
 void sp_engine::step(int n, int flags, const AttnPlan &ap) {
     const int nchunk = ap.nchunk;
     const int H = d.hidden, I = d.intermediate, NH = d.n_heads, NKV = d.n_kv_heads, HD = d.head_dim;
@@ -832,20 +891,8 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
             dim3 agrid(nchunk, NKV, n);
             if (HD == 64) launch_attn_rope_hd<64>(G, agrid, st, aa, ra, sq);
             else launch_attn_rope_hd<128>(G, agrid, st, aa, ra, sq);
-        } else if (ap.mq) {
-            AttnMqArgs am{q, kc[l], vc[l], dtoks, dgroups, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD),
-                          attn_part, ap.splits};
-            dim3 agrid(nchunk, NKV, ap.ngroups * ap.splits);
-            if (HD == 64) launch_attn_mq_hd<64>(G, agrid, st, am);
-            else launch_attn_mq_hd<128>(G, agrid, st, am);
-        } else if (ap.dec) {
-            AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
-            launch_attn_dec(HD, dim3(NKV, n, nchunk), st, aa, attn, NH * HD, ap.dec_direct ? 1 : 0, mtp);
         } else {
-            AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, 1.0f / std::sqrt((float)HD), attn_part};
-            dim3 agrid(nchunk, NKV, n);
-            if (HD == 64) launch_attn_hd<64>(G, agrid, st, aa);
-            else launch_attn_hd<128>(G, agrid, st, aa);
+            launch_attention(l, n, ap, mtp, st);
         }
         if (fuse && !ap.dec_direct) {
             ProArgs pc{};
@@ -949,8 +996,7 @@ int sp_engine_set_stream(sp_engine *e, void *s) {
     return guarded(e, [&] {
         HIPCHK(hipStreamSynchronize(e->stream));
         if (e->own_stream) HIPCHK(hipStreamDestroy(e->stream));
-        for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
-        e->graphs.clear();
+        e->drop_graphs();
         e->stream = (hipStream_t)s;
         e->own_stream = false;
     });
@@ -992,8 +1038,7 @@ int sp_engine_load(sp_engine *e, int32_t kind, int32_t layer, int32_t fmt, int32
             case SP_T_DOWN: mat(e->layers[layer].down, d.hidden, d.intermediate, false); break;
             default: throw Fail{SP_EINVAL, "unknown tensor kind"};
         }
-        for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
-        e->graphs.clear();
+        e->drop_graphs();
     });
 }
 
@@ -1038,8 +1083,7 @@ void install_pool(sp_engine *e, int n_seq, int n_slots, std::vector<f16 *> &k, s
     e->max_nchunk = (n_slots + 64 + ATT_CH - 1) / ATT_CH;
     e->attn_part = dev_alloc<float>((size_t)e->maxT * e->d.n_heads * e->max_nchunk * part_floats(e->d.head_dim));
     e->n_seq = n_seq; e->n_slots = n_slots;
-    for (auto &kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
-    e->graphs.clear();
+    e->drop_graphs();
     e->pk.tried = false;
 }
 }  // namespace
@@ -1131,19 +1175,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         const bool feed = flags & SP_F_FEED;
         require(!feed || n <= e->argmax_cols, SP_ESTATE,
                 "SP_F_FEED needs a previous SP_F_ARGMAX call over at least as many columns");
-        for (int i = 0; i < n; ++i) {
-            const sp_token &t = toks[i];
-            require(feed || (t.token >= 0 && t.token < d.vocab), SP_EINVAL, "token id out of range");
-            require(t.seq >= 0 && t.seq < e->n_seq, SP_EINVAL, "sequence index out of range");
-            require(t.slot >= 0 && t.slot < e->n_slots, SP_EINVAL, "slot out of range");
-            require(t.pos >= 0, SP_EINVAL, "position must be non-negative");
-            require(t.ctx_lo >= 0, SP_EINVAL, "ctx_lo must be non-negative");
-            const int nlin = t.ctx_hi >= t.ctx_lo ? t.ctx_hi - t.ctx_lo + 1 : 0;
-            require(nlin <= e->n_slots, SP_ECAPACITY, "visible range exceeds the KV slots");
-            require(t.tree_count >= 0 && t.tree_count <= 64, SP_EINVAL, "tree_count must be in [0, 64]");
-            require(t.tree_count == 0 || (t.tree_base >= 0 && t.tree_base < e->n_slots), SP_EINVAL, "tree_base out of range");
-            require(nlin + t.tree_count >= 1, SP_EINVAL, "a column must see at least one key");
-        }
+        e->check_columns(n, toks, feed);
         const bool use_graph = flags & SP_F_GRAPH;
         const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX | SP_F_UNFUSED | SP_F_FEED);
         if (n == 1 && (flags & SP_F_PERSISTENT) && !feed) {
@@ -1154,15 +1186,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         }
         e->last_path = 0;
         const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
-        {
-            HIPCHK(hipEventSynchronize(e->upload_done));       // the previous call's copy has read the staging buffer
-            const size_t go = (char *)e->dgroups - e->d_upload, co = (char *)e->dcolnc - e->d_upload;
-            std::memcpy(e->h_upload, toks, n * sizeof(sp_token));
-            std::memcpy(e->h_upload + go, ap.groups.data(), ap.ngroups * sizeof(AttnGroup));
-            std::memcpy(e->h_upload + co, ap.colnc.data(), n * sizeof(int));
-            HIPCHK(hipMemcpyAsync(e->d_upload, e->h_upload, co + n * sizeof(int), hipMemcpyHostToDevice, e->stream));
-            HIPCHK(hipEventRecord(e->upload_done, e->stream));
-        }
+        e->upload(n, toks, ap);
         if (use_graph) {
             auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? (ap.dec_direct ? -3 : -2) : (ap.rope_fused ? -4 : -1)));
             auto it = e->graphs.find(key);
@@ -1183,14 +1207,27 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
                 hipError_t ce = hipStreamEndCapture(e->stream, &g);
                 e->stream = run_stream;
                 HIPCHK(ce);
+                size_t nn = 0;
+                HIPCHK(hipGraphGetNodes(g, nullptr, &nn));
+                std::vector<hipGraphNode_t> nodes(nn);
+                if (nn) HIPCHK(hipGraphGetNodes(g, nodes.data(), &nn));
+                int kernels = 0;
+                for (auto nd : nodes) {
+                    hipGraphNodeType ty;
+                    HIPCHK(hipGraphNodeGetType(nd, &ty));
+                    kernels += ty == hipGraphNodeTypeKernel;
+                }
                 hipGraphExec_t ge;
                 HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
                 (void)hipGraphDestroy(g);
                 it = e->graphs.emplace(key, ge).first;
+                e->graph_kernels[key] = kernels;
             }
             HIPCHK(hipGraphLaunch(it->second, e->stream));
+            e->last_dispatches = e->graph_kernels[key];
         } else {
             e->step(n, sflags, ap);
+            e->last_dispatches = -1;
         }
         if (sflags & SP_F_ARGMAX) e->argmax_cols = n;
         if (logits_dev && (flags & SP_F_LOGITS))
@@ -1205,6 +1242,8 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
 }
 
 int sp_engine_last_path(const sp_engine *e) { return e ? e->last_path : -1; }
+
+int sp_engine_last_dispatches(const sp_engine *e) { return e ? e->last_dispatches : -1; }
 
 #ifdef SP_GEMV_TUNE
 void sp_debug_gemv_plan(int r, int nw, int s) { g_tune[0] = r; g_tune[1] = nw; g_tune[2] = s; }
@@ -1317,6 +1356,48 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
         HIPCHK(hipGetLastError());
         *avg_us = ms * 1000.f / iters;
         *bytes = m->bytes;
+    });
+}
+
+int sp_engine_time_attention(sp_engine *e, int32_t n, const sp_token *toks, int32_t iters, float *avg_us,
+                             uint64_t *bytes) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        const sp_model_desc &d = e->d;
+        require(avg_us && bytes && toks, SP_EINVAL, "NULL argument");
+        require(n >= 1 && n <= e->maxT && iters >= 1, SP_EINVAL, "n must be in [1, max_tokens], iters >= 1");
+        require(e->n_seq > 0, SP_ESTATE, "KV cache not reserved");
+        e->check_columns(n, toks, true);
+        sp_engine::AttnPlan ap = e->plan_attention(n, toks, false);
+        ap.rope_fused = false;
+        e->upload(n, toks, ap);
+        HIPCHK(hipMemsetAsync(e->q, 0, (size_t)e->maxT * d.n_heads * d.head_dim * sizeof(float), e->stream));
+        const int mtp = n > 1 ? (n + 15) / 16 : 0;
+        int cur = 0;
+        auto launch = [&] { e->launch_attention(cur, n, ap, mtp, e->stream); cur = (cur + 1) % d.n_layers; };
+        hipEvent_t a, b;
+        HIPCHK(hipEventCreate(&a));
+        HIPCHK(hipEventCreate(&b));
+        launch();
+        HIPCHK(hipEventRecord(a, e->stream));
+        for (int i = 0; i < iters; ++i) launch();
+        HIPCHK(hipEventRecord(b, e->stream));
+        HIPCHK(hipEventSynchronize(b));
+        float ms = 0.f;
+        HIPCHK(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        HIPCHK(hipGetLastError());
+        uint64_t keys = 0;
+        for (int i = 0; i < n; ++i)
+            keys += (uint64_t)(toks[i].ctx_hi >= toks[i].ctx_lo ? toks[i].ctx_hi - toks[i].ctx_lo + 1 : 0) + toks[i].tree_count;
+        // every visible key's K and V (fp16) of its kv head; a multi-query group reads its shared keys once
+        if (ap.mq) {
+            keys = 0;
+            for (const AttnGroup &g : ap.groups) keys += (uint64_t)g.nlin + g.tree_count;
+        }
+        *avg_us = ms * 1000.f / iters;
+        *bytes = keys * d.n_kv_heads * d.head_dim * 2 * 2;
     });
 }
 

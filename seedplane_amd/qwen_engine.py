@@ -202,6 +202,22 @@ class Qwen2Engine:
                    self.h)
         return us.value, nb.value
 
+    def time_attention(self, caches, iters=100):
+        """Average duration (us) and K/V bytes of one launch of the attention kernel a decode step of `caches` (one
+        column each, at their current lengths) runs, timed with HIP events on the engine's stream.  Clobbers
+        activation buffers."""
+        cols = [self._column(0, c, c.length, c.length) for c in caches]
+        arr = (_lib.Token * len(cols))(*[_lib.Token(*c) for c in cols])
+        us, nb = ctypes.c_float(), ctypes.c_uint64()
+        _lib.check(self.lib.sp_engine_time_attention(self.h, len(cols), arr, iters, ctypes.byref(us), ctypes.byref(nb)),
+                   self.h)
+        return us.value, nb.value
+
+    @property
+    def last_dispatches(self):
+        """Kernels the last engine call launched when it replayed a graph (-1 after an eager call)."""
+        return int(self.lib.sp_engine_last_dispatches(self.h))
+
     def fill_cache(self, cache, n_positions, seed=0, scale=1.0):
         """Benchmark stand-in for a long prefill: positions [0, n_positions) of `cache` get seeded pseudo-random K/V
         (the decode step reads the same bytes whatever the values); cache.length = n_positions."""
