@@ -51,6 +51,20 @@ __device__ __forceinline__ f16x8 q8_unpack8(uint32_t d0, uint32_t d1) {
     f16x2 c = q8_pair(d1, 0x04010400u), d = q8_pair(d1, 0x04030402u);
     return (f16x8){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
+// The same codes offset by 1152 (1024 + 128): fp16 1152 + c, exact, without the subtraction.  A GEMV that takes these
+// removes 1152 * sum(x) from the fp32 MFMA result instead (one correction per quant block, not per weight).
+__device__ __forceinline__ f16x8 q8_biased8(uint32_t d0, uint32_t d1) {
+    d0 ^= 0x80808080u; d1 ^= 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, d0, 0x04010400u), b = __builtin_amdgcn_perm(0x64646464u, d0, 0x04030402u);
+    const uint32_t c = __builtin_amdgcn_perm(0x64646464u, d1, 0x04010400u), d = __builtin_amdgcn_perm(0x64646464u, d1, 0x04030402u);
+    return __builtin_bit_cast(f16x8, (u32x4){a, b, c, d});
+}
+// 8 uint4 codes of one dword -> 8 fp16 1024 + c (exact; see q4_unpack8 for the nibble order).
+__device__ __forceinline__ f16x8 q4_biased8(uint32_t v) {
+    const uint32_t a = (v & 0x000F000Fu) | 0x64006400u, b = ((v >> 4) & 0x000F000Fu) | 0x64006400u;
+    const uint32_t c = ((v >> 8) & 0x000F000Fu) | 0x64006400u, d = ((v >> 12) & 0x000F000Fu) | 0x64006400u;
+    return __builtin_bit_cast(f16x8, (u32x4){a, b, c, d});
+}
 // 8 uint4 codes of one dword -> 8 fp16 in k order.  The packer stores k-order codes c0..c7 at nibble positions
 // 0,4,1,5,2,6,3,7 so that (v >> 4j) & 0x000F000F yields the pair (c_{2j}, c_{2j+1}) in the two fp16 halves; OR-ing
 // 0x6400 gives 1024 + c exactly, and subtracting 1024 leaves c.

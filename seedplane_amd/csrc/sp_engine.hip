@@ -22,6 +22,7 @@
 #include "sp_attn.h"
 #include "sp_decode.h"
 #include "sp_gemv.h"
+#include "sp_gemv1.h"
 #include "sp_pack.h"
 #include "sp_sample.h"
 
@@ -100,6 +101,8 @@ struct GemvPlan {
 #ifdef SP_GEMV_TUNE
 // plan override for launch-shape sweeps (row groups per wave, waves per block, slices); 0 keeps the heuristic
 int g_tune[3] = {0, 0, 0};
+// single-column step plans: qkv slices, qkv waves, down slices, down waves, gate_up waves (0 keeps the defaults)
+int g_tune_one[5] = {0, 0, 0, 0, 0};
 #endif
 
 // Launch shape of one GEMV, from launch-shape sweeps (row groups per wave x waves x slices) of the Qwen2-0.5B fp16,
@@ -148,7 +151,10 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
 template <int FMT, int RG, int R>
 void launch_gemv_r(int mt, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
     switch (mt) {
-        case 1: hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R>), grid, block, smem, st, a); break;
+        case 1:
+            if (a.m == 1) hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R, true>), grid, block, smem, st, a);
+            else hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R>), grid, block, smem, st, a);
+            break;
         case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, RG, R>), grid, block, smem, st, a); break;
         case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, RG, R>), grid, block, smem, st, a); break;
         default: hipLaunchKernelGGL((k_gemv<FMT, 4, RG, R>), grid, block, smem, st, a); break;
@@ -198,6 +204,35 @@ bool gemv_pro_ok(const DevMat &m, int pro, int H, int HD, int slices = 0, int wa
     return true;
 }
 
+// One column through k_gemv1: T = the wave's k-tile count (template), NW waves, the prologue if any.
+template <int FMT, int RG, int PRO>
+bool launch_gemv1_t(int T, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a, const ProArgs &pa) {
+    switch (T) {
+        case 1: hipLaunchKernelGGL((k_gemv1<FMT, RG, 1, PRO>), grid, block, smem, st, a, pa); return true;
+        case 2: hipLaunchKernelGGL((k_gemv1<FMT, RG, 2, PRO>), grid, block, smem, st, a, pa); return true;
+        case 3: hipLaunchKernelGGL((k_gemv1<FMT, RG, 3, PRO>), grid, block, smem, st, a, pa); return true;
+        case 4: hipLaunchKernelGGL((k_gemv1<FMT, RG, 4, PRO>), grid, block, smem, st, a, pa); return true;
+        default: break;
+    }
+    if constexpr (PRO == PRO_NONE) {
+        switch (T) {
+            case 5: hipLaunchKernelGGL((k_gemv1<FMT, RG, 5, PRO>), grid, block, smem, st, a, pa); return true;
+            case 6: hipLaunchKernelGGL((k_gemv1<FMT, RG, 6, PRO>), grid, block, smem, st, a, pa); return true;
+            case 7: case 8: hipLaunchKernelGGL((k_gemv1<FMT, RG, 8, PRO>), grid, block, smem, st, a, pa); return true;
+            default: break;
+        }
+    }
+    return false;
+}
+template <int FMT>
+bool launch_gemv1_fmt(bool paired, int pro, int T, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a,
+                      const ProArgs &pa) {
+    if (paired) return pro == PRO_NONE && launch_gemv1_t<FMT, 2, PRO_NONE>(T, grid, block, smem, st, a, pa);
+    if (pro == PRO_NORM) return launch_gemv1_t<FMT, 1, PRO_NORM>(T, grid, block, smem, st, a, pa);
+    if (pro == PRO_COMB) return launch_gemv1_t<FMT, 1, PRO_COMB>(T, grid, block, smem, st, a, pa);
+    return launch_gemv1_t<FMT, 1, PRO_NONE>(T, grid, block, smem, st, a, pa);
+}
+
 // Launches y = W x for mcols columns.  With `part` given (and a matrix that is not the SwiGLU pair) the plan may
 // split K: the kernel then writes raw slices to part[s][m][ldo] and the return value is the slice count that the
 // consumer must add (plus the bias, for EPI_STORE); otherwise the epilogue is applied and 0 is returned.  With a
@@ -220,6 +255,33 @@ int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, floa
     require(xmtp == 0 || xmtp == mt, SP_EINVAL, "gemv input layout does not match the column count");
     a.xmtp = xmtp; a.omtp = omtp;
     if (p.s > 1) { a.epi = EPI_PART; a.out_f32 = part; a.bias = nullptr; }
+    // one column of a layer matrix: k_gemv1 (row groups one per block; the prologues need their fixed block sizes)
+    if (mcols == 1 && xmtp == 0 && p.units < 2048 && m.rows_pad / 16 / p.rg == p.units) {
+        int nw = pro == PRO_NONE ? p.nw : pro_threads(pro) / 64;
+        // the SwiGLU pair: 8 waves of <= 3 k-tiles each keep the most loads in flight (launch-shape sweep)
+        if (m.paired && waves == 0) {
+            nw = std::min(p.kslice, 8);
+#ifdef SP_GEMV_TUNE
+            if (g_tune_one[4] > 0) nw = std::min(p.kslice, g_tune_one[4]);
+            if (g_tune[1] > 0) nw = std::min(g_tune[1], 16);
+#endif
+        }
+        const int T = (p.kslice + nw - 1) / nw;
+        const int kt = m.fmt == 1 ? 32 : (m.fmt == 2 ? 64 : 128);
+        const int prof = pro == PRO_NONE ? 0 : pro_scratch_floats(pro, pa->H, pa->HD);
+        const size_t smem = g1_smem_bytes(p.kslice, kt, nw, p.rg, prof);
+        const dim3 grid1(p.units, p.s), block1(64 * nw);
+        const ProArgs pz = pro == PRO_NONE ? ProArgs{} : *pa;
+        if (smem <= GEMV_MAX_LDS) {
+            bool ok = false;
+            switch (m.fmt) {
+                case 1: ok = launch_gemv1_fmt<1>(m.paired, pro, T, grid1, block1, smem, st, a, pz); break;
+                case 2: ok = launch_gemv1_fmt<2>(m.paired, pro, T, grid1, block1, smem, st, a, pz); break;
+                default: ok = launch_gemv1_fmt<3>(m.paired, pro, T, grid1, block1, smem, st, a, pz); break;
+            }
+            if (ok) return p.s > 1 ? p.s : 0;
+        }
+    }
     dim3 grid(p.units / p.r, p.s), block(64 * p.nw);
     if (pro != PRO_NONE) {
         require(p.r == 1 && p.nw <= pro_threads(pro) / 64, SP_EINVAL, "gemv prologue plan out of range");
@@ -852,17 +914,23 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
     const int mtp = n > 1 ? (n + 15) / 16 : 0;
     int pend = 0;     // residual slices of a split-K o / down GEMV waiting in gpart (added by the next RMSNorm)
     // One column: the input RMSNorm runs as the prologue of the qkv GEMV and the attention combine as the prologue of
-    // o_proj (two launches fewer per layer); qkv and the down projection run in ONE_SLICES k-slices, so the prologue
-    // adds few pending slices (launch-shape sweeps: as fast as the many-slice plans with 8 / 16 waves per block).
-    // The prologue writes the updated residual to the other one of x / x2 (its blocks still read the first), so the
+    // o_proj (two launches fewer per layer); qkv and the down projection run in the k-slices below, which the next
+    // norm adds.  The prologue writes the updated residual to the other one of x / x2 (its blocks still read the first), so the
     // residual changes buffer at every layer; the qkv slices go to gpart2 while the blocks still read the down slices
     // in gpart.  SP_F_UNFUSED keeps the plans and runs the norm and the combine as kernels of their own.
-    constexpr int ONE_SLICES = 2, ONE_QKV_WAVES = 8, ONE_DOWN_WAVES = 16;
-    const bool one = n == 1 && !layers.empty() && gemv_pro_ok(layers[0].qkv, PRO_NORM, H, HD, ONE_SLICES, ONE_QKV_WAVES) &&
+    // launch-shape sweep of whole bs1 steps (1.5B int8): qkv in 2 slices of 8 waves, down in 8 slices of 8 waves
+    int one_qs = 2, one_qw = 8, one_ds = 8, one_dw = 8;
+#ifdef SP_GEMV_TUNE
+    if (g_tune_one[0] > 0) one_qs = g_tune_one[0];
+    if (g_tune_one[1] > 0) one_qw = g_tune_one[1];
+    if (g_tune_one[2] > 0) one_ds = g_tune_one[2];
+    if (g_tune_one[3] > 0) one_dw = g_tune_one[3];
+#endif
+    const bool one = n == 1 && !layers.empty() && gemv_pro_ok(layers[0].qkv, PRO_NORM, H, HD, one_qs, one_qw) &&
                      gemv_pro_ok(layers[0].o, PRO_COMB, H, HD);
     const bool fuse = one && !(flags & SP_F_UNFUSED);
-    const int qkv_s = one ? ONE_SLICES : 0, qkv_w = one ? ONE_QKV_WAVES : 0;
-    const int down_s = one ? ONE_SLICES : 0, down_w = one ? ONE_DOWN_WAVES : 0;
+    const int qkv_s = one ? one_qs : 0, qkv_w = one ? one_qw : 0;
+    const int down_s = one ? one_ds : 0, down_w = one ? one_dw : 0;
     float *const qpart = fuse ? gpart2 : gpart;
     float *res = x;                             // residual at the start of the layer
     for (int l = 0; l < d.n_layers; ++l) {
@@ -1247,6 +1315,9 @@ int sp_engine_last_dispatches(const sp_engine *e) { return e ? e->last_dispatche
 
 #ifdef SP_GEMV_TUNE
 void sp_debug_gemv_plan(int r, int nw, int s) { g_tune[0] = r; g_tune[1] = nw; g_tune[2] = s; }
+void sp_debug_one_plan(int qs, int qw, int ds, int dw, int gw) {
+    g_tune_one[0] = qs; g_tune_one[1] = qw; g_tune_one[2] = ds; g_tune_one[3] = dw; g_tune_one[4] = gw;
+}
 void sp_debug_attn_plan(int nwv, int sub) { g_tune_attn[0] = nwv; g_tune_attn[1] = sub; }
 #endif
 

@@ -55,13 +55,30 @@ __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
         return q4_unpack8(t[s]);
     }
 }
+// The codes of step s offset by QBIAS<FMT> (exact fp16; Q8 and Q4 only).
+template <int FMT> struct QBias { static constexpr float V = FMT == 2 ? 1152.f : 1024.f; };
+template <int FMT>
+__device__ __forceinline__ f16x8 biased_step(const u32x4 &t, int s) {
+    if constexpr (FMT == 2) return s == 0 ? q8_biased8(t[0], t[1]) : q8_biased8(t[2], t[3]);
+    else return q4_biased8(t[s]);
+}
 
 // Threads per block: single-column-tile variants with one unit per block use up to 16 waves (128 VGPRs each), those
 // with two units up to 4, wider ones up to 8 (each wave may then hold up to 256 VGPRs: the weight tiles and
 // activation fragments of a whole batch stay in registers).
 // TB = k-tiles per wave whose loads are in flight together.
-template <int MT, int R> struct GemvLimits { static constexpr int MAX_THREADS = MT == 1 ? (R == 1 ? 1024 : 256) : 512; };
-template <int FMT, int MT> struct GemvBatch { static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : 4) : 2; };
+#ifndef SP_GU_TB
+#define SP_GU_TB 4
+#endif
+#ifndef SP_GU_THREADS
+#define SP_GU_THREADS 1024
+#endif
+template <int MT, int RG, int R> struct GemvLimits {
+    static constexpr int MAX_THREADS = MT == 1 ? (R == 1 ? (RG == 2 ? SP_GU_THREADS : 1024) : 256) : 512;
+};
+template <int FMT, int MT, int RG> struct GemvBatch {
+    static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : (RG == 2 ? SP_GU_TB : 4)) : 2;
+};
 
 // Lane holds D[m = mt*16 + 4g + j][n = unit*16 + r], j < 4.  Operands the epilogue reads (bias, the residual) are
 // loaded from clamped addresses before any store, so their loads are in flight together.
@@ -257,10 +274,14 @@ __device__ __forceinline__ void pro_comb(const ProArgs &p, f16 *act, int klo, in
     }
 }
 
-template <int FMT, int MT, int RG, int R, int PRO>
+// MT == 1 (up to 16 columns) with Q8 / Q4 codes: the MFMA takes the codes offset by QBias (no per-weight subtraction)
+// and each quant block's result is corrected by QBias (+ the Q4 zero) times the block's activation sums, one fp32 FMA
+// per output; ONE (a single column) keeps only output component 0 (the other rows of the MFMA A operand are zero).
+// Every column gets the same operations in either case, so one column and a batch give the same bits.
+template <int FMT, int MT, int RG, int R, int PRO, bool ONE = false>
 __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, unsigned char *smem_raw) {
     constexpr int KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
-    constexpr int TB = GemvBatch<FMT, MT>::TB;
+    constexpr int TB = PRO == PRO_NONE ? GemvBatch<FMT, MT, RG>::TB : GemvBatch<FMT, MT, 1>::TB;
     constexpr int NR = R * RG;                 // row groups per wave
     const int NW = PRO == PRO_NONE ? (int)(blockDim.x >> 6) : a.nwk;   // waves taking k-tiles
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -352,9 +373,31 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
 #pragma unroll
             for (int s = 0; s < ST; ++s) {
                 f32x4 xs[MT];
-                if constexpr (FMT == 3) {
+                if constexpr (FMT == 3 || (FMT == 2 && MT == 1)) {
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) xs[mt] = mfma16(xa[t][mt][s], ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                }
+                if constexpr (FMT != 1 && MT == 1) {
+                    // biased codes: acc_j += scale * (mfma(x, code + bias)_j - (bias + zero) * sum(x)_j)
+                    constexpr int NJ = ONE ? 1 : 4;
+#pragma unroll
+                    for (int i = 0; i < NR; ++i) {
+                        const f32x4 dd = mfma16(xa[t][0][s], biased_step<FMT>(wt[t][i], s), (f32x4){0.f, 0.f, 0.f, 0.f});
+                        float scale, off;
+                        if constexpr (FMT == 2) {
+                            const uint32_t d = sq8[t][i];
+                            scale = (float)__builtin_bit_cast(f16, (uint16_t)(s == 0 ? (d & 0xffffu) : (d >> 16)));
+                            off = QBias<FMT>::V;
+                        } else {
+                            uint32_t d;
+                            if (s == 0) d = sq4[t][i].x; else if (s == 1) d = sq4[t][i].y; else if (s == 2) d = sq4[t][i].z; else d = sq4[t][i].w;
+                            scale = (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
+                            off = QBias<FMT>::V + (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
+                        }
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j) acc[i][0][j] = fmaf(scale, fmaf(-off, xs[0][j], dd[j]), acc[i][0][j]);
+                    }
+                    continue;
                 }
 #pragma unroll
                 for (int i = 0; i < NR; ++i) {
@@ -417,15 +460,15 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
     }
 }
 
-template <int FMT, int MT, int RG, int R>
-__global__ void __launch_bounds__((GemvLimits<MT, R>::MAX_THREADS)) k_gemv(GemvArgs a) {
+template <int FMT, int MT, int RG, int R, bool ONE = false>
+__global__ void __launch_bounds__((GemvLimits<MT, RG, R>::MAX_THREADS)) k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    gemv_run<FMT, MT, RG, R, PRO_NONE>(a, ProArgs{}, smem_raw);
+    gemv_run<FMT, MT, RG, R, PRO_NONE, ONE>(a, ProArgs{}, smem_raw);
 }
 
 // One column with an activation prologue (PRO_NORM before qkv / gate_up, PRO_COMB before o_proj).
 template <int FMT, int RG, int PRO>
 __global__ void __launch_bounds__(pro_threads(PRO)) k_gemv_pro(GemvArgs a, ProArgs p) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    gemv_run<FMT, 1, RG, 1, PRO>(a, p, smem_raw);
+    gemv_run<FMT, 1, RG, 1, PRO, true>(a, p, smem_raw);
 }
