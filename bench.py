@@ -103,13 +103,12 @@ def verify_cost(eng, cfg, prefix=2048, n_branches=8, depth=4, reps=20):
     branches = [list(rng.integers(0, V, depth)) for _ in range(n_branches)]
     tree = flatten(int(rng.integers(0, V)), branches)
     verifier = TreeVerifier(eng)
-    p = torch.empty((tree.size, V), dtype=torch.float32, device=eng.device)
     for _ in range(3):
-        verifier.forward(cache, tree, logits_out=p, graph=True, ids=False)
+        p = verifier.forward(cache, tree, graph=True, ids=False)
     sync()
     t0 = time.perf_counter()
     for _ in range(reps):
-        verifier.forward(cache, tree, logits_out=p, graph=True, ids=False)   # logits for the acceptance walk
+        p = verifier.forward(cache, tree, graph=True, ids=False)   # logits for the acceptance walk (engine buffer)
     sync()
     t_verify = (time.perf_counter() - t0) / reps
     q = p + 0.3 * torch.randn_like(p)
@@ -124,7 +123,7 @@ def verify_cost(eng, cfg, prefix=2048, n_branches=8, depth=4, reps=20):
     # one speculative step as the loop runs it: the pass, then the acceptance walk (which waits for the GPU)
     t0 = time.perf_counter()
     for i in range(reps):
-        verifier.forward(cache, tree, logits_out=p, graph=True, ids=False)
+        p = verifier.forward(cache, tree, graph=True, ids=False)
         verifier.accept(p, q, tree, uniforms(3, i, 64), 0.8)
     sync()
     t_step = (time.perf_counter() - t0) / reps

@@ -505,7 +505,7 @@ struct sp_engine {
 
     void free_all();
     void alloc_activations();
-    void step(int n, int flags, const AttnPlan &ap);
+    void step(int n, int flags, const AttnPlan &ap, int l0, int l1);
     void launch_attention(int l, int n, const AttnPlan &ap, int mtp, hipStream_t st);
     void check_columns(int n, const sp_token *toks, bool feed) const;
     void upload(int n, const sp_token *toks, const AttnPlan &ap);
@@ -898,15 +898,20 @@ void sp_engine::launch_attention(int l, int n, const AttnPlan &ap, int mtp, hipS
     }
 }
 
-void sp_engine::step(int n, int flags, const AttnPlan &ap) {
+// Layers [l0, l1) of a forward call; the embedding when l0 == 0, the final norm / head / argmax when l1 == n_layers.
+// A call may run as several such parts in order (each captured as a graph of its own): the state crossing a part
+// boundary (which residual buffer holds the stream, how many split-K slices are pending) follows from the layer index.
+void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
     const int nchunk = ap.nchunk;
     const int H = d.hidden, I = d.intermediate, NH = d.n_heads, NKV = d.n_kv_heads, HD = d.head_dim;
     hipStream_t st = stream;
     const int *feed = (flags & SP_F_FEED) ? am_out : nullptr;   // tokens = the previous step's argmax ids
-    switch (embed.fmt) {
-        case 1: launch_embed<1>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
-        case 2: launch_embed<2>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
-        default: launch_embed<3>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
+    if (l0 == 0) {
+        switch (embed.fmt) {
+            case 1: launch_embed<1>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
+            case 2: launch_embed<2>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
+            default: launch_embed<3>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
+        }
     }
     const bool logits_on = flags & SP_F_LOGITS;
     const size_t ps = gpart_stride;
@@ -933,7 +938,13 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
     const int down_s = one ? one_ds : 0, down_w = one ? one_dw : 0;
     float *const qpart = fuse ? gpart2 : gpart;
     float *res = x;                             // residual at the start of the layer
-    for (int l = 0; l < d.n_layers; ++l) {
+    if (l0 > 0) {
+        // fused one-column steps alternate x / x2 every layer; the down GEMV of layer l0 - 1 left its slices pending
+        res = fuse && (l0 & 1) ? x2 : x;
+        const GemvPlan dp = plan_gemv(layers[0].down, (n + 15) / 16, true, down_s, down_w);
+        pend = dp.s > 1 ? dp.s : 0;
+    }
+    for (int l = l0; l < l1; ++l) {
         Layer &ly = layers[l];
         float *rmid = res;                      // residual after the input norm
         int sq;
@@ -980,7 +991,7 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap) {
                            down_s, down_w, mtp);
         res = rmid;
     }
-    if (logits_on) {
+    if (logits_on && l1 == d.n_layers) {
         const DevMat &hm = d.tied_head ? embed : head;
         launch_rmsnorm(n, res, H, gpart, pend, ps, final_norm, d.rms_eps, xn, st, mtp);
         launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, st, nullptr, 0, PRO_NONE, nullptr, 0, 0, mtp);
@@ -1256,45 +1267,56 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
         e->upload(n, toks, ap);
         if (use_graph) {
-            auto key = std::make_tuple(n, sflags, ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? (ap.dec_direct ? -3 : -2) : (ap.rope_fused ? -4 : -1)));
-            auto it = e->graphs.find(key);
-            if (it == e->graphs.end()) {
-                // record on the private stream (the caller's may be the null stream, which cannot capture)
-                hipGraph_t g;
-                hipStream_t run_stream = e->stream;
-                e->stream = e->capture_stream;
-                HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
-                try {
-                    e->step(n, sflags, ap);
-                } catch (...) {
-                    hipGraph_t dummy;
-                    (void)hipStreamEndCapture(e->stream, &dummy);
+            // The step runs as up to three graphs: a short first part (the embedding and layer 0) starts the GPU while
+            // the host is still submitting the rest, which a caller that waits for every call (tree verification)
+            // would otherwise see as idle GPU time.
+            const int L = d.n_layers;
+            const int cuts[4] = {0, std::min(1, L), std::min(5, L), L};
+            const int plan_code = ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? (ap.dec_direct ? -3 : -2) : (ap.rope_fused ? -4 : -1));
+            int total = 0;
+            for (int part = 0; part < 3; ++part) {
+                if (cuts[part] >= cuts[part + 1]) continue;      // empty (short models); the head ran in its part
+                auto key = std::make_tuple(n, sflags | (part << 8), plan_code);
+                auto it = e->graphs.find(key);
+                if (it == e->graphs.end()) {
+                    // record on the private stream (the caller's may be the null stream, which cannot capture)
+                    hipGraph_t g;
+                    hipStream_t run_stream = e->stream;
+                    e->stream = e->capture_stream;
+                    HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+                    try {
+                        e->step(n, sflags, ap, cuts[part], cuts[part + 1]);
+                    } catch (...) {
+                        hipGraph_t dummy;
+                        (void)hipStreamEndCapture(e->stream, &dummy);
+                        e->stream = run_stream;
+                        throw;
+                    }
+                    hipError_t ce = hipStreamEndCapture(e->stream, &g);
                     e->stream = run_stream;
-                    throw;
+                    HIPCHK(ce);
+                    size_t nn = 0;
+                    HIPCHK(hipGraphGetNodes(g, nullptr, &nn));
+                    std::vector<hipGraphNode_t> nodes(nn);
+                    if (nn) HIPCHK(hipGraphGetNodes(g, nodes.data(), &nn));
+                    int kernels = 0;
+                    for (auto nd : nodes) {
+                        hipGraphNodeType ty;
+                        HIPCHK(hipGraphNodeGetType(nd, &ty));
+                        kernels += ty == hipGraphNodeTypeKernel;
+                    }
+                    hipGraphExec_t ge;
+                    HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+                    (void)hipGraphDestroy(g);
+                    it = e->graphs.emplace(key, ge).first;
+                    e->graph_kernels[key] = kernels;
                 }
-                hipError_t ce = hipStreamEndCapture(e->stream, &g);
-                e->stream = run_stream;
-                HIPCHK(ce);
-                size_t nn = 0;
-                HIPCHK(hipGraphGetNodes(g, nullptr, &nn));
-                std::vector<hipGraphNode_t> nodes(nn);
-                if (nn) HIPCHK(hipGraphGetNodes(g, nodes.data(), &nn));
-                int kernels = 0;
-                for (auto nd : nodes) {
-                    hipGraphNodeType ty;
-                    HIPCHK(hipGraphNodeGetType(nd, &ty));
-                    kernels += ty == hipGraphNodeTypeKernel;
-                }
-                hipGraphExec_t ge;
-                HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
-                (void)hipGraphDestroy(g);
-                it = e->graphs.emplace(key, ge).first;
-                e->graph_kernels[key] = kernels;
+                HIPCHK(hipGraphLaunch(it->second, e->stream));
+                total += e->graph_kernels[key];
             }
-            HIPCHK(hipGraphLaunch(it->second, e->stream));
-            e->last_dispatches = e->graph_kernels[key];
+            e->last_dispatches = total;
         } else {
-            e->step(n, sflags, ap);
+            e->step(n, sflags, ap, 0, d.n_layers);
             e->last_dispatches = -1;
         }
         if (sflags & SP_F_ARGMAX) e->argmax_cols = n;

@@ -76,8 +76,11 @@ __device__ __forceinline__ f16x8 biased_step(const u32x4 &t, int s) {
 template <int MT, int RG, int R> struct GemvLimits {
     static constexpr int MAX_THREADS = MT == 1 ? (R == 1 ? (RG == 2 ? SP_GU_THREADS : 1024) : 256) : 512;
 };
+#ifndef SP_MT_TB
+#define SP_MT_TB 2
+#endif
 template <int FMT, int MT, int RG> struct GemvBatch {
-    static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : (RG == 2 ? SP_GU_TB : 4)) : 2;
+    static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : (RG == 2 ? SP_GU_TB : 4)) : SP_MT_TB;
 };
 
 // Lane holds D[m = mt*16 + 4g + j][n = unit*16 + r], j < 4.  Operands the epilogue reads (bias, the residual) are
@@ -380,9 +383,15 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                 if constexpr (FMT != 1 && MT == 1) {
                     // biased codes: acc_j += scale * (mfma(x, code + bias)_j - (bias + zero) * sum(x)_j)
                     constexpr int NJ = ONE ? 1 : 4;
+                    // the products of every row group first, then their corrections: no FMA waits on the MFMA it
+                    // follows
+                    f32x4 ddv[NR];
+#pragma unroll
+                    for (int i = 0; i < NR; ++i)
+                        ddv[i] = mfma16(xa[t][0][s], biased_step<FMT>(wt[t][i], s), (f32x4){0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                     for (int i = 0; i < NR; ++i) {
-                        const f32x4 dd = mfma16(xa[t][0][s], biased_step<FMT>(wt[t][i], s), (f32x4){0.f, 0.f, 0.f, 0.f});
+                        const f32x4 dd = ddv[i];
                         float scale, off;
                         if constexpr (FMT == 2) {
                             const uint32_t d = sq8[t][i];
@@ -408,19 +417,21 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                     } else if constexpr (FMT == 2) {
                         const uint32_t d = sq8[t][i];
                         const float scale = (float)__builtin_bit_cast(f16, (uint16_t)(s == 0 ? (d & 0xffffu) : (d >> 16)));
+                        f32x4 dd[MT];                  // every column tile's product first, then the scaling
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt)
-                            acc[i][mt] += scale * mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) acc[i][mt] += scale * dd[mt];
                     } else {
                         uint32_t d;
                         if (s == 0) d = sq4[t][i].x; else if (s == 1) d = sq4[t][i].y; else if (s == 2) d = sq4[t][i].z; else d = sq4[t][i].w;
                         const float scale = (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
                         const float zero = (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
+                        f32x4 dd[MT];
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) {
-                            const f32x4 dd = mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
-                            acc[i][mt] += scale * (dd - zero * xs[mt]);
-                        }
+                        for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) acc[i][mt] += scale * (dd[mt] - zero * xs[mt]);
                     }
                 }
             }

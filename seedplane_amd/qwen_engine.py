@@ -353,6 +353,19 @@ class Qwen2Engine:
         """1 if the last engine call ran the persistent single-column kernel, 0 for the kernel chain."""
         return int(self.lib.sp_engine_last_path(self.h))
 
+    def logits_view(self, n):
+        """The engine's own fp32 logits of the first n columns of the last SP_F_LOGITS call, as a [n, vocab] CUDA tensor
+        that shares the engine's memory (no copy; overwritten by the next forward call)."""
+        if not 1 <= n <= self.max_tokens:
+            raise ValueError('n must be in [1, max_tokens]')
+        ptr = ctypes.c_void_p()
+        _lib.check(self.lib.sp_engine_logits(self.h, ctypes.byref(ptr)), self.h)
+
+        class _Rows:
+            __cuda_array_interface__ = {'shape': (n, self.vocab), 'typestr': '<f4', 'data': (ptr.value, False),
+                                        'version': 3, 'strides': None}
+        return torch.as_tensor(_Rows(), device=self.device)
+
     def _scratch_logits(self, n):
         if self._logits_buf is None or self._logits_buf.shape[0] < n:
             self._logits_buf = torch.empty((self.max_tokens, self.vocab), dtype=torch.float32, device=self.device)

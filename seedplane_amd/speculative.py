@@ -279,7 +279,9 @@ class TreeVerifier:
         """One pass over every node: node i is written at cache position cache.length + i, RoPE position
         cache.length + depth[i], and attends to the cache before the root plus its own ancestors.  Returns the
         greedy ids per node; logits [nodes, vocab] go to `logits_out` when given.  With ids=False (acceptance
-        sampling needs the logits only) no argmax runs, the call does not wait for the GPU, and None is returned."""
+        sampling needs the logits only) no argmax runs and the call does not wait for the GPU: it returns the logits,
+        in `logits_out` or, without it, as a view of the engine's own logits buffer (no copy; valid until the
+        engine's next forward call)."""
         e = self.engine
         e._check_cache(cache)
         n = tree.size
@@ -302,9 +304,10 @@ class TreeVerifier:
         cols['tree_count'] = n
         cols['tree_mask'] = masks
         flags = self._lib.SP_F_LOGITS | (self._lib.SP_F_GRAPH if graph else 0)
-        if not ids and logits_out is None:
-            raise ValueError('ids=False needs logits_out')
-        return e.run(cols, flags, logits_out=logits_out, want_ids=ids)
+        out = e.run(cols, flags, logits_out=logits_out, want_ids=ids)
+        if ids:
+            return out
+        return logits_out if logits_out is not None else e.logits_view(n)
 
     def commit(self, cache, tree: FlatTree, path_nodes):
         """Keep the root and the accepted path nodes (in order) in the cache: their K/V move to consecutive slots
@@ -538,8 +541,7 @@ def speculative_generate(target, drafter, prompt, steps, n_branches=8, depth=4, 
         pending = committed[dcache.length:]
         branches, rows, used = drafter.propose(dcache, pending, n_branches, depth, temperature, u)
         tree = flatten(committed[-1], branches)
-        p = torch.empty((tree.size, target.vocab), dtype=torch.float32, device=target.device)
-        verifier.forward(tcache, tree, logits_out=p, ids=False)
+        p = verifier.forward(tcache, tree, ids=False)          # the target engine's own logits rows, no copy
         q = q_rows_for_tree(tree, rows, target.vocab, target.device)
         path, final, _, bonus = verifier.accept(p, q, tree, u[used:], temperature)
         acc_tokens = [tree.token[n] for n in path]

@@ -2,6 +2,8 @@
 logits and uniforms (every compared decision is checked to lie outside rounding of its threshold), tree-masked
 logits equal linear causal logits of each root path, greedy tree verification equals the reference verify_greedy,
 and the KV compaction keeps later decoding consistent."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -166,3 +168,21 @@ def test_linear_verify_with_rollback_matches_fresh_run(model):
                 break
         if all(top2_margin(r) > TOL * float(r.abs().max()) for r in ref.teacher_forced(prefix, greedy[:5])):
             assert emitted == exp_emitted, (draft, emitted, exp_emitted)
+
+
+def test_logits_only_pass_returns_the_engine_rows_without_a_copy(model):
+    # ids=False without logits_out hands back a view of the engine's own logits buffer; it equals the copied rows
+    cfg, w, eng, _ = model
+    prefix = random_prompt(9, cfg['vocab_size'], seed=14)
+    tree = flatten(prefix[-1], [[1, 2, 3], [1, 5], [7]])
+    verifier = TreeVerifier(eng)
+    cache = eng.new_cache(64)
+    eng.forward(prefix[:-1], cache)
+    copied = torch.empty((tree.size, cfg['vocab_size']), dtype=torch.float32, device=eng.device)
+    verifier.forward(cache, tree, logits_out=copied)
+    view = verifier.forward(cache, tree, ids=False)
+    assert view.shape == copied.shape and view.dtype == torch.float32
+    ptr = ctypes.c_void_p()
+    _lib.check(eng.lib.sp_engine_logits(eng.h, ctypes.byref(ptr)), eng.h)
+    assert view.data_ptr() == ptr.value
+    assert torch.equal(view, copied)
