@@ -179,7 +179,14 @@ class NativeEngine:
         return self._cache
 
     def _stream(self, ids, reset, sampling):
-        """Append `ids` to the session and generate (qwen_vk.cpp:589-613)."""
+        """The text pieces of _events (non-empty ones only)."""
+        for _, piece in self._events(ids, reset, sampling):
+            if piece:
+                yield piece
+
+    def _events(self, ids, reset, sampling):
+        """Append `ids` to the session and generate (qwen_vk.cpp:589-613), yielding (token, text piece) per generated
+        token (a stop token's piece is empty) and finally (-1, rest) when the incremental detokenizer held text back."""
         import torch
         self._live()
         if reset:
@@ -227,8 +234,7 @@ class NativeEngine:
                 self.last_tokens.append(int(t))
                 is_stop = int(t) in stop
                 piece = '' if is_stop else dec.push(t)
-                if piece:
-                    yield piece
+                yield int(t), piece
                 if is_stop:
                     res['reason'] = 'stop'
                     break
@@ -248,7 +254,7 @@ class NativeEngine:
             res['reason'] = 'context'
         rest = dec.flush()
         if rest:
-            yield rest
+            yield -1, rest
         torch.cuda.synchronize(eng.device)
         res['decode_s'] = time.perf_counter() - t0
         res['decode_tok_s'] = res['generated'] / max(res['decode_s'], 1e-9)
@@ -269,6 +275,20 @@ class NativeEngine:
         if ids is None:
             ids = self._need_tok().encode(text or '', add_special_tokens=False).ids
         yield from self._stream(list(ids), reset, sampling)
+
+    def chat_events(self, content, system=None, reset=False, **sampling):
+        """chat() as (token, text piece) events (the wire records of the --serve protocol)."""
+        tok = self._need_tok()
+        if reset:
+            self.reset()
+        text = chat_turn(self._seq, self.system if system is None else system, content, self.im_end_id)
+        yield from self._events(tok.encode(text, add_special_tokens=False).ids, False, sampling)
+
+    def generate_events(self, text=None, ids=None, reset=True, **sampling):
+        """generate() as (token, text piece) events."""
+        if ids is None:
+            ids = self._need_tok().encode(text or '', add_special_tokens=False).ids
+        yield from self._events(list(ids), reset, sampling)
 
     def tokenize(self, text, special=True):
         self._live()
