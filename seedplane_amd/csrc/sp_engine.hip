@@ -1714,8 +1714,8 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token_dev, trial_start_dev, n_trials_dev, trials_dev, u_dev,
                      n_u, 1.0 / temperature, sc.xbuf, sc.err, launches << 12, n_nodes, n_trials_total, out_dev,
                      max_depth};
-        void *args[] = {&a};
-        HIPCHK(hipLaunchCooperativeKernel((const void *)k_accept_tree, dim3(ACC_NB), dim3(ACC_T), args, 0, st));
+        hipLaunchKernelGGL(k_accept_tree, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
+        HIPCHK(hipGetLastError());
         HIPCHK(hipMemcpyAsync(sc.pin, sc.err, sizeof(unsigned), hipMemcpyDeviceToHost, st));
         if (out_host)
             HIPCHK(hipMemcpyAsync(sc.pin + PIN_OUT, out_dev, (max_depth + 4) * sizeof(int32_t), hipMemcpyDeviceToHost, st));

@@ -142,7 +142,10 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(const float *logits, int
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Tree acceptance on ACC_NB co-resident blocks.  The vocabulary is cut into ACC_NB x ACC_T contiguous chunks of
+// Tree acceptance on ACC_NB co-resident blocks (a plain launch: 64 blocks of 256 threads are all resident on the
+// 256-CU chip once the stream's previous kernel has finished, and every exchange wait is bounded, so a block that
+// never arrives ends the launch with an error instead of a hang; a cooperative launch enqueued behind a running
+// kernel slowed that kernel by ~10 %).  The vocabulary is cut into ACC_NB x ACC_T contiguous chunks of
 // C = ceil(V / (ACC_NB * ACC_T)) entries; thread t of block b owns chunk b * ACC_T + t and keeps its logits' weights
 // in registers.  Sums are taken sequentially inside a chunk, then over the ACC_T chunk sums of a block (butterfly in
 // each wave, wave sums in order: the block partial), then sequentially over the ACC_NB block partials.  Block partials are all-gathered through
