@@ -1690,12 +1690,14 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
         // the kernel checks every node / trial / token index it follows before using it (err = 2 if one is bad)
         hipStream_t st = (hipStream_t)stream;
-        // exchange words + error word, one set per device, zeroed once; tags never repeat within 2^20 launches, so
-        // neither needs clearing between launches (the kernel writes every entry of out_dev itself).  The error word
-        // and the result come back through a pinned block (device-to-host copies into pageable memory are staged
-        // by the runtime and cost tens of microseconds each); out_host may be any host memory.
-        struct AccScratch { unsigned long long *xbuf; unsigned *err; int32_t *pin; };
-        constexpr int PIN_OUT = 16;                      // out at int 16 of the pinned block, the error word at 0
+        // exchange words + a read-back block, one set per device, zeroed once; tags never repeat within 2^20
+        // launches, so neither needs clearing between launches (the kernel writes every entry of out_dev itself).
+        // The read-back block holds the error word (int 0), the completion tag (int 1) and a copy of the result (from
+        // int PIN_OUT), so one device-to-host copy into a pinned block returns all of it; the host polls the tag in
+        // that block before it synchronises (the wait then ends as soon as the copy lands).  out_host may be any
+        // host memory.
+        struct AccScratch { unsigned long long *xbuf; int32_t *back; int32_t *pin; };
+        constexpr int PIN_OUT = 16, BACK_INTS = PIN_OUT + 64 + 4;
         static std::map<int, AccScratch> scratch_of;
         static unsigned launches = 0;
         int dev = 0;
@@ -1703,26 +1705,31 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         auto it = scratch_of.find(dev);
         if (it == scratch_of.end()) {
             unsigned long long *xb = dev_alloc<unsigned long long>(4 * ACC_NB * 4);
-            unsigned *er = dev_alloc<unsigned>(1);
+            int32_t *back = dev_alloc<int32_t>(BACK_INTS);
             HIPCHK(hipMemset(xb, 0, 4 * ACC_NB * 4 * sizeof(unsigned long long)));
+            HIPCHK(hipMemset(back, 0, BACK_INTS * sizeof(int32_t)));
             int32_t *pin = nullptr;
-            HIPCHK(hipHostMalloc((void **)&pin, (PIN_OUT + 64 + 4) * sizeof(int32_t), hipHostMallocDefault));
-            it = scratch_of.emplace(dev, AccScratch{xb, er, pin}).first;
+            HIPCHK(hipHostMalloc((void **)&pin, BACK_INTS * sizeof(int32_t), hipHostMallocDefault));
+            it = scratch_of.emplace(dev, AccScratch{xb, back, pin}).first;
         }
         const AccScratch &sc = it->second;
         launches = launches % 0xFFFFFu + 1;
+        const unsigned tag = launches << 12;
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token_dev, trial_start_dev, n_trials_dev, trials_dev, u_dev,
-                     n_u, 1.0 / temperature, sc.xbuf, sc.err, launches << 12, n_nodes, n_trials_total, out_dev,
-                     max_depth};
+                     n_u, 1.0 / temperature, sc.xbuf, (unsigned *)sc.back, tag, n_nodes, n_trials_total, out_dev,
+                     max_depth, sc.back + PIN_OUT, sc.back + 1};
+        volatile int32_t *pin_tag = sc.pin + 1;
+        *pin_tag = 0;
         hipLaunchKernelGGL(k_accept_tree, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
         HIPCHK(hipGetLastError());
-        HIPCHK(hipMemcpyAsync(sc.pin, sc.err, sizeof(unsigned), hipMemcpyDeviceToHost, st));
-        if (out_host)
-            HIPCHK(hipMemcpyAsync(sc.pin + PIN_OUT, out_dev, (max_depth + 4) * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+        HIPCHK(hipMemcpyAsync(sc.pin, sc.back, (PIN_OUT + max_depth + 4) * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+        // bounded poll (about 1 s), then the stream synchronisation that reports any error of the copy or kernel
+        for (long spin = 0; *pin_tag != (int32_t)tag && spin < (1l << 26); ++spin) {
+        }
         HIPCHK(hipStreamSynchronize(st));
         const unsigned err = (unsigned)sc.pin[0];
         if (out_host) std::memcpy(out_host, sc.pin + PIN_OUT, (max_depth + 4) * sizeof(int32_t));
-        const unsigned code = (err & ~0xfffu) == (launches << 12) ? err & 0xfffu : 0u;
+        const unsigned code = (err & ~0xfffu) == tag ? err & 0xfffu : 0u;
         require(code != 2, SP_EINVAL, "malformed tree: node, trial or token index out of range");
         require(code == 0, SP_EHIP, "acceptance exchange timed out");
     });

@@ -177,6 +177,8 @@ struct AcceptArgs {
     int *out;                // [0] k, [1..k] accepted node ids, [max_depth+1] final token, [max_depth+2] uniforms used,
                              // [max_depth+3] bonus flag
     int max_depth;
+    int *out2;               // a second copy of out (may be NULL): the library's read-back block, next to err
+    int *done;               // may be NULL: block 0 stores tag_base here when it leaves (completion tag)
 };
 
 struct AccShared {
@@ -329,6 +331,11 @@ __device__ __forceinline__ bool acc_bad(const AcceptArgs &a) {
     return false;
 }
 
+__device__ __forceinline__ void acc_put(const AcceptArgs &a, int i, int v) {
+    a.out[i] = v;
+    if (a.out2) a.out2[i] = v;
+}
+
 __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
     __shared__ AccShared sh;
     const int C = (a.V + ACC_NB * ACC_T - 1) / (ACC_NB * ACC_T);
@@ -414,7 +421,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         }
         if (!alive) break;
         if (accepted >= 0) {
-            if (blockIdx.x == 0 && threadIdx.x == 0) a.out[1 + k] = accepted;
+            if (blockIdx.x == 0 && threadIdx.x == 0) acc_put(a, 1 + k, accepted);
             ++k;
             cur = accepted;
             continue;
@@ -424,16 +431,16 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         ++ui;
         break;
     }
-    if (!alive) return;
-    if (threadIdx.x == 0) {
+    if (alive && threadIdx.x == 0) {
         if (blockIdx.x == 0) {          // every block took the same decisions; block 0 reports them
-            a.out[0] = k;
-            for (int i = 1 + k; i <= a.max_depth; ++i) a.out[i] = -1;   // unused path entries
-            a.out[a.max_depth + 2] = ui;
-            a.out[a.max_depth + 3] = bonus;
+            acc_put(a, 0, k);
+            for (int i = 1 + k; i <= a.max_depth; ++i) acc_put(a, i, -1);   // unused path entries
+            acc_put(a, a.max_depth + 2, ui);
+            acc_put(a, a.max_depth + 3, bonus);
         }
-        if (final_tok >= 0) a.out[a.max_depth + 1] = final_tok;   // only the block owning the draw has it
+        if (final_tok >= 0) acc_put(a, a.max_depth + 1, final_tok);   // only the block owning the draw has it
     }
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.done) *a.done = (int)a.tag_base;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
