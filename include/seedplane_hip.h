@@ -62,8 +62,8 @@ enum {
     SP_F_LOGITS = 1,      /* run the final norm + LM head and produce fp32 logits for every column   */
     SP_F_ARGMAX = 2,      /* also produce the greedy id per column (first index on ties)             */
     SP_F_GRAPH = 4,       /* capture the step into a hipGraph on first use and replay it afterwards  */
-    SP_F_PERSISTENT = 8,  /* one decode column without a tree: run the whole step as one persistent   */
-                          /* cooperative kernel when the model fits it (else the kernel chain runs)  */
+    SP_F_PERSISTENT = 8,  /* accepted for compatibility; the step runs as the kernel chain (a whole-   */
+                          /* step persistent kernel was slower than the chain and has been removed)  */
     SP_F_UNFUSED = 16,    /* one column: run every RMSNorm and attention combine as a kernel of its   */
                           /* own instead of inside the next GEMV (same results; for checking)        */
     SP_F_FEED = 32        /* column b's token is the argmax id of column b of the last SP_F_ARGMAX   */
@@ -139,7 +139,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
                       int32_t *argmax_host);
 
 /* Introspection (no counterpart in the reference): which implementation ran the last sp_engine_forward call:
- * 1 = the persistent single-column kernel (SP_F_PERSISTENT accepted), 0 = the kernel chain, -1 = none yet. */
+ * 0 = the kernel chain (the only one), -1 = none yet. */
 int sp_engine_last_path(const sp_engine *e);
 
 /* Introspection (no counterpart in the reference; its decode report counts dispatches per token,

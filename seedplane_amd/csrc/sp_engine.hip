@@ -20,7 +20,6 @@
 
 #include "../../include/seedplane_hip.h"
 #include "sp_attn.h"
-#include "sp_decode.h"
 #include "sp_gemv.h"
 #include "sp_gemv1.h"
 #include "sp_pack.h"
@@ -471,25 +470,7 @@ struct sp_engine {
         graph_kernels.clear();
     }
 
-    // persistent decode kernel state (built on first use, rebuilt when the KV pool moves)
-    struct Persistent {
-        bool tried = false, ok = false;
-        std::string why;                 // reason it is unavailable
-        mk::Plan *d_plans = nullptr;
-        mk::LayerPtr *d_lp = nullptr;
-        mk::LayerAux *d_aux = nullptr;
-        mk::u64 *ll = nullptr;
-        unsigned *status = nullptr;      // [0] error word, [1] chosen token id
-        size_t words = 0;
-        unsigned launch = 0;
-        int nb = 0;
-        const f16 *kv0 = nullptr;        // layer-0 key cache the tables were built for
-        mk::Args args{};
-    } pk;
     int last_path = -1;
-    static constexpr bool persistent_enabled = false;
-    bool persistent_setup();
-    bool persistent_step(const sp_token &t, int flags, float *logits_dev, int32_t *argmax_host);
 
     // attention plan of one forward call: same-sequence column groups (multi-query kernel) or one block row per column
     struct AttnPlan {
@@ -528,8 +509,6 @@ void sp_engine::free_all() {
     for (auto p : kc) dev_free(p);
     for (auto p : vc) dev_free(p);
     kc.clear(); vc.clear();
-    dev_free(pk.d_plans); dev_free(pk.d_lp); dev_free(pk.d_aux); dev_free(pk.ll); dev_free(pk.status);
-    pk = Persistent{};
     if (h_upload) (void)hipHostFree(h_upload);
     if (h_ids) (void)hipHostFree(h_ids);
     if (upload_done) (void)hipEventDestroy(upload_done);
@@ -675,177 +654,6 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
         }
     }
     return p;
-}
-
-// ------------------------------------------------------------------------------------------- persistent decode
-namespace {
-template <int FMT, int HD>
-const void *decode_kernel() { return (const void *)mk::k_decode<FMT, HD>; }
-
-const void *pick_decode_kernel(int fmt, int hd) {
-    if (hd == 64) return fmt == 1 ? decode_kernel<1, 64>() : fmt == 2 ? decode_kernel<2, 64>() : decode_kernel<3, 64>();
-    return fmt == 1 ? decode_kernel<1, 128>() : fmt == 2 ? decode_kernel<2, 128>() : decode_kernel<3, 128>();
-}
-
-int kt_of(int fmt) { return fmt == 1 ? 32 : fmt == 2 ? 64 : 128; }
-}  // namespace
-
-// Checks that the model fits the persistent kernel's fixed on-chip buffers, plans the work of every block and builds
-// the tables.  Returns false (with pk.why) when it does not fit; the kernel chain is then used.
-//
-// Plan: every GEMV row group (a gate/up pair for gate_up), every attention item (kv head, chunk of mk::CH keys) and
-// every combine item (query head) of a layer is owned by one block; items are placed longest first on the least
-// loaded block (load = weight tiles, K/V 1-KiB pieces for attention), at most mk::MAXI per phase and one attention /
-// combine item per block.  LM-head row groups are cut into contiguous, equal ranges.
-bool sp_engine::persistent_setup() {
-    const int H = d.hidden, NH = d.n_heads, NKV = d.n_kv_heads, HD = d.head_dim, I = d.intermediate, L = d.n_layers;
-    const int fmt = embed.fmt, KT = kt_of(fmt);
-    if (pk.tried && pk.ok && pk.kv0 == kc[0]) return true;
-    if (pk.tried && !pk.ok) return false;
-    pk.tried = true;
-    auto no = [&](const char *why) { pk.why = why; pk.ok = false; return false; };
-    // Switched off: one launch of this kernel (a profiling build) ended in a GPU memory fault whose cause has not been
-    // found; until it is, single-column decode always runs the kernel chain.
-    if (!persistent_enabled) return no("the persistent decode kernel is switched off");
-    if (HD != 64 && HD != 128) return no("head_dim must be 64 or 128");
-    if (NH % NKV || NH / NKV > mk::MAX_G) return no("query group larger than 8");
-    if (H > 64 * mk::MAX_HN || H > mk::STAGE) return no("hidden size above 2048");
-    if (L > mk::MAX_L) return no("too many layers for the on-chip pointer table");
-    if (I % 16) return no("intermediate size must be a multiple of 16");
-    const DevMat &hm = d.tied_head ? embed : head;
-    std::vector<const DevMat *> mats = {&hm};
-    for (auto &l : layers) { mats.push_back(&l.qkv); mats.push_back(&l.o); mats.push_back(&l.gate_up); mats.push_back(&l.down); }
-    for (auto m : mats) {
-        if (m->fmt != fmt) return no("mixed weight formats");
-        if (m->nkt * KT > mk::MAX_K) return no("a matrix is wider than the on-chip operand buffer");
-    }
-    const int G = NH / NKV;
-    const int nch_max = (n_slots + mk::CH - 1) / mk::CH;
-    if (nch_max > mk::MAX_NCH || nch_max * (HD + 2) > mk::STAGE) return no("KV window too long");
-    if ((G + 2) * HD > mk::STAGE || NH * HD > mk::STAGE) return no("attention operands too large");
-    int dev = 0, ncu = 0;
-    HIPCHK(hipGetDevice(&dev));
-    HIPCHK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
-    const void *kern = pick_decode_kernel(fmt, HD);
-    int per_cu = 0;
-    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, mk::NT, 0));
-    if (per_cu < 1) return no("the persistent kernel does not fit on a CU");
-    const int nb = ncu;
-    if (NKV * nch_max > nb || NH > nb) return no("more attention items than blocks");
-    pk.nb = nb;
-
-    // ---- work plan
-    const Layer &l0 = layers[0];
-    const int np = 2 * mk::CH * HD * 2 / 1024;                // K/V pieces of one attention chunk
-    struct Item { int cost, ph, id; };
-    std::vector<Item> items;
-    auto add = [&](int ph, int n, int cost) { for (int i = 0; i < n; ++i) items.push_back({cost, ph, i}); };
-    add(3, l0.down.rows_pad / 16, l0.down.nkt);
-    add(2, l0.gate_up.rows_pad / 32, 2 * l0.gate_up.nkt);
-    add(0, l0.qkv.rows_pad / 16, l0.qkv.nkt);
-    add(1, l0.o.rows_pad / 16, l0.o.nkt);
-    add(4, NKV * nch_max, np);
-    add(5, NH, 2);
-    std::stable_sort(items.begin(), items.end(), [](const Item &x, const Item &y) { return x.cost > y.cost; });
-    std::vector<mk::Plan> plans(nb);
-    std::vector<long> load(nb, 0);
-    for (auto &p : plans) { std::memset(&p, 0, sizeof(p)); p.att = -1; p.cmb = -1; }
-    for (const Item &it : items) {
-        int best = -1;
-        for (int b = 0; b < nb; ++b) {
-            mk::Plan &p = plans[b];
-            const bool room = it.ph < 4 ? p.n[it.ph] < mk::MAXI : it.ph == 4 ? p.att < 0 : p.cmb < 0;
-            if (room && (best < 0 || load[b] < load[best])) best = b;
-        }
-        if (best < 0) return no("a layer has more items than the blocks can hold");
-        mk::Plan &p = plans[best];
-        if (it.ph < 4) p.item[it.ph][p.n[it.ph]++] = (short)it.id;
-        else if (it.ph == 4) p.att = (it.id % NKV) * nch_max + it.id / NKV;   // chunk-major: early chunks spread
-        else p.cmb = it.id;
-        load[best] += it.cost;
-    }
-    const int hg = hm.rows_pad / 16;
-    const int nb_head = std::min(nb, hg);
-    for (int b = 0; b < nb_head; ++b) {
-        plans[b].h0 = (int)((long)hg * b / nb_head);
-        plans[b].h1 = (int)((long)hg * (b + 1) / nb_head);
-    }
-
-    mk::Args &A = pk.args;
-    A = mk::Args{};
-    A.emb_w = embed.w; A.emb_sz = embed.sz; A.emb_nkt = embed.nkt;
-    A.head_w = hm.w; A.head_sz = hm.sz;
-    A.final_norm = final_norm; A.inv_freq = inv_freq;
-    A.nkt[0] = np; A.nkt[1] = l0.qkv.nkt; A.nkt[2] = l0.o.nkt; A.nkt[3] = l0.gate_up.nkt; A.nkt[4] = l0.down.nkt;
-    A.nkt[5] = hm.nkt;
-    A.L = L; A.H = H; A.NH = NH; A.NKV = NKV; A.I = I; A.V = d.vocab; A.Nqkv = Nqkv; A.n_slots = n_slots;
-    A.nch_max = nch_max;
-    A.eps = d.rms_eps; A.scale = 1.0f / std::sqrt((float)HD);
-    A.o_part = (size_t)Nqkv;
-    A.o_att = A.o_part + (size_t)NH * nch_max * (HD + 2);
-    A.o_xmid = A.o_att + (size_t)NH * HD;
-    A.o_act = A.o_xmid + (size_t)H;
-    A.o_x = A.o_act + (size_t)I / 2;
-    A.stride = A.o_x + (size_t)H;
-    A.o_am = (size_t)L * A.stride;
-    A.nb_head = nb_head;
-    std::vector<mk::LayerPtr> lp(L + 1);
-    std::vector<mk::LayerAux> aux(L);
-    for (int i = 0; i < L; ++i) {
-        const Layer &y = layers[i];
-        const DevMat *m4[4] = {&y.qkv, &y.o, &y.gate_up, &y.down};
-        for (int j = 0; j < 4; ++j) { lp[i].w[j] = m4[j]->w; lp[i].sz[j] = m4[j]->sz; }
-        lp[i].kc = kc[i]; lp[i].vc = vc[i];
-        aux[i] = mk::LayerAux{y.qkv_b, y.in_norm, y.post_norm, kc[i], vc[i]};
-    }
-    lp[L] = mk::LayerPtr{};
-    lp[L].w[0] = hm.w; lp[L].sz[0] = hm.sz;
-    dev_free(pk.d_plans); dev_free(pk.d_lp); dev_free(pk.d_aux); dev_free(pk.ll); dev_free(pk.status);
-    pk.d_plans = nullptr; pk.d_lp = nullptr; pk.d_aux = nullptr; pk.ll = nullptr; pk.status = nullptr;
-    pk.d_plans = dev_alloc<mk::Plan>(nb);
-    pk.d_lp = dev_alloc<mk::LayerPtr>(L + 1);
-    pk.d_aux = dev_alloc<mk::LayerAux>(L);
-    HIPCHK(hipMemcpy(pk.d_plans, plans.data(), nb * sizeof(mk::Plan), hipMemcpyHostToDevice));
-    HIPCHK(hipMemcpy(pk.d_lp, lp.data(), (L + 1) * sizeof(mk::LayerPtr), hipMemcpyHostToDevice));
-    HIPCHK(hipMemcpy(pk.d_aux, aux.data(), L * sizeof(mk::LayerAux), hipMemcpyHostToDevice));
-    pk.words = A.o_am + 2 * (size_t)nb;
-    pk.ll = dev_alloc<mk::u64>(pk.words);
-    HIPCHK(hipMemset(pk.ll, 0, pk.words * sizeof(mk::u64)));      // tag 0 is never used
-    pk.status = dev_alloc<unsigned>(2);
-    HIPCHK(hipMemset(pk.status, 0, 2 * sizeof(unsigned)));
-    A.plans = pk.d_plans; A.lp = pk.d_lp; A.aux = pk.d_aux; A.ll = pk.ll;
-    A.err = pk.status; A.out_id = (int *)(pk.status + 1);
-    pk.kv0 = kc[0];
-    pk.ok = true;
-    return true;
-}
-
-// One decode column through the persistent kernel (logits into logits_dev, or the engine buffer when NULL; the token
-// id into argmax_host).  Returns false (nothing launched) when the column or the model does not fit it.
-bool sp_engine::persistent_step(const sp_token &t, int flags, float *logits_dev, int32_t *argmax_host) {
-    if (t.tree_count != 0 || t.ctx_hi < t.ctx_lo || t.slot != t.ctx_hi % n_slots || !(flags & SP_F_LOGITS)) return false;
-    if (pk.kv0 != (kc.empty() ? nullptr : kc[0])) pk.tried = false;       // KV pool reallocated: rebuild tables
-    if (!persistent_setup()) return false;
-    const int nlin = t.ctx_hi - t.ctx_lo + 1;
-    if ((nlin + mk::CH - 1) / mk::CH > pk.args.nch_max) return false;
-    mk::Args A = pk.args;
-    pk.launch = pk.launch % 0xFFFFFu + 1;
-    A.tag0 = pk.launch << 12;
-    A.tok = t;
-    A.logits = logits_dev ? logits_dev : logits;
-    void *args[] = {&A};
-    HIPCHK(hipLaunchCooperativeKernel(pick_decode_kernel(embed.fmt, d.head_dim), dim3(pk.nb), dim3(mk::NT), args, 0,
-                                      stream));
-    unsigned st[2] = {0, 0};
-    HIPCHK(hipMemcpyAsync(st, pk.status, sizeof(st), hipMemcpyDeviceToHost, stream));
-    HIPCHK(hipStreamSynchronize(stream));
-    if (st[0] != 0) {
-        HIPCHK(hipMemset(pk.status, 0, sizeof(unsigned)));
-        throw Fail{SP_EHIP, st[0] == 2 ? "persistent decode kernel: weight stream out of order (internal error)"
-                                       : "persistent decode kernel: a cross-block exchange timed out"};
-    }
-    if (argmax_host) *argmax_host = (int32_t)st[1];
-    return true;
 }
 
 // Every column must name a token (unless fed from the last argmax), a reserved sequence and slot, and a visible range
@@ -1145,7 +953,7 @@ void alloc_pool(const sp_engine *e, int n_seq, int n_slots, std::vector<f16 *> &
 }
 
 // Makes (k, v) the engine's pool: frees the old one, sizes the attention partials for n_slots and drops the recorded
-// graphs and persistent tables (they hold the old addresses).  The stream must be idle.
+// graphs (they hold the old addresses).  The stream must be idle.
 void install_pool(sp_engine *e, int n_seq, int n_slots, std::vector<f16 *> &k, std::vector<f16 *> &v, uint64_t bytes) {
     for (auto p : e->kc) dev_free(p);
     for (auto p : e->vc) dev_free(p);
@@ -1163,7 +971,6 @@ void install_pool(sp_engine *e, int n_seq, int n_slots, std::vector<f16 *> &k, s
     e->attn_part = dev_alloc<float>((size_t)e->maxT * e->d.n_heads * e->max_nchunk * part_floats(e->d.head_dim));
     e->n_seq = n_seq; e->n_slots = n_slots;
     e->drop_graphs();
-    e->pk.tried = false;
 }
 }  // namespace
 
@@ -1257,13 +1064,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         e->check_columns(n, toks, feed);
         const bool use_graph = flags & SP_F_GRAPH;
         const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX | SP_F_UNFUSED | SP_F_FEED);
-        if (n == 1 && (flags & SP_F_PERSISTENT) && !feed) {
-            if (e->persistent_step(toks[0], sflags, logits_dev, argmax_host)) {
-                e->last_path = 1;
-                return;
-            }
-        }
-        e->last_path = 0;
+        e->last_path = 0;                  // SP_F_PERSISTENT is accepted; every step runs as the kernel chain
         const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
         e->upload(n, toks, ap);
         if (use_graph) {
@@ -1341,12 +1142,6 @@ void sp_debug_one_plan(int qs, int qw, int ds, int dw, int gw) {
     g_tune_one[0] = qs; g_tune_one[1] = qw; g_tune_one[2] = ds; g_tune_one[3] = dw; g_tune_one[4] = gw;
 }
 void sp_debug_attn_plan(int nwv, int sub) { g_tune_attn[0] = nwv; g_tune_attn[1] = sub; }
-#endif
-
-#ifdef SP_DECODE_TRACE
-int sp_debug_decode_trace(unsigned long long *host) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(mk::trace_buf), sizeof(mk::trace_buf)) == hipSuccess ? SP_OK : SP_EHIP;
-}
 #endif
 
 int sp_engine_logits(sp_engine *e, float **logits_dev) {

@@ -360,10 +360,14 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
 #pragma unroll
                 for (int s = 0; s < ST; ++s) {
                     if constexpr (PRO == PRO_NONE) {
-                        // either layout; columns past m read as zeros (their lanes do not load)
-                        const f16 *src = a.xmtp ? a.x + ((size_t)(kt * ST + s) * a.xmtp + mt) * 512 + lane * 8
-                                                : xrow[mt] + kt * KT + s * 32;
-                        xa[t][mt][s] = xon[mt] ? *(const f16x8 *)src : zero8;
+                        // fragment-major (xmtp == MT): every lane loads, columns past m included -- the buffers hold
+                        // whole 16-column tiles, and an MFMA output row depends only on its own A row, so whatever
+                        // those columns hold never reaches a stored output; row-major: columns past m read as zeros
+                        // (their lanes do not load)
+                        if (a.xmtp)
+                            xa[t][mt][s] = *(const f16x8 *)(a.x + ((size_t)(kt * ST + s) * MT + mt) * 512 + lane * 8);
+                        else
+                            xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(xrow[mt] + kt * KT + s * 32) : zero8;
                     } else
                         xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(act + (kt - k0) * KT + s * 32 + 8 * g) : zero8;
                 }

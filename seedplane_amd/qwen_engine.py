@@ -106,7 +106,6 @@ class Qwen2Engine:
             self.weight_format = _lib.SP_FMT_F16
         self.tied = 'lm_head.weight' not in tensors and 'lm_head.qweight' not in tensors
         self.max_tokens = int(max_tokens)
-        self.persistent = False      # single-column decode through the persistent kernel (decode(persistent=...))
 
         _lib.require_gpu()
         self.device = torch.device(device if device not in ('hip', None) else 'cuda')
@@ -350,7 +349,7 @@ class Qwen2Engine:
 
     @property
     def last_path(self):
-        """1 if the last engine call ran the persistent single-column kernel, 0 for the kernel chain."""
+        """0 once an engine call ran (every step is the kernel chain), -1 before the first."""
         return int(self.lib.sp_engine_last_path(self.h))
 
     def logits_view(self, n):
@@ -372,10 +371,9 @@ class Qwen2Engine:
         return self._logits_buf[:n]
 
     @torch.inference_mode()
-    def decode(self, tokens, caches, logits_out=None, graph=True, persistent=None):
+    def decode(self, tokens, caches, logits_out=None, graph=True):
         """One batched decode step: token i appended to caches[i] (all distinct sequences).  Returns greedy ids.
-        A single column runs as one persistent kernel when `persistent` and the model fits it (see
-        `last_path`); otherwise, and for batches, the kernel chain runs (captured as a graph when `graph`)."""
+        The step runs as the kernel chain, captured as a graph when `graph`."""
         if len(tokens) != len(caches) or not tokens:
             raise ValueError('one token per cache')
         cols = []
@@ -385,10 +383,6 @@ class Qwen2Engine:
                 raise ValueError(f'KV cache capacity {c.capacity} exceeded')
             cols.append(self._column(t, c, c.length, c.length))
         flags = _lib.SP_F_GRAPH if graph else 0
-        if persistent is None:
-            persistent = self.persistent
-        if persistent and len(cols) == 1:
-            flags |= _lib.SP_F_PERSISTENT
         ids = self.run(cols, flags, logits_out=logits_out, want_ids=True)
         for c in caches:
             c.length += 1
