@@ -498,12 +498,29 @@ def workload_spec(args, out):
                 'config': {'workload': r['workload']}, **{k: r[k] for k in ('accepted_per_step', 'emitted_per_step')}})
 
 
+def workload_sampling(args, out):
+    """The filtered sampler alone: 16 draws per launch over 16 rows of 151936 fp32 logits (the Qwen2 vocabulary),
+    T = 0.8, for three filters.  The draws use only the library's sampling op; a tiny engine provides the handle."""
+    from seedplane_amd.presets import preset
+    from seedplane_amd.qwen_engine import Qwen2Engine
+    from seedplane_amd.synth import make_weights
+    cfg, w = make_weights(preset('tiny'), 'q8', seed=0)
+    eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=16)
+    r = sampling_cost(eng, 151936, reps=20)
+    main_us = r['top_k50_top_p0.9']['us_per_launch']
+    out.update({'metric': 'filtered sampling launch time (16 draws, top-k 50 + top-p 0.9, T 0.8)', 'value': main_us,
+                'unit': 'us/launch', 'steps': 20, 'warmup': 1, 'ms_per_step': round(main_us / 1e3, 4),
+                'higher_is_better': False, 'dtype': 'fp32 logits, 64-bit integer masses',
+                'data': 'synthetic (N(0, 3) logits, seeded uniforms)',
+                'config': {'workload': '16 rows x 151936 fp32 logits, one draw per row'}, 'sampling': r})
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=256)
     ap.add_argument('--warmup', type=int, default=16)
-    ap.add_argument('--workload', default='c3', choices=['c3', 'c2', 'c5', 'spec', 'verify', 'roofline'])
+    ap.add_argument('--workload', default='c3', choices=['c3', 'c2', 'c5', 'spec', 'verify', 'roofline', 'sampling'])
     ap.add_argument('--no-bs16', action='store_true')
     ap.add_argument('--no-verify', action='store_true')
     ap.add_argument('--no-cpu-baseline', action='store_true')
@@ -521,7 +538,7 @@ def main():
     out = {'metric': METRIC, 'value': None, 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
            'ms_per_step': None, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None}
     {'c3': workload_c3, 'c2': workload_c2, 'c5': workload_c5, 'spec': workload_spec, 'verify': workload_verify,
-     'roofline': workload_roofline}[args.workload](args, out)
+     'roofline': workload_roofline, 'sampling': workload_sampling}[args.workload](args, out)
     print(json.dumps(out), flush=True)
 
 

@@ -1462,9 +1462,40 @@ int sp_op_sample_filtered(const float *logits_dev, int32_t vocab, int32_t ld, co
         require(vocab >= 1 && ld >= vocab && n >= 1 && n <= 65535, SP_EINVAL, "bad sizes");
         require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
         require(top_p > 0.0, SP_EINVAL, "top_p must be positive");
-        hipLaunchKernelGGL(k_sample_filtered, dim3(n), dim3(FS_THREADS), 0, (hipStream_t)stream, logits_dev, vocab, ld,
-                           row_dev, u_dev, (float)temperature, top_k, top_p, out_dev);
-        HIPCHK(hipGetLastError());
+        hipStream_t st = (hipStream_t)stream;
+        // histograms and per-row state for FM_ROWS draws, one set per device (calls on one device must not overlap)
+        struct FmScratch { FmHist *hist; FmState *st; };
+        static std::map<int, FmScratch> scratch_of;
+        static std::mutex mu;
+        int dev = 0;
+        HIPCHK(hipGetDevice(&dev));
+        FmScratch sc;
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            auto it = scratch_of.find(dev);
+            if (it == scratch_of.end())
+                it = scratch_of.emplace(dev, FmScratch{dev_alloc<FmHist>((size_t)FM_ROWS * FM_NLEV),
+                                                       dev_alloc<FmState>(FM_ROWS)}).first;
+            sc = it->second;
+        }
+        const int nb = (vocab + FM_SPAN - 1) / FM_SPAN;
+        const bool topk = top_k > 0 && top_k < vocab;
+        for (int r0 = 0; r0 < n; r0 += FM_ROWS) {
+            const int nr = std::min(FM_ROWS, n - r0);
+            const FmArgs a{logits_dev, vocab, ld, row_dev, u_dev, (float)temperature, top_k, top_p, out_dev, sc.hist,
+                           sc.st, r0};
+            const dim3 grid(nb, nr), block(FS_THREADS);
+            hipLaunchKernelGGL(k_fm_init, dim3(nr), dim3(256), 0, st, a);
+            hipLaunchKernelGGL(k_fm_max, grid, block, 0, st, a);
+            if (topk)
+                for (int j = 0; j < 4; ++j) hipLaunchKernelGGL(k_fm_topk, grid, block, 0, st, a, j);
+            hipLaunchKernelGGL(k_fm_h1, grid, block, 0, st, a);
+            if (top_p < 1.0)
+                for (int j = 0; j < 3; ++j) hipLaunchKernelGGL(k_fm_select<false>, grid, block, 0, st, a, j);
+            for (int j = 0; j < 3; ++j) hipLaunchKernelGGL(k_fm_select<true>, grid, block, 0, st, a, j);
+            hipLaunchKernelGGL(k_fm_finish, dim3(nr), block, 0, st, a);
+            HIPCHK(hipGetLastError());
+        }
     });
 }
 

@@ -445,7 +445,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
 
 // ---------------------------------------------------------------------------------------------------------------
 // Filtered sampling: temperature, top-k and top-p (nucleus) exactly as Qwen2Engine.sample defines them
-// (qwen_engine.py:146-156; native Sampler::distribution, sampler.hpp:22-57), one block of FS_THREADS per draw.
+// (qwen_engine.py:146-156; native Sampler::distribution, sampler.hpp:22-57), many blocks of FS_THREADS per draw.
 //   z_i   = fp32(l_i / T);  the order is z descending, ties by ascending index (the native sampler's comparator);
 //   top-k (0 < k < V): keep z_i >= the k-th largest z (ties at the cutoff kept);
 //   mass  m_i = floor(exp(z_i - z_max) * 2^40) as a 64-bit integer (fp64 exp; z_max = the row maximum, so m <= 2^40
@@ -456,8 +456,9 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
 //   draw: target = floor(u * K) (clamped below K) over the kept mass K; the token is the first in sorted order whose
 //         inclusive cumulative mass exceeds the target (inverse CDF, Sampler::draw, sampler.hpp:93-97).
 // Selections in sorted order never sort: a radix descent over the 32-bit order key (8 bits per level, LDS histograms
-// of counts and 64-bit masses restricted to the candidates) finds the bin holding the k-th token / the target mass;
-// at the last level the bin is one z value, whose tokens (equal masses) are ordered by index.
+// of counts and 64-bit masses restricted to the candidates, added into global histograms) finds the bin holding the
+// k-th token / the target mass; at the last level the bin is one z value, whose tokens (equal masses) are ordered
+// by index.
 constexpr int FS_THREADS = 1024;
 
 __device__ __forceinline__ uint32_t fs_key(float z) {      // monotone: larger z, larger key
@@ -487,8 +488,10 @@ struct FsShared {
 // Histogram add with the wave's lanes combined per bin first: most keys of a row share their top bits, and 64 lanes
 // adding to one LDS word serialise.  Up to FS_AGG distinct bins of the wave are combined (one atomic per bin, from
 // the lowest active lane); lanes left after that add on their own.  Integer sums: the result is order-independent.
-constexpr int FS_AGG = 1;
-constexpr int FS_U = 16;             // elements per thread whose loads are issued together in every pass
+#ifndef SP_FS_AGG
+#define SP_FS_AGG 1
+#endif
+constexpr int FS_AGG = SP_FS_AGG;
 template <bool MASS>
 __device__ __forceinline__ void fs_hist_add(FsShared &sh, bool act, int bin, unsigned long long mass) {
     const int lane = threadIdx.x & 63;
@@ -574,53 +577,6 @@ __device__ __forceinline__ unsigned long long fs_block_sum(unsigned long long v,
     return t;
 }
 
-// First token (z descending, index ascending) among the candidates (key >= kmin) whose inclusive cumulative mass
-// exceeds `target`.  Returns its key; *above_out = the mass of every candidate before the key's tie group,
-// *rank_out = the token's rank inside its tie group (index order).  The caller guarantees target < total mass.
-__device__ uint32_t fs_select_mass(const float *row, int V, float T, float zmax, uint32_t kmin,
-                                   unsigned long long target, FsShared &sh, unsigned long long *above_out,
-                                   unsigned long long *rank_out, int *first_out = nullptr) {
-    uint32_t prefix = 0, mask = 0;
-    unsigned long long above = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int b = threadIdx.x; b < 256; b += FS_THREADS) {
-            sh.hmass[b] = shift == 24 ? sh.h1mass[b] : 0ull;
-            sh.hcnt[b] = shift == 24 ? sh.h1cnt[b] : 0u;
-            sh.hidx[b] = 0xffffffffu;
-        }
-        __syncthreads();
-        for (int i0 = 0; shift < 24 && i0 < V; i0 += FS_THREADS * FS_U) {   // block-uniform: whole waves vote
-            float lv[FS_U];
-#pragma unroll
-            for (int u = 0; u < FS_U; ++u) {
-                const int i = i0 + u * FS_THREADS + threadIdx.x;
-                lv[u] = i < V ? row[i] : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < FS_U; ++u) {
-                const int i = i0 + u * FS_THREADS + threadIdx.x;
-                const float z = __fdiv_rn(lv[u], T);
-                const uint32_t k = fs_key(z);
-                const bool act = i < V && k >= kmin && (k & mask) == prefix;
-                fs_hist_add<true>(sh, act, (k >> shift) & 255, act ? fs_mass(z, zmax) : 0ull);
-                if (shift == 0 && act) atomicMin(&sh.hidx[k & 255], (unsigned)i);
-            }
-        }
-        __syncthreads();
-        fs_choose_bin<true>(sh, above, target, 0u);
-        __syncthreads();
-        prefix |= sh.sel_bin << shift;
-        mask |= 255u << shift;
-        above = sh.above;
-        __syncthreads();
-    }
-    const unsigned long long m = fs_mass(fs_unkey(prefix), zmax);
-    if (first_out) *first_out = (int)sh.hidx[prefix & 255];    // the tie group's smallest index
-    *above_out = above;
-    *rank_out = m > 0 ? (target - above) / m : 0;
-    return prefix;
-}
-
 // Index of the rank-th token (index order) whose key equals `key` (a block-wide scan over contiguous chunks).
 __device__ int fs_index_of(const float *row, int V, float T, uint32_t key, unsigned long long rank, FsShared &sh) {
     const int C = (V + FS_THREADS - 1) / FS_THREADS, lo = threadIdx.x * C, hi = min(V, lo + C);
@@ -648,107 +604,252 @@ __device__ int fs_index_of(const float *row, int V, float T, uint32_t key, unsig
     return found;
 }
 
-// out[s] = filtered draw from row rows[s] with uniform u[s]; top_k <= 0 or >= V: no top-k; top_p >= 1: no top-p.
-__global__ void __launch_bounds__(FS_THREADS) k_sample_filtered(const float *logits, int V, int ld, const int *rows,
-                                                               const double *u, float T, int top_k, double top_p,
-                                                               int *out) {
-    __shared__ FsShared sh;
-    const int s = blockIdx.x;
-    const float *row = logits + (size_t)rows[s] * ld;
-    // ---- maximum z (its key)
-    uint32_t kmax = 0;
-    for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {
-        float lv[FS_U];
+// ---------------------------------------------------------------------------------------------------------------
+// The launches: one block covers FM_SPAN consecutive entries of a row (19 blocks for 151936 entries),
+// so every pass over the row runs on the whole chip instead of one CU.  Each launch first repeats the bin choice of
+// the previous level (every block from the same global histogram, so every block takes the same choice; block 0
+// also records it for the later launches), then histograms its entries into LDS and adds the block's bins to the
+// level's global histogram with integer atomics (exact, order-independent).  Launches per draw batch: init, max,
+// 4 top-k levels (when top-k applies), the candidates' first level, 3 top-p levels (when top-p applies), 3 draw
+// levels, finish.  The scratch (histograms and per-row state) is the library's, one set per device: calls on one
+// device must not overlap.
+#ifndef SP_FM_U
+#define SP_FM_U 8
+#endif
+constexpr int FM_U = SP_FM_U;                      // entries per thread and pass
+constexpr int FM_SPAN = FS_THREADS * FM_U;         // entries of a row per block
+constexpr int FM_ROWS = 256;                       // rows per launch sequence (the scratch holds this many)
+enum { FM_TOPK = 0, FM_H1 = 4, FM_TOPP = 5, FM_DRAW = 8, FM_NLEV = 11 };
+struct FmHist {
+    unsigned long long mass[256];
+    unsigned int cnt[256];
+    unsigned int idx[256];                         // last level: the smallest index in each bin
+};
+struct FmState {
+    unsigned int kmax, kmin;
+    unsigned int prefix[FM_NLEV];                  // key bits chosen above the level's shift
+    unsigned int rem[4];                           // top-k: tokens still to count inside the prefix
+    unsigned long long above[FM_NLEV];             // mass before the prefix (sorted order)
+    unsigned long long F, tp, K, tgt;
+    int topp;                                      // 1: the top-p cut applies (tp < F)
+};
+struct FmArgs {
+    const float *logits;
+    int V, ld;
+    const int *rows;
+    const double *u;
+    float T;
+    int top_k;                                     // > 0 and < V: the top-k levels ran
+    double top_p;                                  // < 1: the top-p levels ran
+    int *out;
+    FmHist *hist;                                  // [FM_ROWS][FM_NLEV]
+    FmState *st;                                   // [FM_ROWS]
+    int row0;                                      // draws row0 .. row0 + gridDim.y - 1 (blockIdx.y = draw - row0)
+};
+
+__global__ void __launch_bounds__(256) k_fm_init(FmArgs a) {
+    const int r = blockIdx.x;
+    unsigned int *h = (unsigned int *)(a.hist + (size_t)r * FM_NLEV);
+    constexpr int W = sizeof(FmHist) / 4, IDX0 = (256 * 8 + 256 * 4) / 4;
+    for (int i = threadIdx.x; i < FM_NLEV * W; i += blockDim.x) h[i] = (i % W) >= IDX0 ? 0xffffffffu : 0u;
+    unsigned int *s = (unsigned int *)(a.st + r);
+    for (int i = threadIdx.x; i < (int)(sizeof(FmState) / 4); i += blockDim.x) s[i] = 0u;
+}
+
+__global__ void __launch_bounds__(FS_THREADS) k_fm_max(FmArgs a) {
+    __shared__ unsigned int red[FS_THREADS / 64];
+    const int r = blockIdx.y, i0 = blockIdx.x * FM_SPAN;
+    const float *row = a.logits + (size_t)a.rows[a.row0 + r] * a.ld;
+    float lv[FM_U];
 #pragma unroll
-        for (int u = 0; u < FS_U; ++u) {
-            const int i = i0 + u * FS_THREADS + threadIdx.x;
-            lv[u] = i < V ? row[i] : -INFINITY;
-        }
-#pragma unroll
-        for (int u = 0; u < FS_U; ++u) kmax = max(kmax, fs_key(__fdiv_rn(lv[u], T)));
+    for (int u = 0; u < FM_U; ++u) {
+        const int i = i0 + u * FS_THREADS + threadIdx.x;
+        lv[u] = i < a.V ? row[i] : -INFINITY;
     }
-    for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
-    if ((threadIdx.x & 63) == 0) sh.redu[threadIdx.x >> 6] = kmax;
+    uint32_t k = 0;
+#pragma unroll
+    for (int u = 0; u < FM_U; ++u) k = max(k, fs_key(__fdiv_rn(lv[u], a.T)));
+    for (int o = 32; o > 0; o >>= 1) k = max(k, (uint32_t)__shfl_xor((int)k, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
     __syncthreads();
-    kmax = 0;
-    for (int i = 0; i < FS_THREADS / 64; ++i) kmax = max(kmax, sh.redu[i]);
-    const float zmax = fs_unkey(kmax);
-    // ---- top-k cutoff: the k-th largest key by a radix descent on counts (ties at the cutoff kept)
-    uint32_t kmin = 0;
-    if (top_k > 0 && top_k < V) {
-        uint32_t prefix = 0, mask = 0;
-        unsigned int rem = (unsigned)top_k;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            for (int b = threadIdx.x; b < 256; b += FS_THREADS) sh.hcnt[b] = 0;
-            __syncthreads();
-            for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {
-                float lv[FS_U];
-#pragma unroll
-                for (int u = 0; u < FS_U; ++u) {
-                    const int i = i0 + u * FS_THREADS + threadIdx.x;
-                    lv[u] = i < V ? row[i] : 0.f;
-                }
-#pragma unroll
-                for (int u = 0; u < FS_U; ++u) {
-                    const int i = i0 + u * FS_THREADS + threadIdx.x;
-                    const uint32_t k = fs_key(__fdiv_rn(lv[u], T));
-                    fs_hist_add<false>(sh, i < V && (k & mask) == prefix, (k >> shift) & 255, 0ull);
-                }
-            }
-            __syncthreads();
-            fs_choose_bin<false>(sh, 0ull, 0ull, rem);
-            __syncthreads();
-            prefix |= sh.sel_bin << shift;
-            mask |= 255u << shift;
-            rem = sh.redu[0];
-            __syncthreads();
-        }
-        kmin = prefix;
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < FS_THREADS / 64; ++i) k = max(k, red[i]);
+        atomicMax(&a.st[r].kmax, k);
     }
-    // ---- first-level histogram of the candidates (count and mass per top key byte); F = the total mass
-    for (int b = threadIdx.x; b < 256; b += FS_THREADS) { sh.hmass[b] = 0; sh.hcnt[b] = 0; }
-    __syncthreads();
-    for (int i0 = 0; i0 < V; i0 += FS_THREADS * FS_U) {
-        float lv[FS_U];
-#pragma unroll
-        for (int u = 0; u < FS_U; ++u) {
-            const int i = i0 + u * FS_THREADS + threadIdx.x;
-            lv[u] = i < V ? row[i] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < FS_U; ++u) {
-            const int i = i0 + u * FS_THREADS + threadIdx.x;
-            const float z = __fdiv_rn(lv[u], T);
-            const uint32_t k = fs_key(z);
-            const bool act = i < V && k >= kmin;
-            fs_hist_add<true>(sh, act, k >> 24, act ? fs_mass(z, zmax) : 0ull);
-        }
-    }
-    __syncthreads();
-    unsigned long long F = 0;
+}
+
+// The level's global histogram into the block's LDS (counts, and masses for a mass level).
+__device__ __forceinline__ void fm_load_hist(FsShared &sh, const FmHist &g, bool mass) {
     for (int b = threadIdx.x; b < 256; b += FS_THREADS) {
-        sh.h1mass[b] = sh.hmass[b];
-        sh.h1cnt[b] = sh.hcnt[b];
-        F += sh.hmass[b];
+        sh.hcnt[b] = g.cnt[b];
+        sh.hmass[b] = mass ? g.mass[b] : 0ull;
     }
-    F = fs_block_sum(F, sh);
-    // ---- top-p: kept mass K = inclusive mass of the first token whose inclusive mass exceeds floor(p * F)
-    unsigned long long K = F;
-    if (top_p < 1.0) {
-        const unsigned long long tp = (unsigned long long)(top_p * (double)F);
-        if (tp < F) {
-            unsigned long long above, rank;
-            const uint32_t key = fs_select_mass(row, V, T, zmax, kmin, tp, sh, &above, &rank);
-            K = above + (rank + 1) * fs_mass(fs_unkey(key), zmax);
+    __syncthreads();
+}
+// One choice of fs_choose_bin on the histogram in LDS; every thread gets (bin, above or rem).
+template <bool MASS>
+__device__ __forceinline__ void fm_choose(FsShared &sh, unsigned long long above, unsigned long long target,
+                                          unsigned int rem, unsigned int &bin, unsigned long long &above_out,
+                                          unsigned int &rem_out) {
+    fs_choose_bin<MASS>(sh, above, target, rem);
+    __syncthreads();
+    bin = sh.sel_bin;
+    above_out = MASS ? sh.above : 0ull;
+    rem_out = MASS ? 0u : sh.redu[0];
+    __syncthreads();
+}
+// Adds this block's entries with (key & mask) == prefix (and key >= kmin) to the level's global histogram by key
+// byte (key >> shift) & 255: counts, masses (MASS), smallest index per bin (IDX).
+template <bool MASS, bool IDX>
+__device__ __forceinline__ void fm_pass(const FmArgs &a, FsShared &sh, const float *row, float zmax, uint32_t kmin,
+                                        uint32_t mask, uint32_t prefix, int shift, FmHist &g) {
+    const int i0 = blockIdx.x * FM_SPAN;
+    float lv[FM_U];
+#pragma unroll
+    for (int u = 0; u < FM_U; ++u) {
+        const int i = i0 + u * FS_THREADS + threadIdx.x;
+        lv[u] = i < a.V ? row[i] : 0.f;
+    }
+    for (int b = threadIdx.x; b < 256; b += FS_THREADS) { sh.hmass[b] = 0ull; sh.hcnt[b] = 0u; sh.hidx[b] = 0xffffffffu; }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < FM_U; ++u) {
+        const int i = i0 + u * FS_THREADS + threadIdx.x;
+        const float z = __fdiv_rn(lv[u], a.T);
+        const uint32_t k = fs_key(z);
+        const bool act = i < a.V && k >= kmin && (k & mask) == prefix;
+        fs_hist_add<MASS>(sh, act, (k >> shift) & 255, MASS && act ? fs_mass(z, zmax) : 0ull);
+        if (IDX && act) atomicMin(&sh.hidx[(k >> shift) & 255], (unsigned)i);
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < 256; b += FS_THREADS) {
+        if (sh.hcnt[b] == 0) continue;
+        atomicAdd(&g.cnt[b], sh.hcnt[b]);
+        if (MASS) atomicAdd(&g.mass[b], sh.hmass[b]);
+        if (IDX) atomicMin(&g.idx[b], sh.hidx[b]);
+    }
+}
+__device__ __forceinline__ uint32_t fm_mask(int shift) { return shift >= 24 ? 0u : 0xffffffffu << (shift + 8); }
+
+// Top-k count level j (shift 24 - 8j): the k-th largest key by a radix descent on counts.
+__global__ void __launch_bounds__(FS_THREADS) k_fm_topk(FmArgs a, int j) {
+    __shared__ FsShared sh;
+    const int r = blockIdx.y;
+    FmState &S = a.st[r];
+    FmHist *H = a.hist + (size_t)r * FM_NLEV;
+    const float *row = a.logits + (size_t)a.rows[a.row0 + r] * a.ld;
+    uint32_t prefix = 0, rem = (unsigned)a.top_k;
+    if (j > 0) {
+        fm_load_hist(sh, H[FM_TOPK + j - 1], false);
+        unsigned int bin, rn;
+        unsigned long long ab;
+        fm_choose<false>(sh, 0ull, 0ull, S.rem[j - 1], bin, ab, rn);
+        prefix = S.prefix[FM_TOPK + j - 1] | (bin << (32 - 8 * j));
+        rem = rn;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) { S.prefix[FM_TOPK + j] = prefix; S.rem[j] = rem; }
+    const int shift = 24 - 8 * j;
+    fm_pass<false, false>(a, sh, row, 0.f, 0u, fm_mask(shift), prefix, shift, H[FM_TOPK + j]);
+}
+
+// The candidates' first level (count and mass by the top key byte), after the top-k cut.
+__global__ void __launch_bounds__(FS_THREADS) k_fm_h1(FmArgs a) {
+    __shared__ FsShared sh;
+    const int r = blockIdx.y;
+    FmState &S = a.st[r];
+    FmHist *H = a.hist + (size_t)r * FM_NLEV;
+    const float *row = a.logits + (size_t)a.rows[a.row0 + r] * a.ld;
+    uint32_t kmin = 0;
+    if (a.top_k > 0 && a.top_k < a.V) {
+        fm_load_hist(sh, H[FM_TOPK + 3], false);
+        unsigned int bin, rn;
+        unsigned long long ab;
+        fm_choose<false>(sh, 0ull, 0ull, S.rem[3], bin, ab, rn);
+        kmin = S.prefix[FM_TOPK + 3] | bin;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) S.kmin = kmin;
+    fm_pass<true, false>(a, sh, row, fs_unkey(S.kmax), kmin, 0u, 0u, 24, H[FM_H1]);
+}
+
+// Total mass F of the candidates (sum of the first-level bins).
+__device__ __forceinline__ unsigned long long fm_total(FsShared &sh, const FmHist &h1) {
+    unsigned long long f = 0;
+    for (int b = threadIdx.x; b < 256; b += FS_THREADS) f += h1.mass[b];
+    return fs_block_sum(f, sh);
+}
+
+// Mass-selection level j (shift 16 - 8j) of the top-p cut (DRAW false) or of the draw (DRAW true).
+template <bool DRAW>
+__global__ void __launch_bounds__(FS_THREADS) k_fm_select(FmArgs a, int j) {
+    __shared__ FsShared sh;
+    const int r = blockIdx.y;
+    FmState &S = a.st[r];
+    FmHist *H = a.hist + (size_t)r * FM_NLEV;
+    const float *row = a.logits + (size_t)a.rows[a.row0 + r] * a.ld;
+    const float zmax = fs_unkey(S.kmax);
+    const int base = DRAW ? FM_DRAW : FM_TOPP;
+    const bool lead = blockIdx.x == 0 && threadIdx.x == 0;
+    unsigned long long target, above;
+    uint32_t prefix;
+    unsigned int bin, rn;
+    if (j == 0) {
+        if (!DRAW) {
+            const unsigned long long F = fm_total(sh, H[FM_H1]);
+            const unsigned long long tp = (unsigned long long)(a.top_p * (double)F);
+            const int on = tp < F;
+            if (lead) { S.F = F; S.tp = tp; S.topp = on; }
+            if (!on) return;
+            target = tp;
+        } else {
+            // the kept mass K: the top-p cut's result when it applied, else the candidates' total
+            unsigned long long K;
+            if (a.top_p < 1.0 && S.topp) {
+                fm_load_hist(sh, H[FM_TOPP + 2], true);
+                fm_choose<true>(sh, S.above[FM_TOPP + 2], S.tp, 0u, bin, above, rn);
+                const uint32_t key = S.prefix[FM_TOPP + 2] | bin;
+                const unsigned long long m = fs_mass(fs_unkey(key), zmax);
+                const unsigned long long rank = m > 0 ? (S.tp - above) / m : 0;
+                K = above + (rank + 1) * m;
+            } else {
+                K = a.top_p < 1.0 ? S.F : fm_total(sh, H[FM_H1]);
+            }
+            unsigned long long tgt = (unsigned long long)(a.u[a.row0 + r] * (double)K);
+            if (tgt >= K) tgt = K - 1;
+            if (lead) { S.K = K; S.tgt = tgt; }
+            target = tgt;
         }
+        fm_load_hist(sh, H[FM_H1], true);
+        fm_choose<true>(sh, 0ull, target, 0u, bin, above, rn);
+        prefix = bin << 24;
+    } else {
+        if (!DRAW && !S.topp) return;
+        target = DRAW ? S.tgt : S.tp;
+        fm_load_hist(sh, H[base + j - 1], true);
+        fm_choose<true>(sh, S.above[base + j - 1], target, 0u, bin, above, rn);
+        prefix = S.prefix[base + j - 1] | (bin << (24 - 8 * j));
     }
-    // ---- the draw
-    unsigned long long tgt = (unsigned long long)(u[s] * (double)K);
-    if (tgt >= K) tgt = K - 1;
-    unsigned long long above, rank;
-    int first = -1;
-    const uint32_t key = fs_select_mass(row, V, T, zmax, kmin, tgt, sh, &above, &rank, &first);
+    if (lead) { S.prefix[base + j] = prefix; S.above[base + j] = above; }
+    const int shift = 16 - 8 * j;
+    if (shift == 0) fm_pass<true, true>(a, sh, row, zmax, S.kmin, fm_mask(0), prefix, 0, H[base + j]);
+    else fm_pass<true, false>(a, sh, row, zmax, S.kmin, fm_mask(shift), prefix, shift, H[base + j]);
+}
+
+// The drawn token: the last draw level's choice, its rank inside the tie group, and its index.
+__global__ void __launch_bounds__(FS_THREADS) k_fm_finish(FmArgs a) {
+    __shared__ FsShared sh;
+    const int r = blockIdx.x;
+    FmState &S = a.st[r];
+    FmHist *H = a.hist + (size_t)r * FM_NLEV;
+    const float *row = a.logits + (size_t)a.rows[a.row0 + r] * a.ld;
+    const float zmax = fs_unkey(S.kmax);
+    fm_load_hist(sh, H[FM_DRAW + 2], true);
+    unsigned int bin, rn;
+    unsigned long long above;
+    fm_choose<true>(sh, S.above[FM_DRAW + 2], S.tgt, 0u, bin, above, rn);
+    const uint32_t key = S.prefix[FM_DRAW + 2] | bin;
+    const unsigned long long m = fs_mass(fs_unkey(key), zmax);
+    const unsigned long long rank = m > 0 ? (S.tgt - above) / m : 0;
     // rank 0 (always, unless the drawn z value is shared by several tokens) is the group's smallest index
-    const int tok = rank == 0 ? first : fs_index_of(row, V, T, key, rank, sh);
-    if (threadIdx.x == 0) out[s] = tok;
+    const int tok = rank == 0 ? (int)H[FM_DRAW + 2].idx[key & 255] : fs_index_of(row, a.V, a.T, key, rank, sh);
+    if (threadIdx.x == 0) a.out[a.row0 + r] = tok;
 }
