@@ -239,8 +239,10 @@ int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32
  * draw (native/vulkan_decode/sampler.hpp:22-57, 93-97) on the GPU: z = fp32(logits / T); top_k > 0 (and < vocab)
  * keeps z >= the k-th largest z (ties kept); top_p < 1 keeps the prefix of the z-descending order (ties by index)
  * whose exclusive cumulative mass is <= top_p of the kept mass; out_dev[s] = the inverse-CDF draw over what is kept
- * with uniform u_dev[s] (masses are 64-bit fixed point, exp(z - z_max) * 2^40, so every sum is exact).  One block
- * per draw; all pointers are device memory.  Errors: NULL pointers, bad sizes, temperature <= 0, top_p <= 0. */
+ * with uniform u_dev[s] (masses are 64-bit fixed point, exp(z - z_max) * 2^40, so every sum is exact).  Each draw
+ * runs over many blocks (a short launch per radix level) with a histogram scratch the library keeps per device: calls
+ * on one device must not overlap.  All pointers are device memory.  Errors: NULL pointers, bad sizes,
+ * temperature <= 0, top_p <= 0. */
 int sp_op_sample_filtered(const float *logits_dev, int32_t vocab, int32_t ld, const int32_t *row_dev,
                           const double *u_dev, int32_t n, double temperature, int32_t top_k, double top_p,
                           int32_t *out_dev, void *hip_stream);
