@@ -175,7 +175,7 @@ def sampling_cost(eng, V, rows=16, reps=20):
 
 
 TRAFFIC_FILE = ROOT / 'profiles' / 'k_gemv_q8_gate_up_traffic.md'
-GEMV_SOURCES = ('sp_gemv.h', 'sp_device.h', 'sp_pack.h')
+GEMV_SOURCES = ('sp_gemv1.h', 'sp_gemv.h', 'sp_device.h', 'sp_pack.h')
 
 
 def gemv_source_hash():
