@@ -254,7 +254,7 @@ def gemv_roofline(eng):
     traffic, source = measured_traffic()
     return {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM / 1e9, 'unit': 'GB/s',
             'frac': round(achieved * 1e9 / PEAK_HBM, 4), 'traffic': traffic, 'traffic_source': source,
-            'kernel': 'k_gemv<Q8, 1 m-tile, gate+up pair> (SwiGLU gate_up, 17920x1536 int8 + scales)',
+            'kernel': 'k_gemv1<Q8, gate+up pair, 3 k-tiles per wave> (SwiGLU gate_up, 17920x1536 int8 + scales, 1 column)',
             'bytes_per_launch': gbytes, 'avg_launch_us': round(us, 3)}
 
 

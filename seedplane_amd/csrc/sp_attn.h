@@ -697,18 +697,19 @@ struct AttnMqArgs {
     int splits;            // blocks per (chunk, kv head, group); block s takes row tiles 4s .. 4s+3
 };
 
-template <int HD, int G>
+template <int HD, int G, int CH>
 __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
-    constexpr int KP = HD + 8, VP = ATT_CH + 8;      // padded rows (halves): 68 / 36 dwords, 16-byte aligned
+    constexpr int KP = HD + 8, VP = CH + 8;          // padded rows (halves), 16-byte aligned
+    constexpr int NST = CH / 16, NS2 = CH / 32, NP2 = CH / 2;   // key tiles, P.V k-steps, key pairs
     constexpr int ST = HD / 32;                      // MFMA k-steps over head dim
     constexpr int CPR = HD / 8;                      // 16-byte pieces per key row
-    constexpr int KPER = ATT_CH * CPR / 256;         // K pieces per thread
-    constexpr int VPER = ATT_CH / 2 * CPR / 256;     // V (key pair, piece) items per thread
-    static_assert(KPER * 256 == ATT_CH * CPR && VPER * 256 == ATT_CH / 2 * CPR, "chunk staging split");
-    __shared__ __align__(16) f16 k_s[ATT_CH][KP];
+    constexpr int KPER = CH * CPR / 256;         // K pieces per thread
+    constexpr int VPER = CH / 2 * CPR / 256;     // V (key pair, piece) items per thread
+    static_assert(KPER * 256 == CH * CPR && VPER * 256 == CH / 2 * CPR, "chunk staging split");
+    __shared__ __align__(16) f16 k_s[CH][KP];
     __shared__ __align__(16) f16 vt_s[HD][VP];
     __shared__ __align__(16) f16 p_s[4][16][VP];
-    __shared__ int kpos_s[ATT_CH];                  // ring position of key j, or -(1 + tree index), or INT_MIN
+    __shared__ int kpos_s[CH];                  // ring position of key j, or -(1 + tree index), or INT_MIN
     __shared__ int clo_s[64], chi_s[64], ctc_s[64];
     __shared__ unsigned long long cmask_s[64];
 
@@ -716,11 +717,11 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     const int split = blockIdx.z % a.splits;
     const AttnGroup gr = a.groups[blockIdx.z / a.splits];
     const int nvis = gr.nlin + gr.tree_count;
-    const int v0 = c * ATT_CH;
+    const int v0 = c * CH;
     if (v0 >= nvis) return;
     const int R = gr.ncols * G;
     if (split * 64 >= R) return;                    // 4 row tiles of 16 rows per block
-    const int cnt = min(ATT_CH, nvis - v0);
+    const int cnt = min(CH, nvis - v0);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r16 = lane & 15, g4 = lane >> 4;
     const int n_tiles = (R + 15) / 16;
@@ -733,9 +734,9 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     // block and a conditional subtraction per key replace a division per key (branch-free: the selects keep the
     // wave converged).
     const int lin_base = (gr.lo + v0) % a.n_slots;   // slot of visible key v0 when it is a ring key
-    auto wrap = [&](int x) {                         // x mod n_slots for 0 <= x < n_slots + ATT_CH
+    auto wrap = [&](int x) {                         // x mod n_slots for 0 <= x < n_slots + CH
         x = x >= a.n_slots ? x - a.n_slots : x;
-        return a.n_slots >= ATT_CH ? x : x % a.n_slots;
+        return a.n_slots >= CH ? x : x % a.n_slots;
     };
     auto key_at = [&](int j, int &kp) {
         const int vis = v0 + j;
@@ -747,7 +748,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
 
     // ---- every global load before the first LDS store.  Keys past cnt load key 0 of the chunk (clamped address,
     // unconditional load) and are replaced by zeros.  K: item i = key i / CPR, piece i % CPR.  V: item i = key pair
-    // i % 32, piece i / 32 (a wave's 64 items: 32 key pairs x 2 pieces, see the transposed store below).
+    // i % (CH / 2), piece i / (CH / 2) (see the transposed store below).
     f16x8 kf[KPER], vf[VPER][2];
 #pragma unroll
     for (int i = 0; i < KPER; ++i) {
@@ -758,7 +759,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < VPER; ++i) {
-        const int idx = tid + 256 * i, kp2 = idx & 31, ch = idx >> 5;
+        const int idx = tid + 256 * i, kp2 = idx % NP2, ch = idx / NP2;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int j = 2 * kp2 + h;
@@ -789,8 +790,8 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     const sp_token ct = a.toks[gr.first_col + min(tid, gr.ncols - 1)];
 
     // ---- LDS: K row-major; V transposed, two keys per dword: lane (key pair p, piece ch) writes the dword holding
-    // keys 2p, 2p+1 of dims 8ch .. 8ch+7.  A wave's 32 pairs x 2 pieces hit 64 distinct banks (the two pieces' rows
-    // are 8 * 36 dwords apart).
+    // keys 2p, 2p+1 of dims 8ch .. 8ch+7.  A wave's 64 items hit 64 distinct banks (64-key chunks: 32 pairs x 2
+    // pieces whose rows are 8 * 36 dwords apart; 128-key chunks: 64 consecutive pairs of one row).
 #pragma unroll
     for (int i = 0; i < KPER; ++i) {
         const int idx = tid + 256 * i, j = idx / CPR, ch = idx - j * CPR;
@@ -798,7 +799,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < VPER; ++i) {
-        const int idx = tid + 256 * i, kp2 = idx & 31, ch = idx >> 5;
+        const int idx = tid + 256 * i, kp2 = idx % NP2, ch = idx / NP2;
         const f16x8 va = 2 * kp2 < cnt ? vf[i][0] : zero8, vb = 2 * kp2 + 1 < cnt ? vf[i][1] : zero8;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -806,7 +807,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
             *(f16x2 *)&vt_s[ch * 8 + e][2 * kp2] = pr;
         }
     }
-    if (tid < ATT_CH) {
+    if (tid < CH) {
         int kp = INT_MIN;
         if (tid < cnt) (void)key_at(tid, kp);
         kpos_s[tid] = kp;
@@ -816,9 +817,9 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     if (!active) return;                             // no block-wide barrier follows
 
     // ---- S = Q K^T: 4 slot tiles of 16; lane holds S[row 4*g4 + j][slot 16*st + r16]
-    f32x4 sc[4];
+    f32x4 sc[NST];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
+    for (int st = 0; st < NST; ++st) {
         f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < ST; ++s) {
@@ -830,9 +831,9 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     // ---- mask, chunk-local max / exp / sum per row.  The key codes of the lane's 4 slot tiles and the range / tree
     // bits of its 4 rows are read once; the mask is selects only (ring key: inside the column's range; tree key:
     // its bit set in the column's ancestor mask; padding key: never).
-    int kpv[4];
+    int kpv[NST];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) kpv[st] = kpos_s[16 * st + r16];
+    for (int st = 0; st < NST; ++st) kpv[st] = kpos_s[16 * st + r16];
     int clo[4], chi[4], ctc[4];
     unsigned long long cmk[4];
 #pragma unroll
@@ -847,7 +848,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
         const int row = rt * 16 + 4 * g4 + j;
         float m = -INFINITY;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
+        for (int st = 0; st < NST; ++st) {
             const int kp = kpv[st];
             const int tj = ~kp;                      // tree index of a tree key (kp = ~tj < 0)
             const bool in_ring = (kp >= clo[j]) & (kp <= chi[j]);
@@ -860,7 +861,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
         m = row16_max(m);
         float l = 0.f;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
+        for (int st = 0; st < NST; ++st) {
             const float e = (m == -INFINITY || sc[st][j] == -INFINITY) ? 0.f : expf(sc[st][j] - m);
             sc[st][j] = e;
             l += e;
@@ -870,20 +871,20 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     }
     // ---- P (fp16) to this wave's LDS rows, read back as the A operand (LDS is in order within a wave)
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
+    for (int st = 0; st < NST; ++st)
 #pragma unroll
         for (int j = 0; j < 4; ++j) p_s[wv][4 * g4 + j][16 * st + r16] = (f16)sc[st][j];
     __builtin_amdgcn_wave_barrier();
-    f16x8 pa[2];
+    f16x8 pa[NS2];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) pa[s2] = *(const f16x8 *)&p_s[wv][r16][32 * s2 + 8 * g4];
+    for (int s2 = 0; s2 < NS2; ++s2) pa[s2] = *(const f16x8 *)&p_s[wv][r16][32 * s2 + 8 * g4];
     // ---- O = P V over HD/16 dim tiles; lane holds O[row 4*g4 + j][dim 16*dt + r16]
     f32x4 o[HD / 16];
 #pragma unroll
     for (int dt = 0; dt < HD / 16; ++dt) {
         o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < NS2; ++s2) {
             const f16x8 vb = *(const f16x8 *)&vt_s[16 * dt + r16][32 * s2 + 8 * g4];
             o[dt] = mfma16(pa[s2], vb, o[dt]);
         }

@@ -333,18 +333,27 @@ void launch_attn_rope_hd(int G, dim3 grid, hipStream_t st, const AttnArgs &a, co
     }
 }
 
-template <int HD>
-void launch_attn_mq_hd(int G, dim3 grid, hipStream_t st, const AttnMqArgs &a) {
+// Keys per multi-query block (one partial record per block and row): 128 for tree groups (verify pass: 33 x 12
+// query rows, fewer and larger blocks, half the records to merge; -1 % per pass), 64 otherwise (the plain batches
+// and prefill chunks got slower with 128: bs16 +16 %, prefill +3 %).  g_mq_ch != 0 forces one size (sweeps).
+int g_mq_ch = 0;
+template <int HD, int CH>
+void launch_attn_mq_ch(int G, dim3 grid, hipStream_t st, const AttnMqArgs &a) {
     switch (G) {
-        case 1: hipLaunchKernelGGL((k_attn_mq<HD, 1>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((k_attn_mq<HD, 2>), grid, dim3(256), 0, st, a); break;
-        case 3: hipLaunchKernelGGL((k_attn_mq<HD, 3>), grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((k_attn_mq<HD, 4>), grid, dim3(256), 0, st, a); break;
-        case 5: hipLaunchKernelGGL((k_attn_mq<HD, 5>), grid, dim3(256), 0, st, a); break;
-        case 6: hipLaunchKernelGGL((k_attn_mq<HD, 6>), grid, dim3(256), 0, st, a); break;
-        case 7: hipLaunchKernelGGL((k_attn_mq<HD, 7>), grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL((k_attn_mq<HD, 8>), grid, dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((k_attn_mq<HD, 1, CH>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((k_attn_mq<HD, 2, CH>), grid, dim3(256), 0, st, a); break;
+        case 3: hipLaunchKernelGGL((k_attn_mq<HD, 3, CH>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((k_attn_mq<HD, 4, CH>), grid, dim3(256), 0, st, a); break;
+        case 5: hipLaunchKernelGGL((k_attn_mq<HD, 5, CH>), grid, dim3(256), 0, st, a); break;
+        case 6: hipLaunchKernelGGL((k_attn_mq<HD, 6, CH>), grid, dim3(256), 0, st, a); break;
+        case 7: hipLaunchKernelGGL((k_attn_mq<HD, 7, CH>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_attn_mq<HD, 8, CH>), grid, dim3(256), 0, st, a); break;
     }
+}
+template <int HD>
+void launch_attn_mq_hd(int G, int ch, dim3 grid, hipStream_t st, const AttnMqArgs &a) {
+    if (ch == 128) launch_attn_mq_ch<HD, 128>(G, grid, st, a);
+    else launch_attn_mq_ch<HD, 64>(G, grid, st, a);
 }
 
 template <class F>
@@ -478,6 +487,7 @@ struct sp_engine {
         bool dec = false;        // every column a plain ring range (no tree block): k_attn_dec over key splits
         bool dec_direct = false; // ... and every column fits one split: no combine
         bool rope_fused = false; // chunk kernel with RoPE / KV write folded in (plain columns of distinct sequences)
+        int mq_ch = ATT_CH;      // keys per multi-query block
         int ngroups = 0, nchunk = 1, splits = 1;
         std::vector<AttnGroup> groups;
         std::vector<int> colnc;
@@ -609,8 +619,11 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
     p.colnc.assign(n, 0);
     int mx = 1;
     if (p.mq) {
+        bool trees = true;
+        for (auto &g : p.groups) trees = trees && g.tree_count > 0;
+        p.mq_ch = g_mq_ch ? g_mq_ch : (trees ? 128 : ATT_CH);
         for (auto &g : p.groups) {
-            const int nc = (g.nlin + g.tree_count + ATT_CH - 1) / ATT_CH;
+            const int nc = (g.nlin + g.tree_count + p.mq_ch - 1) / p.mq_ch;
             for (int c = 0; c < g.ncols; ++c) p.colnc[g.first_col + c] = nc;
             mx = std::max(mx, nc);
         }
@@ -620,7 +633,8 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
             mx = std::max(mx, p.colnc[c]);
         }
     }
-    p.nchunk = graph ? max_nchunk : mx;
+    // a recorded graph serves every later length: its grid covers the longest visible list the slots allow
+    p.nchunk = graph ? (p.mq ? (max_nchunk * ATT_CH + p.mq_ch - 1) / p.mq_ch : max_nchunk) : mx;
     if (!p.mq && dec_cols) {
         // the MFMA decode kernel pays off once its key splits fill the chip (long contexts, large batches); short
         // ranges stay on the 64-key chunk kernel, which spreads them over more CUs
@@ -693,8 +707,8 @@ void sp_engine::launch_attention(int l, int n, const AttnPlan &ap, int mtp, hipS
     if (ap.mq) {
         AttnMqArgs am{q, kc[l], vc[l], dtoks, dgroups, NH, NKV, HD, n_slots, nchunk, scale, attn_part, ap.splits};
         dim3 agrid(nchunk, NKV, ap.ngroups * ap.splits);
-        if (HD == 64) launch_attn_mq_hd<64>(G, agrid, st, am);
-        else launch_attn_mq_hd<128>(G, agrid, st, am);
+        if (HD == 64) launch_attn_mq_hd<64>(G, ap.mq_ch, agrid, st, am);
+        else launch_attn_mq_hd<128>(G, ap.mq_ch, agrid, st, am);
     } else if (ap.dec) {
         AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, scale, attn_part};
         launch_attn_dec(HD, dim3(NKV, n, nchunk), st, aa, attn, NH * HD, ap.dec_direct ? 1 : 0, mtp);
@@ -1073,7 +1087,8 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             // would otherwise see as idle GPU time.
             const int L = d.n_layers;
             const int cuts[4] = {0, std::min(1, L), std::min(5, L), L};
-            const int plan_code = ap.mq ? ap.ngroups * 1024 + ap.splits : (ap.dec ? (ap.dec_direct ? -3 : -2) : (ap.rope_fused ? -4 : -1));
+            const int plan_code = ap.mq ? (ap.mq_ch == 128 ? 1 << 20 : 0) + ap.ngroups * 1024 + ap.splits
+                                        : (ap.dec ? (ap.dec_direct ? -3 : -2) : (ap.rope_fused ? -4 : -1));
             int total = 0;
             for (int part = 0; part < 3; ++part) {
                 if (cuts[part] >= cuts[part + 1]) continue;      // empty (short models); the head ran in its part
@@ -1142,6 +1157,7 @@ void sp_debug_one_plan(int qs, int qw, int ds, int dw, int gw) {
     g_tune_one[0] = qs; g_tune_one[1] = qw; g_tune_one[2] = ds; g_tune_one[3] = dw; g_tune_one[4] = gw;
 }
 void sp_debug_attn_plan(int nwv, int sub) { g_tune_attn[0] = nwv; g_tune_attn[1] = sub; }
+void sp_debug_mq_ch(int ch) { g_mq_ch = ch == 128 ? 128 : ch == 64 ? 64 : 0; }
 #endif
 
 int sp_engine_logits(sp_engine *e, float **logits_dev) {
