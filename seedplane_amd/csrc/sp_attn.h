@@ -34,9 +34,17 @@ __device__ __forceinline__ float packed_elem(const uint8_t *w, const f16 *sz, in
 // of column b is feed[b] (the previous step's argmax of that column, kept on the device), clamped to the vocabulary.
 template <int FMT>
 __global__ void __launch_bounds__(256) k_embed(const uint8_t *w, const f16 *sz, int nkt, const sp_token *toks,
-                                               int H, float *x, int ldx, const int *feed, int vocab) {
+                                               int H, float *x, int ldx, const int *feed, int vocab,
+                                               const float *inv_freq, int half, float2 *rtab) {
     const int b = blockIdx.x, tok = feed ? min(max(feed[b], 0), vocab - 1) : toks[b].token;
     for (int k = threadIdx.x; k < H; k += blockDim.x) x[(size_t)b * ldx + k] = packed_elem<FMT>(w, sz, nkt, tok, k);
+    // the step's rotation table: (cos, sin) of phase = float(pos) * inv_freq[j] for every column, computed once here
+    // and read by the RoPE steps of every layer (the same values they would compute themselves)
+    const float fpos = (float)toks[b].pos;
+    for (int j = threadIdx.x; j < half; j += blockDim.x) {
+        const float ph = fpos * inv_freq[j];
+        rtab[(size_t)b * half + j] = make_float2(cosf(ph), sinf(ph));
+    }
 }
 
 // out[b][k] = fp16(x * rsqrt(mean(x^2) + eps) * w).  Replaces Qwen2Engine._norm (qwen_engine.py:90-92): the weight
@@ -85,7 +93,7 @@ __global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, con
 struct RopeArgs {
     const float *qkv;       // [n][Nqkv] fp32 (bias already added) when nparts == 0
     int Nqkv, NH, NKV, HD;
-    const float *inv_freq;  // [HD/2]
+    const float2 *rtab;     // [n][HD/2] (cos, sin) of float(pos) * inv_freq, from the step's embedding kernel
     const sp_token *toks;
     float *q;               // [n][NH*HD] fp32, rotated
     f16 *kc, *vc;           // this layer's K/V: [seq][kvh][slot][HD]
@@ -118,11 +126,10 @@ __global__ void __launch_bounds__(ROPE_THREADS) k_rope_kv(RopeArgs a) {
     const int b = blockIdx.x;
     const sp_token t = a.toks[b];
     const int half = a.HD >> 1;
-    const float fpos = (float)t.pos;
     for (int idx = threadIdx.x; idx < (a.NH + a.NKV) * half; idx += blockDim.x) {
         const int head = idx / half, i = idx - head * half;
-        const float ph = fpos * a.inv_freq[i];
-        const float c = cosf(ph), s = sinf(ph);
+        const float2 cs = a.rtab[(size_t)b * half + i];
+        const float c = cs.x, s = cs.y;
         const float x1 = qkv_value<NP>(a, b, head * a.HD + i), x2 = qkv_value<NP>(a, b, head * a.HD + i + half);
         const float o1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(-x2, s));
         const float o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
@@ -283,7 +290,6 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
         kr[k] = *(const f16x8 *)(a.kc + off);
         vr[k] = *(const f16x8 *)(a.vc + off);
     }
-    const float fpos = (float)t.pos;
     // queries of the group (then the key of the newest position, in the owning block) are rotated; the owning block
     // also stores the new value.  Every projection load of the thread (all slices and the bias of its rotation pairs
     // and of its value dim) is issued in one batch from clamped indices before the first add, so the owning block
@@ -294,6 +300,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
     const float *prow = np == 0 ? r.qkv + (size_t)b * r.Nqkv : r.part + (size_t)b * r.Nqkv;
     const size_t pstr = np == 0 ? 0 : r.pstride;
     float t1[RI][8], t2[RI][8], bb1[RI], bb2[RI], tv[8], bv = 0.f;
+    float2 tw[RI];
     int id1[RI];
 #pragma unroll
     for (int ri = 0; ri < RI; ++ri) {
@@ -310,6 +317,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
         }
         bb1[ri] = np == 0 ? 0.f : r.bias[id1[ri]];
         bb2[ri] = np == 0 ? 0.f : r.bias[id1[ri] + HALF];
+        tw[ri] = r.rtab[(size_t)b * HALF + j];
     }
     const int vidx = (a.NH + a.NKV + kvh) * HD + min(tid, HD - 1);
 #pragma unroll
@@ -328,8 +336,7 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
         const int i = tid + ri * NT;
         if (i >= nrot) break;
         const int hh = i / HALF, j = i - hh * HALF;
-        const float ph = fpos * r.inv_freq[j];
-        const float cs = cosf(ph), sn = sinf(ph);
+        const float cs = tw[ri].x, sn = tw[ri].y;
         const float x1 = sum_of(t1[ri], bb1[ri]), x2 = sum_of(t2[ri], bb2[ri]);
         const float o1 = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(-x2, sn));
         const float o2 = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));

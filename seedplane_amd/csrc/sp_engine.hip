@@ -417,8 +417,9 @@ void launch_attn_dec(int HD, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 
 
 template <int FMT>
 void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x, hipStream_t st, const int *feed,
-                  int vocab) {
-    hipLaunchKernelGGL((k_embed<FMT>), dim3(n), dim3(256), 0, st, m.w, m.sz, m.nkt, toks, H, x, H, feed, vocab);
+                  int vocab, const float *inv_freq, int half, float2 *rtab) {
+    hipLaunchKernelGGL((k_embed<FMT>), dim3(n), dim3(256), 0, st, m.w, m.sz, m.nkt, toks, H, x, H, feed, vocab,
+                       inv_freq, half, rtab);
 }
 
 }  // namespace
@@ -444,6 +445,7 @@ struct sp_engine {
     // activations
     int Nqkv = 0, maxT = 0, max_nchunk = 0;
     float *x = nullptr, *qkv = nullptr, *q = nullptr, *logits = nullptr, *attn_part = nullptr;
+    float2 *rtab = nullptr;      // the step's RoPE (cos, sin) per column and frequency, written by the embedding kernel
     float *gpart = nullptr;      // split-K GEMV slices [GEMV_MAX_SLICES][maxT][max(H, Nqkv)]
     size_t gpart_stride = 0;
     // single-column steps with the norms / combine folded into the GEMVs: the residual alternates between x (layer
@@ -511,7 +513,7 @@ void sp_engine::free_all() {
     layers.clear();
     embed.release(); head.release();
     dev_free(final_norm); dev_free(inv_freq);
-    for (void *p : {(void *)x, (void *)x2, (void *)qkv, (void *)q, (void *)logits, (void *)attn_part, (void *)gpart,
+    for (void *p : {(void *)x, (void *)x2, (void *)qkv, (void *)q, (void *)rtab, (void *)logits, (void *)attn_part, (void *)gpart,
                     (void *)gpart2, (void *)xn, (void *)attn,
                     (void *)act, (void *)am_v, (void *)am_i, (void *)am_out,
                     (void *)d_upload, (void *)d_kl, (void *)d_vl, (void *)d_move})
@@ -544,6 +546,8 @@ void sp_engine::alloc_activations() {
     gpart2 = dev_alloc<float>(GEMV_MAX_SLICES * gpart_stride);
     x2 = dev_alloc<float>((size_t)maxT * H);
     q = dev_alloc<float>((size_t)maxT * d.n_heads * d.head_dim);
+    rtab = dev_alloc<float2>((size_t)maxT * (d.head_dim / 2));
+    HIPCHK(hipMemset(rtab, 0, (size_t)maxT * (d.head_dim / 2) * sizeof(float2)));
     attn = dev_alloc<f16>(tpad * d.n_heads * d.head_dim);
     act = dev_alloc<f16>(tpad * I);
     logits = dev_alloc<float>((size_t)maxT * V);
@@ -730,9 +734,9 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
     const int *feed = (flags & SP_F_FEED) ? am_out : nullptr;   // tokens = the previous step's argmax ids
     if (l0 == 0) {
         switch (embed.fmt) {
-            case 1: launch_embed<1>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
-            case 2: launch_embed<2>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
-            default: launch_embed<3>(embed, dtoks, n, H, x, st, feed, d.vocab); break;
+            case 1: launch_embed<1>(embed, dtoks, n, H, x, st, feed, d.vocab, inv_freq, HD / 2, rtab); break;
+            case 2: launch_embed<2>(embed, dtoks, n, H, x, st, feed, d.vocab, inv_freq, HD / 2, rtab); break;
+            default: launch_embed<3>(embed, dtoks, n, H, x, st, feed, d.vocab, inv_freq, HD / 2, rtab); break;
         }
     }
     const bool logits_on = flags & SP_F_LOGITS;
@@ -782,7 +786,7 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
             sq = launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, qpart, ps, PRO_NONE, nullptr,
                              qkv_s, qkv_w, mtp);
         }
-        RopeArgs ra{qkv, Nqkv, NH, NKV, HD, inv_freq, dtoks, q, kc[l], vc[l], n_slots, qpart, ps, ly.qkv_b};
+        RopeArgs ra{qkv, Nqkv, NH, NKV, HD, rtab, dtoks, q, kc[l], vc[l], n_slots, qpart, ps, ly.qkv_b};
         const bool fused = ap.rope_fused && logits_on;
         if (!fused) launch_rope(n, ra, sq, st);
         if (l + 1 == d.n_layers && !logits_on) break;   // K/V-only: the last layer only needs its K/V
