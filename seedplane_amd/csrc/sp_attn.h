@@ -399,8 +399,8 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
 }
 
 // Decode attention on MFMA for columns whose keys are one ring range (no tree block).  One block per (kv head, column,
-// split of NWV * SUB * DEC_KC keys); wave w owns SUB * DEC_KC consecutive keys of the split and issues all of their
-// K and V loads before the first use (one memory round trip per block).  Per sub-chunk of DEC_KC keys: S = Q K^T on
+// split of NWV * SUB * DEC_KC keys); wave w owns SUB * DEC_KC consecutive keys of the split and streams them with two
+// sub-chunks of K / V loads in flight while it computes.  Per sub-chunk of DEC_KC keys: S = Q K^T on
 // MFMA (rows = the G query heads of the kv head, K fragments straight from the cache), online softmax per row, P and
 // V^T staged in the wave's own LDS region, O += P V on MFMA.  The wave states are merged in wave order; a column
 // whose keys fit one split gets its fp16 attention row directly, otherwise each split writes {m, l, acc / l} in
@@ -425,11 +425,13 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
     const int v_lo = b_lo + w * DEC_KW, v_hi = min(nlin, v_lo + DEC_KW);
     const size_t head_base = ((size_t)t.seq * a.NKV + kvh) * a.n_slots;
     const f16x8 zero8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    // ---- every load of the wave: K fragments (lane: key r16 of a 16-key tile, dims g4 * 8 ..) and V rows (lane:
-    // key lane / 2 of a sub-chunk, dims (lane & 1) * HD/2 ..)
-    f16x8 kf[DEC_SUB][2][ST], vf[DEC_SUB][VPL];
-#pragma unroll
-    for (int sc = 0; sc < DEC_SUB; ++sc) {
+    // ---- the wave's K / V stream: sub-chunk sc's loads (K fragments -- lane: key r16 of a 16-key tile, dims g4 * 8 ..
+    // -- and V rows -- lane: key lane / 2, dims (lane & 1) * HD/2 .., the layout whose transposed LDS stores are
+    // conflict-free) land in register slot sc % 2; the loads of
+    // sub-chunk sc + 2 are issued as soon as sub-chunk sc has been consumed, so two sub-chunks are always in flight
+    // while the wave computes (loads complete in order, so each use waits only for its own sub-chunk)
+    f16x8 kf[2][2][ST], vf[2][VPL];
+    auto load_sub = [&](int sc, int slot) {
         const int v0 = v_lo + sc * DEC_KC;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
@@ -437,14 +439,16 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
             const bool live = key < v_hi;
             const size_t off = (head_base + (size_t)((t.ctx_lo + (live ? key : 0)) % a.n_slots)) * HD + g4 * 8;
 #pragma unroll
-            for (int st = 0; st < ST; ++st) kf[sc][kt][st] = live ? *(const f16x8 *)(a.kc + off + st * 32) : zero8;
+            for (int st = 0; st < ST; ++st) kf[slot][kt][st] = live ? *(const f16x8 *)(a.kc + off + st * 32) : zero8;
         }
         const int key = v0 + (lane >> 1);
         const bool live = key < v_hi;
         const size_t off = (head_base + (size_t)((t.ctx_lo + (live ? key : 0)) % a.n_slots)) * HD + (lane & 1) * (HD / 2);
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) vf[sc][i] = live ? *(const f16x8 *)(a.vc + off + i * 8) : zero8;
-    }
+        for (int i = 0; i < VPL; ++i) vf[slot][i] = live ? *(const f16x8 *)(a.vc + off + i * 8) : zero8;
+    };
+    load_sub(0, 0);
+    if (DEC_SUB > 1) load_sub(1, 1);
     // Q fragments (rows = query heads of this kv head, scaled, fp16): unconditional vector loads from a clamped row
     // (a load under a per-lane condition is issued and waited for one at a time)
     f16x8 qa[ST];
@@ -471,18 +475,20 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
 #pragma unroll
     for (int sc = 0; sc < DEC_SUB; ++sc) {
         const int v0 = v_lo + sc * DEC_KC;
-        if (v0 >= v_hi) break;
+        if (v0 >= v_hi) break;                               // wave-uniform
+        const int slot = sc & 1;
 #pragma unroll
         for (int i = 0; i < VPL; ++i)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vt[w][(lane & 1) * (HD / 2) + i * 8 + e][lane >> 1] = vf[sc][i][e];
+            for (int e = 0; e < 8; ++e) vt[w][(lane & 1) * (HD / 2) + i * 8 + e][lane >> 1] = vf[slot][i][e];
         f32x4 sc2[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             sc2[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int st = 0; st < ST; ++st) sc2[kt] = mfma16(qa[st], kf[sc][kt][st], sc2[kt]);
+            for (int st = 0; st < ST; ++st) sc2[kt] = mfma16(qa[st], kf[slot][kt][st], sc2[kt]);
         }
+        if (sc + 2 < DEC_SUB) load_sub(sc + 2, slot);      // the slot's registers are consumed: refill them
         // online softmax: lane holds rows 4 g4 + j, keys v0 + kt * 16 + r16
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

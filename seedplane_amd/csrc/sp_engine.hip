@@ -389,30 +389,41 @@ void launch_rope(int n, const RopeArgs &ra, int np, hipStream_t st) {
 int g_tune_attn[2] = {0, 0};
 #endif
 struct DecShape { int nwv, sub; };
-DecShape dec_shape() {
+// Keys per decode-attention block: 1024 (2 waves streaming 16 sub-chunks of 32 keys, two sub-chunks of loads in
+// flight per wave) when the ranges give the chip at least two such blocks per CU, else 256 (4 waves x 2 sub-chunks).
+// 32 columns of 8260 keys, 4 kv heads: 126 -> 111 us per launch.
+DecShape dec_shape(int kpb) {
 #ifdef SP_GEMV_TUNE
     if (g_tune_attn[0] > 0) return DecShape{g_tune_attn[0], g_tune_attn[1]};
 #endif
-    return DecShape{4, 2};
+    return kpb >= 1024 ? DecShape{2, 16} : DecShape{4, 2};
 }
-int dec_keys_per_block() { const DecShape d = dec_shape(); return d.nwv * d.sub * DEC_KC; }
+int dec_keys(const DecShape &d) { return d.nwv * d.sub * DEC_KC; }
+// The routing between the attention kernels (plan_attention) counts work in splits of this many keys (the sweeps
+// that set its thresholds used 256-key blocks); the decode kernel's own grid uses its shape's key count.
+constexpr int DEC_ROUTE_KEYS = 256;
 
 template <int HD>
-void launch_attn_dec_hd(dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct, int mtp) {
-    const DecShape d = dec_shape();
+void launch_attn_dec_hd(int kpb, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct, int mtp) {
+    const DecShape d = dec_shape(kpb);
 #ifdef SP_GEMV_TUNE
     if (d.nwv == 1 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 1>), grid, dim3(64), 0, st, aa, out, ldo, direct, mtp); return; }
     if (d.nwv == 2 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 1>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp); return; }
     if (d.nwv == 4 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 1>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
     if (d.nwv == 2 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 2>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp); return; }
     if (d.nwv == 1 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 2>), grid, dim3(64), 0, st, aa, out, ldo, direct, mtp); return; }
+    if (d.nwv == 4 && d.sub == 4) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 4>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
+    if (d.nwv == 4 && d.sub == 8) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 8>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
+    if (d.nwv == 4 && d.sub == 16) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 16>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
+    if (d.nwv == 2 && d.sub == 8) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 8>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp); return; }
 #endif
-    (void)d;
-    hipLaunchKernelGGL((k_attn_dec<HD, 4, 2>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp);
+    if (d.nwv == 2 && d.sub == 16) hipLaunchKernelGGL((k_attn_dec<HD, 2, 16>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp);
+    else hipLaunchKernelGGL((k_attn_dec<HD, 4, 2>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp);
 }
-void launch_attn_dec(int HD, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct, int mtp) {
-    if (HD == 64) launch_attn_dec_hd<64>(grid, st, aa, out, ldo, direct, mtp);
-    else launch_attn_dec_hd<128>(grid, st, aa, out, ldo, direct, mtp);
+void launch_attn_dec(int HD, int kpb, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct,
+                     int mtp) {
+    if (HD == 64) launch_attn_dec_hd<64>(kpb, grid, st, aa, out, ldo, direct, mtp);
+    else launch_attn_dec_hd<128>(kpb, grid, st, aa, out, ldo, direct, mtp);
 }
 
 template <int FMT>
@@ -490,6 +501,7 @@ struct sp_engine {
         bool dec_direct = false; // ... and every column fits one split: no combine
         bool rope_fused = false; // chunk kernel with RoPE / KV write folded in (plain columns of distinct sequences)
         int mq_ch = ATT_CH;      // keys per multi-query block
+        int dec_kpb = 256;       // keys per decode-attention block
         int ngroups = 0, nchunk = 1, splits = 1;
         std::vector<AttnGroup> groups;
         std::vector<int> colnc;
@@ -605,12 +617,12 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
     dec_ok = g_tune_attn[0] >= 0;
     force = g_tune_attn[0] > 0;
 #endif
-    // blocks per kv head and column: decode key splits of dec_keys_per_block() keys, chunk-kernel blocks of ATT_CH
+    // blocks per kv head and column: decode key splits of DEC_ROUTE_KEYS keys, chunk-kernel blocks of ATT_CH
     long dec_work = 0, chunk_work = 0;
     bool dec_cols = G <= 8 && dec_ok;
     for (int c = 0; c < n; ++c) {
         dec_cols = dec_cols && t[c].tree_count == 0 && nlin_of(t[c]) >= 1;
-        dec_work += (long)(nlin_of(t[c]) + dec_keys_per_block() - 1) / dec_keys_per_block() * d.n_kv_heads;
+        dec_work += (long)(nlin_of(t[c]) + DEC_ROUTE_KEYS - 1) / DEC_ROUTE_KEYS * d.n_kv_heads;
         chunk_work += (long)(nlin_of(t[c]) + ATT_CH - 1) / ATT_CH * d.n_kv_heads;
     }
     // several plain columns whose 64-key chunks fill the chip but whose decode splits would not give each CU a few
@@ -657,13 +669,17 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
         p.rope_fused = plain && std::adjacent_find(seqs.begin(), seqs.end()) == seqs.end();
     }
     if (p.dec) {
-        // splits of dec_keys_per_block() keys; a graph is sized for the longest range the ring allows
+        long big = 0;                    // blocks of the 1024-key shape
+        for (int c = 0; c < n; ++c) big += (long)(nlin_of(t[c]) + 1023) / 1024 * d.n_kv_heads;
+        const int kpb = dec_keys(dec_shape(big >= 512 ? 1024 : 256));
+        p.dec_kpb = kpb;
+        // splits of kpb keys; a graph is sized for the longest range the ring allows
         int ms = 1;
         for (int c = 0; c < n; ++c) {
-            p.colnc[c] = (nlin_of(t[c]) + dec_keys_per_block() - 1) / dec_keys_per_block();
+            p.colnc[c] = (nlin_of(t[c]) + kpb - 1) / kpb;
             ms = std::max(ms, p.colnc[c]);
         }
-        p.nchunk = graph ? (n_slots + dec_keys_per_block() - 1) / dec_keys_per_block() : ms;
+        p.nchunk = graph ? (n_slots + kpb - 1) / kpb : ms;
         p.dec_direct = p.nchunk == 1;
         if (p.nchunk > max_nchunk || p.nchunk > ATT_MAX_CHUNKS) {      // splits must fit the partial buffer
             p.dec = p.dec_direct = false;
@@ -715,7 +731,7 @@ void sp_engine::launch_attention(int l, int n, const AttnPlan &ap, int mtp, hipS
         else launch_attn_mq_hd<128>(G, ap.mq_ch, agrid, st, am);
     } else if (ap.dec) {
         AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, scale, attn_part};
-        launch_attn_dec(HD, dim3(NKV, n, nchunk), st, aa, attn, NH * HD, ap.dec_direct ? 1 : 0, mtp);
+        launch_attn_dec(HD, ap.dec_kpb, dim3(NKV, n, nchunk), st, aa, attn, NH * HD, ap.dec_direct ? 1 : 0, mtp);
     } else {
         AttnArgs aa{q, kc[l], vc[l], dtoks, NH, NKV, HD, n_slots, nchunk, scale, attn_part};
         dim3 agrid(nchunk, NKV, n);
@@ -1092,7 +1108,7 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             const int L = d.n_layers;
             const int cuts[4] = {0, std::min(1, L), std::min(5, L), L};
             const int plan_code = ap.mq ? (ap.mq_ch == 128 ? 1 << 20 : 0) + ap.ngroups * 1024 + ap.splits
-                                        : (ap.dec ? (ap.dec_direct ? -3 : -2) : (ap.rope_fused ? -4 : -1));
+                                        : (ap.dec ? (ap.dec_direct ? -3 : -2) - 8 * ap.dec_kpb : (ap.rope_fused ? -4 : -1));
             int total = 0;
             for (int part = 0; part < 3; ++part) {
                 if (cuts[part] >= cuts[part + 1]) continue;      // empty (short models); the head ran in its part
