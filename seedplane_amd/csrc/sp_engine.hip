@@ -125,7 +125,9 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
     if (split_ok && !m.paired) {
         s = std::max(1, 2048 / (p.units / p.r));
         s = std::min(s, std::max(1, m.nkt / 2));
-        s = std::min(s, mt == 1 ? GEMV_MAX_SLICES : 4);
+        // several int4 column tiles: up to 8 slices of 4 waves (7B shape at 32 columns: qkv 10.7 -> 7.4 us, o 7.7 ->
+        // 6.9, down 21.3 -> 19.8 against 4 slices of 8 waves)
+        s = std::min(s, mt == 1 || m.fmt == 3 ? GEMV_MAX_SLICES : 4);
         if (slices > 0) s = std::min(slices, std::max(1, m.nkt / 2));
     }
 #ifdef SP_GEMV_TUNE
@@ -136,7 +138,7 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
     p.kslice = (m.nkt + s - 1) / s;
     // several column tiles: 8 waves for the split layer matrices and long k-ranges, 4 for the gate_up pair and the
     // unsplit head (A/B runs of the whole tree-verify step at 33 columns: gate_up with 4 waves -100 us per pass)
-    int nw = std::min(p.kslice, mt > 1 && (p.kslice >= 32 || s > 1) ? 8 : 4);
+    int nw = std::min(p.kslice, mt > 1 && m.fmt != 3 && (p.kslice >= 32 || s > 1) ? 8 : 4);
     if (waves > 0) nw = std::min(p.kslice, std::min(waves, mt == 1 ? 16 : 8));
 #ifdef SP_GEMV_TUNE
     if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 16 : 8);
