@@ -260,8 +260,9 @@ int sp_op_sample_filtered(const float *logits_dev, int32_t vocab, int32_t ld, co
  * are device int32 [n_nodes].  The residual after j rejections is evaluated as max(p - c_j q, 0) / S_j with c_1 = 1,
  * c_{j+1} = c_j + S_j (the same distribution as renormalising max(p - q, 0) after each rejection).  Float64 sums
  * use 64 x 256 contiguous chunks: sequential inside a chunk, over the 256 chunk sums of each group of 256, then
- * over the 64 group sums.  Synchronous: returns after the walk, SP_EHIP if its cross-block exchange timed out.
- * out_host (may be NULL): host copy of out_dev, made within the same synchronisation. */
+ * over the 64 group sums.  Synchronous: returns after the walk has finished (it polls completion tags the kernel
+ * writes to pinned host memory, so later work on the stream may still be queued), SP_EHIP if its cross-block
+ * exchange timed out.  out_host (may be NULL): host copy of out_dev, written by the kernel itself. */
 int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld, int32_t n_nodes,
                       const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
                       const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,

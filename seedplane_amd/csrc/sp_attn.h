@@ -90,6 +90,16 @@ __global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, con
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// One RoPE rotation pair as the reference rounds it: o1 = x1 c - x2 s, o2 = x2 c + x1 s, each product rounded to fp32,
+// then the sum (qwen_engine.py:94-103: q * cos + rotate_half(q) * sin).  Contraction into fused multiply-adds is off
+// here (hipcc contracts a * b + c by default, and __fmul_rn / __fadd_rn are plain operators in HIP), so every kernel
+// that rotates produces the same bits.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float &o1, float &o2) {
+#pragma clang fp contract(off)
+    o1 = x1 * c - x2 * s;
+    o2 = x2 * c + x1 * s;
+}
+
 struct RopeArgs {
     const float *qkv;       // [n][Nqkv] fp32 (bias already added) when nparts == 0
     int Nqkv, NH, NKV, HD;
@@ -131,8 +141,8 @@ __global__ void __launch_bounds__(ROPE_THREADS) k_rope_kv(RopeArgs a) {
         const float2 cs = a.rtab[(size_t)b * half + i];
         const float c = cs.x, s = cs.y;
         const float x1 = qkv_value<NP>(a, b, head * a.HD + i), x2 = qkv_value<NP>(a, b, head * a.HD + i + half);
-        const float o1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(-x2, s));
-        const float o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+        float o1, o2;
+        rope_pair(x1, x2, c, s, o1, o2);
         if (head < a.NH) {
             float *q = a.q + (size_t)b * a.NH * a.HD + head * a.HD;
             q[i] = o1; q[i + half] = o2;
@@ -338,8 +348,8 @@ __global__ void __launch_bounds__(64 * G) k_attn_part_rope(AttnArgs a, RopeArgs 
         const int hh = i / HALF, j = i - hh * HALF;
         const float cs = tw[ri].x, sn = tw[ri].y;
         const float x1 = sum_of(t1[ri], bb1[ri]), x2 = sum_of(t2[ri], bb2[ri]);
-        const float o1 = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(-x2, sn));
-        const float o2 = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
+        float o1, o2;
+        rope_pair(x1, x2, cs, sn, o1, o2);
         if (hh < G) {
             q_s[hh][j] = o1 * a.scale;
             q_s[hh][j + HALF] = o2 * a.scale;

@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdio>
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <functional>
 #include <map>
@@ -1554,14 +1555,12 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
         // the kernel checks every node / trial / token index it follows before using it (err = 2 if one is bad)
         hipStream_t st = (hipStream_t)stream;
-        // exchange words + a read-back block, one set per device, zeroed once; tags never repeat within 2^20
-        // launches, so neither needs clearing between launches (the kernel writes every entry of out_dev itself).
-        // The read-back block holds the error word (int 0), the completion tag (int 1) and a copy of the result (from
-        // int PIN_OUT), so one device-to-host copy into a pinned block returns all of it; the host polls the tag in
-        // that block before it synchronises (the wait then ends as soon as the copy lands).  out_host may be any
-        // host memory.
-        struct AccScratch { unsigned long long *xbuf; int32_t *back; int32_t *pin; };
-        constexpr int PIN_OUT = 16, BACK_INTS = PIN_OUT + 64 + 4;
+        // exchange words and the error word in device memory, and a pinned host block the kernel writes its result
+        // and completion tags into, one set per device; tags never repeat within 2^20 launches, so nothing needs
+        // clearing between launches (the kernel writes every entry of out_dev itself).  The host polls the tags
+        // (block 0's, then the drawing block's) instead of synchronising the stream; a poll that runs out (about
+        // 1 s) falls back to the synchronisation, which reports any error of the kernel.
+        struct AccScratch { unsigned long long *xbuf; unsigned *err; int32_t *host; };
         static std::map<int, AccScratch> scratch_of;
         static unsigned launches = 0;
         int dev = 0;
@@ -1569,30 +1568,34 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         auto it = scratch_of.find(dev);
         if (it == scratch_of.end()) {
             unsigned long long *xb = dev_alloc<unsigned long long>(4 * ACC_NB * 4);
-            int32_t *back = dev_alloc<int32_t>(BACK_INTS);
+            unsigned *err = dev_alloc<unsigned>(1);
             HIPCHK(hipMemset(xb, 0, 4 * ACC_NB * 4 * sizeof(unsigned long long)));
-            HIPCHK(hipMemset(back, 0, BACK_INTS * sizeof(int32_t)));
-            int32_t *pin = nullptr;
-            HIPCHK(hipHostMalloc((void **)&pin, BACK_INTS * sizeof(int32_t), hipHostMallocDefault));
-            it = scratch_of.emplace(dev, AccScratch{xb, back, pin}).first;
+            HIPCHK(hipMemset(err, 0, sizeof(unsigned)));
+            int32_t *host = nullptr;
+            HIPCHK(hipHostMalloc((void **)&host, (ACC_HOST_OUT + 64 + 4) * sizeof(int32_t), hipHostMallocCoherent));
+            std::memset(host, 0, (ACC_HOST_OUT + 64 + 4) * sizeof(int32_t));
+            it = scratch_of.emplace(dev, AccScratch{xb, err, host}).first;
         }
         const AccScratch &sc = it->second;
         launches = launches % 0xFFFFFu + 1;
         const unsigned tag = launches << 12;
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token_dev, trial_start_dev, n_trials_dev, trials_dev, u_dev,
-                     n_u, 1.0 / temperature, sc.xbuf, (unsigned *)sc.back, tag, n_nodes, n_trials_total, out_dev,
-                     max_depth, sc.back + PIN_OUT, sc.back + 1};
-        volatile int32_t *pin_tag = sc.pin + 1;
-        *pin_tag = 0;
+                     n_u, 1.0 / temperature, sc.xbuf, sc.err, tag, n_nodes, n_trials_total, out_dev, max_depth, sc.host};
+        volatile int32_t *hb = sc.host;
         hipLaunchKernelGGL(k_accept_tree, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
         HIPCHK(hipGetLastError());
-        HIPCHK(hipMemcpyAsync(sc.pin, sc.back, (PIN_OUT + max_depth + 4) * sizeof(int32_t), hipMemcpyDeviceToHost, st));
-        // bounded poll (about 1 s), then the stream synchronisation that reports any error of the copy or kernel
-        for (long spin = 0; *pin_tag != (int32_t)tag && spin < (1l << 26); ++spin) {
-        }
-        HIPCHK(hipStreamSynchronize(st));
-        const unsigned err = (unsigned)sc.pin[0];
-        if (out_host) std::memcpy(out_host, sc.pin + PIN_OUT, (max_depth + 4) * sizeof(int32_t));
+        auto wait_tag = [&](int i) {
+            for (long spin = 0; spin < (1l << 26); ++spin)
+                if (hb[i] == (int32_t)tag) return true;
+            return false;
+        };
+        auto failed = [&] { const unsigned e = (unsigned)hb[0]; return (e & ~0xfffu) == tag && (e & 0xfffu) != 0; };
+        if (!(wait_tag(1) && (failed() || wait_tag(2)))) HIPCHK(hipStreamSynchronize(st));
+        std::atomic_thread_fence(std::memory_order_acquire);
+        require(hb[1] == (int32_t)tag, SP_EHIP, "acceptance walk did not report completion");
+        const unsigned err = (unsigned)hb[0];
+        if (out_host)
+            for (int i = 0; i < max_depth + 4; ++i) out_host[i] = hb[ACC_HOST_OUT + i];
         const unsigned code = (err & ~0xfffu) == tag ? err & 0xfffu : 0u;
         require(code != 2, SP_EINVAL, "malformed tree: node, trial or token index out of range");
         require(code == 0, SP_EHIP, "acceptance exchange timed out");

@@ -177,9 +177,10 @@ struct AcceptArgs {
     int *out;                // [0] k, [1..k] accepted node ids, [max_depth+1] final token, [max_depth+2] uniforms used,
                              // [max_depth+3] bonus flag
     int max_depth;
-    int *out2;               // a second copy of out (may be NULL): the library's read-back block, next to err
-    int *done;               // may be NULL: block 0 stores tag_base here when it leaves (completion tag)
+    int *host;               // may be NULL: pinned host block written directly: [0] the err word, [1] block 0's
+                             // completion tag, [2] the drawing block's tag, [ACC_HOST_OUT ..] a copy of out
 };
+constexpr int ACC_HOST_OUT = 16;
 
 struct AccShared {
     double tsum[ACC_T];      // thread chunk sums
@@ -333,10 +334,13 @@ __device__ __forceinline__ bool acc_bad(const AcceptArgs &a) {
 
 __device__ __forceinline__ void acc_put(const AcceptArgs &a, int i, int v) {
     a.out[i] = v;
-    if (a.out2) a.out2[i] = v;
+    if (a.host) a.host[ACC_HOST_OUT + i] = v;
 }
 
 __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
+    // p - c q products and differences are rounded separately, as the definition writes them (hipcc would otherwise
+    // contract them into fused multiply-adds; __dmul_rn / __dsub_rn are plain operators in HIP)
+#pragma clang fp contract(off)
     __shared__ AccShared sh;
     const int C = (a.V + ACC_NB * ACC_T - 1) / (ACC_NB * ACC_T);
     const int lo = (blockIdx.x * ACC_T + threadIdx.x) * C;
@@ -386,7 +390,12 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
             bonus = 1;
             break;
         }
-        // ---- trials in draw order
+        // ---- trials in draw order.  The normalised weights p_i / Zp and q_i / Zq are formed once per node (the
+        // residual of every trial uses the same quotients)
+#pragma unroll
+        for (int i = 0; i < ACC_PER; ++i) {
+            if (i < n) { wp[i] = __ddiv_rn(wp[i], Zp); wq[i] = __ddiv_rn(wq[i], Zq); }
+        }
         int accepted = -1, J = 0;
         double c = 0.0, S = 0.0;
         for (int j = t0; j < t0 + nt; ++j) {
@@ -408,7 +417,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
             double sr = 0.0;
             for (int i = 0; i < ACC_PER; ++i) {
                 if (i < n) {
-                    const double d = __dsub_rn(__ddiv_rn(wp[i], Zp), __dmul_rn(c, __ddiv_rn(wq[i], Zq)));
+                    const double d = __dsub_rn(wp[i], __dmul_rn(c, wq[i]));
                     w[i] = d > 0.0 ? d : 0.0;
                     sr += w[i];
                 } else w[i] = 0.0;
@@ -440,7 +449,20 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         }
         if (final_tok >= 0) acc_put(a, a.max_depth + 1, final_tok);   // only the block owning the draw has it
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0 && a.done) *a.done = (int)a.tag_base;
+    // host read-back without a copy or a stream synchronisation: each writer's entries reach host memory before its
+    // tag (system-scope fence); the host waits for block 0's tag and, unless the err word reports a failure, for the
+    // drawing block's
+    if (threadIdx.x == 0 && a.host) {
+        if (alive && final_tok >= 0) {
+            __threadfence_system();
+            __hip_atomic_store(a.host + 2, (int)a.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        if (blockIdx.x == 0) {
+            a.host[0] = (int)__hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __threadfence_system();
+            __hip_atomic_store(a.host + 1, (int)a.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -283,6 +283,19 @@ class TreeVerifier:
         in `logits_out` or, without it, as a view of the engine's own logits buffer (no copy; valid until the
         engine's next forward call)."""
         e = self.engine
+        n = tree.size
+        cols = self.columns(cache, tree)
+        flags = self._lib.SP_F_LOGITS | (self._lib.SP_F_GRAPH if graph else 0)
+        out = e.run(cols, flags, logits_out=logits_out, want_ids=ids)
+        if ids:
+            return out
+        return logits_out if logits_out is not None else e.logits_view(n)
+
+    def columns(self, cache, tree: FlatTree):
+        """The engine columns of one tree pass (a numpy array of _lib.TOKEN_DTYPE): node i in slot
+        (cache.length + i) mod slots, which is tree slot i of the pass, at RoPE position cache.length + depth[i],
+        seeing the cached positions before the root (the window's part of them) and the tree nodes of its mask."""
+        e = self.engine
         e._check_cache(cache)
         n = tree.size
         if n > min(e.max_tokens, 64):
@@ -303,11 +316,7 @@ class TreeVerifier:
         cols['tree_base'] = P % S
         cols['tree_count'] = n
         cols['tree_mask'] = masks
-        flags = self._lib.SP_F_LOGITS | (self._lib.SP_F_GRAPH if graph else 0)
-        out = e.run(cols, flags, logits_out=logits_out, want_ids=ids)
-        if ids:
-            return out
-        return logits_out if logits_out is not None else e.logits_view(n)
+        return cols
 
     def commit(self, cache, tree: FlatTree, path_nodes):
         """Keep the root and the accepted path nodes (in order) in the cache: their K/V move to consecutive slots
