@@ -25,6 +25,9 @@
 
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_PART = 3 };
 
+// 16 zero bytes, never written: the activation load address of lanes whose column does not exist (row-major x)
+static __device__ __align__(16) f16 g_zero_line[8];
+
 struct GemvArgs {
     const uint8_t *w;      // packed tiles
     const f16 *sz;         // per-tile scales (Q8) / scale+zero pairs (Q4); unused for F16
@@ -287,7 +290,8 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
     constexpr int TB = PRO == PRO_NONE ? GemvBatch<FMT, MT, RG>::TB : GemvBatch<FMT, MT, 1>::TB;
     constexpr int NR = R * RG;                 // row groups per wave
     const int NW = PRO == PRO_NONE ? (int)(blockDim.x >> 6) : a.nwk;   // waves taking k-tiles
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    // the wave index as a wave-uniform value: the per-wave k-tile bounds below become scalar branches
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool worker = PRO == PRO_NONE || wv < NW;
     const int r = lane & 15, g = lane >> 4;
     const int u0 = blockIdx.x * R;
@@ -362,12 +366,12 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                     if constexpr (PRO == PRO_NONE) {
                         // fragment-major (xmtp == MT): every lane loads, columns past m included -- the buffers hold
                         // whole 16-column tiles, and an MFMA output row depends only on its own A row, so whatever
-                        // those columns hold never reaches a stored output; row-major: columns past m read as zeros
-                        // (their lanes do not load)
-                        if (a.xmtp)
-                            xa[t][mt][s] = *(const f16x8 *)(a.x + ((size_t)(kt * ST + s) * MT + mt) * 512 + lane * 8);
-                        else
-                            xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(xrow[mt] + kt * KT + s * 32) : zero8;
+                        // those columns hold never reaches a stored output; row-major: lanes of columns past m load
+                        // the zero line.  One unconditional load from a selected address: no branch and no select
+                        // on the value, so the loads of a batch stay in flight together.
+                        const f16 *xf = a.x + ((size_t)(kt * ST + s) * MT + mt) * 512 + lane * 8;
+                        const f16 *xr = xon[mt] ? xrow[mt] + kt * KT + s * 32 : g_zero_line;
+                        xa[t][mt][s] = *(const f16x8 *)(a.xmtp ? xf : xr);
                     } else
                         xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(act + (kt - k0) * KT + s * 32 + 8 * g) : zero8;
                 }
