@@ -439,23 +439,25 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
     // -- and V rows -- lane: key lane / 2, dims (lane & 1) * HD/2 .., the layout whose transposed LDS stores are
     // conflict-free) land in register slot sc % 2; the loads of
     // sub-chunk sc + 2 are issued as soon as sub-chunk sc has been consumed, so two sub-chunks are always in flight
-    // while the wave computes (loads complete in order, so each use waits only for its own sub-chunk)
+    // while the wave computes (loads complete in order, so each use waits only for its own sub-chunk).  Keys past the
+    // range load the first key of the range instead (unconditional loads: a per-lane condition would split them into
+    // branches and the waits at their joins would also wait for the prefetched sub-chunks); their scores are masked
+    // (P = 0) and the values they load are finite cache entries, so they contribute nothing.
     f16x8 kf[2][2][ST], vf[2][VPL];
     auto load_sub = [&](int sc, int slot) {
         const int v0 = v_lo + sc * DEC_KC;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const int key = v0 + kt * 16 + r16;
-            const bool live = key < v_hi;
-            const size_t off = (head_base + (size_t)((t.ctx_lo + (live ? key : 0)) % a.n_slots)) * HD + g4 * 8;
+            const size_t off = (head_base + (size_t)((t.ctx_lo + (key < v_hi ? key : 0)) % a.n_slots)) * HD + g4 * 8;
 #pragma unroll
-            for (int st = 0; st < ST; ++st) kf[slot][kt][st] = live ? *(const f16x8 *)(a.kc + off + st * 32) : zero8;
+            for (int st = 0; st < ST; ++st) kf[slot][kt][st] = *(const f16x8 *)(a.kc + off + st * 32);
         }
         const int key = v0 + (lane >> 1);
-        const bool live = key < v_hi;
-        const size_t off = (head_base + (size_t)((t.ctx_lo + (live ? key : 0)) % a.n_slots)) * HD + (lane & 1) * (HD / 2);
+        const size_t off =
+            (head_base + (size_t)((t.ctx_lo + (key < v_hi ? key : 0)) % a.n_slots)) * HD + (lane & 1) * (HD / 2);
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) vf[slot][i] = live ? *(const f16x8 *)(a.vc + off + i * 8) : zero8;
+        for (int i = 0; i < VPL; ++i) vf[slot][i] = *(const f16x8 *)(a.vc + off + i * 8);
     };
     load_sub(0, 0);
     if (DEC_SUB > 1) load_sub(1, 1);
