@@ -160,25 +160,33 @@ __host__ __device__ inline int pro_scratch_floats(int pro, int H, int HD) {
     return 0;
 }
 
-__device__ __forceinline__ void pro_norm(const ProArgs &p, f16 *act, int klo, int klen, float *scr) {
-    constexpr int PRO_THREADS = pro_threads(PRO_NORM), PRO_QMAX = PRO_NORM_HMAX / PRO_THREADS;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, H = p.H;
-    float *v_s = scr, *red = scr + H;
-    // every load first, from clamped addresses: the residual, the slices, the weights of this block's k-range
-    float xv[PRO_QMAX], wk[PRO_QMAX], pv[PRO_MAX_SLICES][PRO_QMAX];
+// The norm prologue's operands (the residual, every slice, the norm weights of this block's k-range), loaded from
+// clamped addresses with no branch: a slice index past the pending ones re-reads the last pending slice (slice 0
+// when none is pending), whose values the sum skips.
+constexpr int PRO_NORM_QMAX = PRO_NORM_HMAX / pro_threads(PRO_NORM);
+struct NormOps { float xv[PRO_NORM_QMAX], wk[PRO_NORM_QMAX], pv[PRO_MAX_SLICES][PRO_NORM_QMAX]; };
+__device__ __forceinline__ void pro_norm_load(const ProArgs &p, int klo, NormOps &o) {
+    constexpr int PRO_THREADS = pro_threads(PRO_NORM);
+    const int tid = threadIdx.x, H = p.H;
 #pragma unroll
-    for (int q = 0; q < PRO_QMAX; ++q) {
-        xv[q] = p.res[min(tid + PRO_THREADS * q, H - 1)];
-        wk[q] = p.w[min(klo + tid + PRO_THREADS * q, H - 1)];
+    for (int q = 0; q < PRO_NORM_QMAX; ++q) {
+        o.xv[q] = p.res[min(tid + PRO_THREADS * q, H - 1)];
+        o.wk[q] = p.w[min(klo + tid + PRO_THREADS * q, H - 1)];
     }
 #pragma unroll
     for (int s = 0; s < PRO_MAX_SLICES; ++s) {
-        if (s < p.np) {                              // uniform: only the pending slices are loaded
+        const size_t so = (size_t)min(s, max(p.np - 1, 0)) * p.pstride;
 #pragma unroll
-            for (int q = 0; q < PRO_QMAX; ++q)
-                pv[s][q] = p.part[(size_t)s * p.pstride + min(tid + PRO_THREADS * q, H - 1)];
-        }
+        for (int q = 0; q < PRO_NORM_QMAX; ++q) o.pv[s][q] = p.part[so + min(tid + PRO_THREADS * q, H - 1)];
     }
+}
+__device__ __forceinline__ void pro_norm_finish(const ProArgs &p, const NormOps &o, f16 *act, int klo, int klen,
+                                                float *scr) {
+    constexpr int PRO_THREADS = pro_threads(PRO_NORM), PRO_QMAX = PRO_NORM_QMAX;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, H = p.H;
+    float *v_s = scr, *red = scr + H;
+    const float *xv = o.xv, *wk = o.wk;
+    const auto &pv = o.pv;
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
 #pragma unroll
     for (int q = 0; q < PRO_QMAX; ++q) {
@@ -219,6 +227,11 @@ __device__ __forceinline__ void pro_norm(const ProArgs &p, f16 *act, int klo, in
         if (e < klen) act[e] = (f16)((v_s[klo + e] * rs) * wk[q]);
     }
     __syncthreads();
+}
+__device__ __forceinline__ void pro_norm(const ProArgs &p, f16 *act, int klo, int klen, float *scr) {
+    NormOps o;
+    pro_norm_load(p, klo, o);
+    pro_norm_finish(p, o, act, klo, klen, scr);
 }
 
 // Heads overlapping the k-range, pro_threads(PRO_COMB) / HD at a time: thread group g of HD threads plays

@@ -44,6 +44,20 @@ __global__ void __launch_bounds__(1024) k_gemv1(GemvArgs a, ProArgs p) {
     float *red = (float *)(smem_raw + xh * 2);
     float *scr = red + NW * RG * 16;
 
+    // ---- 0. the activation side's own global loads first: loads complete in issue order, so the activation work
+    // below then waits only for them and runs while the weight tiles are still streaming in
+    const int nx = klen / 8;                         // 16-byte pieces of the slice's activations
+    uint4 xpre;
+    NormOps npre;
+    if constexpr (PRO == PRO_NONE) {
+        // from a clamped base and index (an empty last slice reads the final piece and stores nothing)
+        const uint4 *src = (const uint4 *)(a.x + (size_t)min(k0, a.nkt - 1) * KT);
+        xpre = src[min((int)threadIdx.x, max(nx - 1, 0))];
+    } else if constexpr (PRO == PRO_NORM) {
+        pro_norm_load(p, k0 * KT, npre);
+    }
+    __builtin_amdgcn_sched_barrier(0);               // keep these loads ahead of the weight loads
+
     // ---- 1. every weight / scale load of the wave's tiles, in tile order
     const uint8_t *wb[RG];
     const f16 *sb[RG];
@@ -74,9 +88,12 @@ __global__ void __launch_bounds__(1024) k_gemv1(GemvArgs a, ProArgs p) {
     if constexpr (PRO == PRO_NONE) {
         const uint4 *src = (const uint4 *)(a.x + (size_t)k0 * KT);
         uint4 *dst = (uint4 *)xs_lds;
-        for (int i = threadIdx.x; i < klen / 8; i += blockDim.x) dst[i] = src[i];
+        // unconditional store (threads past the slice write the first piece of the reduction area, which is only
+        // written again after the barrier below), so the load above is not moved behind the weight loads
+        dst[(int)threadIdx.x < nx ? (int)threadIdx.x : (int)(xh / 8)] = xpre;
+        for (int i = threadIdx.x + blockDim.x; i < nx; i += blockDim.x) dst[i] = src[i];
     } else if constexpr (PRO == PRO_NORM) {
-        pro_norm(p, xs_lds, k0 * KT, klen, scr);
+        pro_norm_finish(p, npre, xs_lds, k0 * KT, klen, scr);
     } else {
         pro_comb(p, xs_lds, k0 * KT, klen, scr);
     }
