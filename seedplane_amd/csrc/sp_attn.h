@@ -52,25 +52,36 @@ __global__ void __launch_bounds__(256) k_embed(const uint8_t *w, const f16 *sz, 
 // the NP split-K slices) is issued before the first use.  With NP > 0 the residual update of a split-K GEMV is
 // completed first: x[b] += part[0][b] + ... + part[NP-1][b] (in slice order) and written back to x.
 constexpr int NORM_THREADS = 1024, NORM_PER_THREAD = 4;
-template <int NP>
-__global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, const float *part, size_t pstride,
-                                                          const float *w, int H, float eps, f16 *out, int ldo,
-                                                          int mtp) {
+// NG = the element groups of NORM_THREADS that H needs (<= NORM_PER_THREAD; the missing groups are zeros, which add
+// nothing to the sum of squares): the body is straight-line code whose loads are all unconditional, from clamped
+// indices (elements past H re-read element H - 1 and become zeros after loading), so they are in flight together.
+template <int NP, int NG>
+__device__ __forceinline__ void rmsnorm_body(float *x, int ldx, const float *part, size_t pstride, const float *w, int H,
+                                             float eps, f16 *out, int ldo, int mtp) {
     __shared__ float red[16];
     const int b = blockIdx.x;
     float *xr = x + (size_t)b * ldx;
-    float v[NORM_PER_THREAD], wk[NORM_PER_THREAD], pv[NP > 0 ? NP : 1][NORM_PER_THREAD];
+    float v[NORM_PER_THREAD], wk[NORM_PER_THREAD], pv[NP > 0 ? NP : 1][NG];
 #pragma unroll
-    for (int i = 0; i < NORM_PER_THREAD; ++i) {
-        const int k = threadIdx.x + i * NORM_THREADS;
-        v[i] = k < H ? xr[k] : 0.f;
-        wk[i] = k < H ? w[k] : 0.f;
+    for (int i = 0; i < NG; ++i) {
+        const int kc = min((int)threadIdx.x + i * NORM_THREADS, H - 1);
+        v[i] = xr[kc];
+        wk[i] = w[kc];
 #pragma unroll
-        for (int s = 0; s < NP; ++s) pv[s][i] = k < H ? part[(size_t)s * pstride + (size_t)b * ldx + k] : 0.f;
+        for (int s = 0; s < NP; ++s) pv[s][i] = part[(size_t)s * pstride + (size_t)b * ldx + kc];
+    }
+#pragma unroll
+    for (int i = NG; i < NORM_PER_THREAD; ++i) { v[i] = 0.f; wk[i] = 0.f; }
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const bool in = (int)threadIdx.x + i * NORM_THREADS < H;
+        v[i] = in ? v[i] : 0.f;
+#pragma unroll
+        for (int s = 0; s < NP; ++s) pv[s][i] = in ? pv[s][i] : 0.f;
     }
     if constexpr (NP > 0) {
 #pragma unroll
-        for (int i = 0; i < NORM_PER_THREAD; ++i) {
+        for (int i = 0; i < NG; ++i) {
             const int k = threadIdx.x + i * NORM_THREADS;
 #pragma unroll
             for (int s = 0; s < NP; ++s) v[i] += pv[s][i];
@@ -83,10 +94,18 @@ __global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, con
     ss = block_sum_dpp(ss, red);
     const float rs = 1.0f / sqrtf(ss / (float)H + eps);
 #pragma unroll
-    for (int i = 0; i < NORM_PER_THREAD; ++i) {
+    for (int i = 0; i < NG; ++i) {
         const int k = threadIdx.x + i * NORM_THREADS;
         if (k < H) out[act_off(b, k, ldo, mtp)] = (f16)((v[i] * rs) * wk[i]);
     }
+}
+template <int NP>
+__global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, const float *part, size_t pstride,
+                                                          const float *w, int H, float eps, f16 *out, int ldo,
+                                                          int mtp) {
+    if (H <= NORM_THREADS) rmsnorm_body<NP, 1>(x, ldx, part, pstride, w, H, eps, out, ldo, mtp);
+    else if (H <= 2 * NORM_THREADS) rmsnorm_body<NP, 2>(x, ldx, part, pstride, w, H, eps, out, ldo, mtp);
+    else rmsnorm_body<NP, NORM_PER_THREAD>(x, ldx, part, pstride, w, H, eps, out, ldo, mtp);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
