@@ -148,13 +148,23 @@ __device__ __forceinline__ float qkv_value(const RopeArgs &a, int b, int idx) {
     }
 }
 // Non-interleaved half rotation x*cos + rotate_half(x)*sin with phase = float(pos) * inv_freq (qwen_engine.py:94-103,
-// rope_kv.comp:1-32); K and V of every column are written to their slot.  One block of ROPE_THREADS per column.
+// rope_kv.comp:1-32); K and V of every column are written to their slot.  Two blocks of ROPE_THREADS per column:
+// block y = 0 rotates the queries and the key, block y = 1 copies the value (each in one memory round trip; one block
+// doing both would issue the value loads only after the rotation's stores).
 constexpr int ROPE_THREADS = 1024;
 template <int NP>
 __global__ void __launch_bounds__(ROPE_THREADS) k_rope_kv(RopeArgs a) {
     const int b = blockIdx.x;
     const sp_token t = a.toks[b];
     const int half = a.HD >> 1;
+    if (blockIdx.y == 1) {
+        const int v0 = (a.NH + a.NKV) * a.HD;
+        for (int idx = threadIdx.x; idx < a.NKV * a.HD; idx += blockDim.x) {
+            const int kvh = idx / a.HD, d = idx - kvh * a.HD;
+            a.vc[(((size_t)t.seq * a.NKV + kvh) * a.n_slots + t.slot) * a.HD + d] = (f16)qkv_value<NP>(a, b, v0 + idx);
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < (a.NH + a.NKV) * half; idx += blockDim.x) {
         const int head = idx / half, i = idx - head * half;
         const float2 cs = a.rtab[(size_t)b * half + i];
@@ -170,11 +180,6 @@ __global__ void __launch_bounds__(ROPE_THREADS) k_rope_kv(RopeArgs a) {
             f16 *k = a.kc + (((size_t)t.seq * a.NKV + kvh) * a.n_slots + t.slot) * a.HD;
             k[i] = (f16)o1; k[i + half] = (f16)o2;
         }
-    }
-    const int v0 = (a.NH + a.NKV) * a.HD;
-    for (int idx = threadIdx.x; idx < a.NKV * a.HD; idx += blockDim.x) {
-        const int kvh = idx / a.HD, d = idx - kvh * a.HD;
-        a.vc[(((size_t)t.seq * a.NKV + kvh) * a.n_slots + t.slot) * a.HD + d] = (f16)qkv_value<NP>(a, b, v0 + idx);
     }
 }
 

@@ -384,7 +384,7 @@ void launch_rmsnorm(int n, float *x, int H, const float *part, int np, size_t ps
 }
 
 void launch_rope(int n, const RopeArgs &ra, int np, hipStream_t st) {
-    by_slices(np, [&](auto c) { hipLaunchKernelGGL((k_rope_kv<decltype(c)::value>), dim3(n), dim3(ROPE_THREADS), 0, st, ra); });
+    by_slices(np, [&](auto c) { hipLaunchKernelGGL((k_rope_kv<decltype(c)::value>), dim3(n, 2), dim3(ROPE_THREADS), 0, st, ra); });
 }
 
 // decode attention split: waves per block x 32-key sub-chunks per wave
