@@ -96,6 +96,7 @@ constexpr int GEMV_MAX_LDS = 64 * 1024;
 
 struct GemvPlan {
     int units, nw, rg, r, s, kslice;
+    bool shallow;      // several column tiles: one k-tile per load batch (k_gemv<..., SHALLOW>)
 };
 
 #ifdef SP_GEMV_TUNE
@@ -141,6 +142,13 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
     // unsplit head (A/B runs of the whole tree-verify step at 33 columns: gate_up with 4 waves -100 us per pass)
     int nw = std::min(p.kslice, mt > 1 && m.fmt != 3 && (p.kslice >= 32 || s > 1) ? 8 : 4);
     if (waves > 0) nw = std::min(p.kslice, std::min(waves, mt == 1 ? 16 : 8));
+    // int8 codes at 3 column tiles (33-48 columns, a tree pass): one k-tile per batch (98 instead of 132 VGPRs for
+    // the gate_up pair, so more resident waves) unless a split matrix gives each wave a long k-range (the down
+    // projection); the LM head then runs 2 waves of 4 units.  Launch sweeps at 33 columns: gate_up 13.2 -> 12.5 us,
+    // head 69.7 -> 59.4, qkv and o -0.15, down 7.8 -> 8.6 (so it keeps 2 k-tiles); at 2 and 4 column tiles and
+    // with int4 codes shallow batches are slower (head at 32 columns 58 -> 64 us, int4 matrices 10-35 %).
+    p.shallow = mt == 3 && m.fmt == 2 && !(s > 1 && p.kslice >= 32);
+    if (p.shallow && p.r == 4 && waves == 0) nw = std::min(nw, 2);
 #ifdef SP_GEMV_TUNE
     if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 16 : 8);
 #endif
@@ -151,32 +159,40 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
 }
 
 template <int FMT, int RG, int R>
-void launch_gemv_r(int mt, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
-    switch (mt) {
-        case 1:
+void launch_gemv_r(int mt, bool shallow, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+    if (mt == 1) {
+        if constexpr (R == 4) {
+            throw Fail{SP_EINVAL, "gemv plan: 4 units per wave need several column tiles"};
+        } else {
             if (a.m == 1) hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R, true>), grid, block, smem, st, a);
             else hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R>), grid, block, smem, st, a);
-            break;
+        }
+        return;
+    }
+    if constexpr (FMT == 2) {
+        if (shallow) {
+            require(mt == 3, SP_EINVAL, "gemv plan: shallow batches are built for 3 column tiles");
+            hipLaunchKernelGGL((k_gemv<FMT, 3, RG, R, false, true>), grid, block, smem, st, a);
+            return;
+        }
+    }
+    switch (mt) {
         case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, RG, R>), grid, block, smem, st, a); break;
         case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, RG, R>), grid, block, smem, st, a); break;
         default: hipLaunchKernelGGL((k_gemv<FMT, 4, RG, R>), grid, block, smem, st, a); break;
     }
 }
 template <int FMT>
-void launch_gemv_fmt(int mt, bool paired, int r, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+void launch_gemv_fmt(int mt, bool paired, int r, bool shallow, dim3 grid, dim3 block, size_t smem, hipStream_t st,
+                     const GemvArgs &a) {
     if (paired) {
-        if (r == 2) launch_gemv_r<FMT, 2, 2>(mt, grid, block, smem, st, a);
-        else launch_gemv_r<FMT, 2, 1>(mt, grid, block, smem, st, a);
+        if (r == 2) launch_gemv_r<FMT, 2, 2>(mt, shallow, grid, block, smem, st, a);
+        else launch_gemv_r<FMT, 2, 1>(mt, shallow, grid, block, smem, st, a);
     } else if (r == 4) {
-        switch (mt) {
-            case 1: throw Fail{SP_EINVAL, "gemv plan: 4 units per wave need several column tiles"};
-            case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, 1, 4>), grid, block, smem, st, a); break;
-            case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, 1, 4>), grid, block, smem, st, a); break;
-            default: hipLaunchKernelGGL((k_gemv<FMT, 4, 1, 4>), grid, block, smem, st, a); break;
-        }
+        launch_gemv_r<FMT, 1, 4>(mt, shallow, grid, block, smem, st, a);
     } else {
-        if (r == 2) launch_gemv_r<FMT, 1, 2>(mt, grid, block, smem, st, a);
-        else launch_gemv_r<FMT, 1, 1>(mt, grid, block, smem, st, a);
+        if (r == 2) launch_gemv_r<FMT, 1, 2>(mt, shallow, grid, block, smem, st, a);
+        else launch_gemv_r<FMT, 1, 1>(mt, shallow, grid, block, smem, st, a);
     }
 }
 
@@ -300,9 +316,9 @@ int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, floa
     }
     const size_t smem = p.nw > 1 ? (size_t)p.nw * p.r * p.rg * mt * 64 * 16 : 0;
     switch (m.fmt) {
-        case 1: launch_gemv_fmt<1>(mt, m.paired, p.r, grid, block, smem, st, a); break;
-        case 2: launch_gemv_fmt<2>(mt, m.paired, p.r, grid, block, smem, st, a); break;
-        default: launch_gemv_fmt<3>(mt, m.paired, p.r, grid, block, smem, st, a); break;
+        case 1: launch_gemv_fmt<1>(mt, m.paired, p.r, p.shallow, grid, block, smem, st, a); break;
+        case 2: launch_gemv_fmt<2>(mt, m.paired, p.r, p.shallow, grid, block, smem, st, a); break;
+        default: launch_gemv_fmt<3>(mt, m.paired, p.r, p.shallow, grid, block, smem, st, a); break;
     }
     return p.s > 1 ? p.s : 0;
 }

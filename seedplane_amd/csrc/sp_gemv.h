@@ -25,7 +25,7 @@
 
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_PART = 3 };
 
-// 16 zero bytes, never written: the activation load address of lanes whose column does not exist (row-major x)
+// 16 zero bytes, never written: the activation load address of lanes whose column does not exist
 static __device__ __align__(16) f16 g_zero_line[8];
 
 struct GemvArgs {
@@ -82,8 +82,10 @@ template <int MT, int RG, int R> struct GemvLimits {
 #ifndef SP_MT_TB
 #define SP_MT_TB 2
 #endif
-template <int FMT, int MT, int RG> struct GemvBatch {
-    static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : (RG == 2 ? SP_GU_TB : 4)) : SP_MT_TB;
+// SHALLOW (several column tiles): one k-tile per batch.  Fewer registers (e.g. 132 -> 98 VGPRs for the int8 gate_up
+// pair at 3 column tiles) and so more resident waves, which the int8 matrices with short per-wave k-ranges prefer.
+template <int FMT, int MT, int RG, bool SHALLOW = false> struct GemvBatch {
+    static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : (RG == 2 ? SP_GU_TB : 4)) : (SHALLOW ? 1 : SP_MT_TB);
 };
 
 // Lane holds D[m = mt*16 + 4g + j][n = unit*16 + r], j < 4.  Operands the epilogue reads (bias, the residual) are
@@ -297,10 +299,10 @@ __device__ __forceinline__ void pro_comb(const ProArgs &p, f16 *act, int klo, in
 // and each quant block's result is corrected by QBias (+ the Q4 zero) times the block's activation sums, one fp32 FMA
 // per output; ONE (a single column) keeps only output component 0 (the other rows of the MFMA A operand are zero).
 // Every column gets the same operations in either case, so one column and a batch give the same bits.
-template <int FMT, int MT, int RG, int R, int PRO, bool ONE = false>
+template <int FMT, int MT, int RG, int R, int PRO, bool ONE = false, bool SHALLOW = false>
 __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, unsigned char *smem_raw) {
     constexpr int KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
-    constexpr int TB = PRO == PRO_NONE ? GemvBatch<FMT, MT, RG>::TB : GemvBatch<FMT, MT, 1>::TB;
+    constexpr int TB = PRO == PRO_NONE ? GemvBatch<FMT, MT, RG, SHALLOW>::TB : GemvBatch<FMT, MT, 1>::TB;
     constexpr int NR = R * RG;                 // row groups per wave
     const int NW = PRO == PRO_NONE ? (int)(blockDim.x >> 6) : a.nwk;   // waves taking k-tiles
     // the wave index as a wave-uniform value: the per-wave k-tile bounds below become scalar branches
@@ -377,14 +379,14 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
 #pragma unroll
                 for (int s = 0; s < ST; ++s) {
                     if constexpr (PRO == PRO_NONE) {
-                        // fragment-major (xmtp == MT): every lane loads, columns past m included -- the buffers hold
-                        // whole 16-column tiles, and an MFMA output row depends only on its own A row, so whatever
-                        // those columns hold never reaches a stored output; row-major: lanes of columns past m load
-                        // the zero line.  One unconditional load from a selected address: no branch and no select
-                        // on the value, so the loads of a batch stay in flight together.
+                        // lanes of columns past m load the zero line (one L1-resident line: a partly used column
+                        // tile, e.g. column 32 of 33, reads only its live columns from L2), the others their
+                        // fragment (fragment-major, xmtp == MT) or row slice (row-major).  One unconditional load
+                        // from a selected address: no branch and no select on the value, so the loads of a batch
+                        // stay in flight together.
                         const f16 *xf = a.x + ((size_t)(kt * ST + s) * MT + mt) * 512 + lane * 8;
-                        const f16 *xr = xon[mt] ? xrow[mt] + kt * KT + s * 32 : g_zero_line;
-                        xa[t][mt][s] = *(const f16x8 *)(a.xmtp ? xf : xr);
+                        const f16 *xr = xrow[mt] + kt * KT + s * 32;
+                        xa[t][mt][s] = *(const f16x8 *)(xon[mt] ? (a.xmtp ? xf : xr) : g_zero_line);
                     } else
                         xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(act + (kt - k0) * KT + s * 32 + 8 * g) : zero8;
                 }
@@ -492,10 +494,10 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
     }
 }
 
-template <int FMT, int MT, int RG, int R, bool ONE = false>
+template <int FMT, int MT, int RG, int R, bool ONE = false, bool SHALLOW = false>
 __global__ void __launch_bounds__((GemvLimits<MT, RG, R>::MAX_THREADS)) k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    gemv_run<FMT, MT, RG, R, PRO_NONE, ONE>(a, ProArgs{}, smem_raw);
+    gemv_run<FMT, MT, RG, R, PRO_NONE, ONE, SHALLOW>(a, ProArgs{}, smem_raw);
 }
 
 // One column with an activation prologue (PRO_NORM before qkv / gate_up, PRO_COMB before o_proj).
