@@ -269,6 +269,16 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
                       double temperature, int32_t max_depth, double *resid_dev, int32_t *out_dev, void *hip_stream,
                       int32_t *out_host);
 
+/* sp_op_accept_tree with the tree arrays and the uniforms in ordinary host memory (the same reference interface and
+ * decision rule): token / trial_start / n_trials [n_nodes], trials [n_trials_total] and u [n_u] are copied by the CPU
+ * into a pinned block the library keeps per device, which the kernel reads directly (no copy on the stream, so the
+ * walk starts as soon as the stream reaches it).  Before refilling that block the call waits for the previous walk
+ * that read it; calls on one device must not overlap.  Same limits, outputs and errors as sp_op_accept_tree. */
+int sp_op_accept_tree_host(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld,
+                           int32_t n_nodes, const int32_t *token, const int32_t *trial_start, const int32_t *n_trials,
+                           const int32_t *trials, int32_t n_trials_total, const double *u, int32_t n_u,
+                           double temperature, int32_t max_depth, int32_t *out_dev, void *hip_stream, int32_t *out_host);
+
 #ifdef __cplusplus
 }
 #endif

@@ -80,6 +80,9 @@ SIGNATURES = {
     'sp_op_accept_tree': (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_int32, c_void_p, c_int32, ctypes.c_double, c_int32, c_void_p, c_void_p,
                                   c_void_p, c_void_p]),
+    'sp_op_accept_tree_host': (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_int32, c_void_p, c_int32, ctypes.c_double, c_int32, c_void_p,
+                                       c_void_p, c_void_p]),
 }
 
 _lib = None

@@ -1554,23 +1554,26 @@ int sp_op_sample_filtered(const float *logits_dev, int32_t vocab, int32_t ld, co
     });
 }
 
-int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld, int32_t n_nodes,
-                      const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
-                      const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,
-                      double temperature, int32_t max_depth, double *resid_dev, int32_t *out_dev, void *stream,
-                      int32_t *out_host) {
-    (void)resid_dev;
-    return guarded(nullptr, [&] {
-        require(p_logits_dev && q_logits_dev && token_dev && trial_start_dev && n_trials_dev && trials_dev && u_dev &&
-                    out_dev, SP_EINVAL, "NULL pointer");
-        require(n_trials_total >= 0 && n_trials_total <= 1024, SP_EINVAL, "n_trials_total must be in [0, 1024]");
+}  // extern "C"
+
+// The acceptance walk over device-readable tree arrays (device memory, or the library's pinned staging for the
+// host-array entry point).  `staged` (may be NULL): an event recorded after the launch, which the host-array entry
+// waits on before it refills its staging.
+static void accept_tree_run(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld,
+                            int32_t n_nodes, const int32_t *token, const int32_t *trial_start, const int32_t *n_trials,
+                            const int32_t *trials, int32_t n_trials_total, const double *u, int32_t n_u,
+                            double temperature, int32_t max_depth, int32_t *out_dev, hipStream_t st, int32_t *out_host,
+                            hipEvent_t staged) {
+    {
+        require(p_logits_dev && q_logits_dev && token && trial_start && n_trials && trials && u && out_dev, SP_EINVAL,
+                "NULL pointer");
+        require(n_trials_total >= 0 && n_trials_total <= ACC_MAX_TRIALS, SP_EINVAL, "n_trials_total must be in [0, 1024]");
         require(vocab >= 1 && vocab <= ACC_NB * ACC_T * ACC_PER && ld >= vocab, SP_EINVAL, "bad vocab / ld");
-        require(n_nodes >= 1 && n_nodes <= 64, SP_EINVAL, "n_nodes must be in [1, 64]");
+        require(n_nodes >= 1 && n_nodes <= ACC_MAX_NODES, SP_EINVAL, "n_nodes must be in [1, 64]");
         require(max_depth >= 1 && max_depth <= 63, SP_EINVAL, "max_depth must be in [1, 63]");
         require(n_u >= 1, SP_EINVAL, "need at least one uniform");
         require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
         // the kernel checks every node / trial / token index it follows before using it (err = 2 if one is bad)
-        hipStream_t st = (hipStream_t)stream;
         // exchange words and the error word in device memory, and a pinned host block the kernel writes its result
         // and completion tags into, one set per device; tags never repeat within 2^20 launches, so nothing needs
         // clearing between launches (the kernel writes every entry of out_dev itself).  The host polls the tags
@@ -1595,11 +1598,12 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         const AccScratch &sc = it->second;
         launches = launches % 0xFFFFFu + 1;
         const unsigned tag = launches << 12;
-        AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token_dev, trial_start_dev, n_trials_dev, trials_dev, u_dev,
+        AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token, trial_start, n_trials, trials, u,
                      n_u, 1.0 / temperature, sc.xbuf, sc.err, tag, n_nodes, n_trials_total, out_dev, max_depth, sc.host};
         volatile int32_t *hb = sc.host;
         hipLaunchKernelGGL(k_accept_tree, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
         HIPCHK(hipGetLastError());
+        if (staged) HIPCHK(hipEventRecord(staged, st));
         auto wait_tag = [&](int i) {
             for (long spin = 0; spin < (1l << 26); ++spin)
                 if (hb[i] == (int32_t)tag) return true;
@@ -1615,6 +1619,64 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
         const unsigned code = (err & ~0xfffu) == tag ? err & 0xfffu : 0u;
         require(code != 2, SP_EINVAL, "malformed tree: node, trial or token index out of range");
         require(code == 0, SP_EHIP, "acceptance exchange timed out");
+    }
+}
+
+extern "C" {
+
+int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld, int32_t n_nodes,
+                      const int32_t *token_dev, const int32_t *trial_start_dev, const int32_t *n_trials_dev,
+                      const int32_t *trials_dev, int32_t n_trials_total, const double *u_dev, int32_t n_u,
+                      double temperature, int32_t max_depth, double *resid_dev, int32_t *out_dev, void *stream,
+                      int32_t *out_host) {
+    (void)resid_dev;
+    return guarded(nullptr, [&] {
+        accept_tree_run(p_logits_dev, q_logits_dev, vocab, ld, n_nodes, token_dev, trial_start_dev, n_trials_dev,
+                        trials_dev, n_trials_total, u_dev, n_u, temperature, max_depth, out_dev, (hipStream_t)stream,
+                        out_host, nullptr);
+    });
+}
+
+int sp_op_accept_tree_host(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld,
+                           int32_t n_nodes, const int32_t *token, const int32_t *trial_start, const int32_t *n_trials,
+                           const int32_t *trials, int32_t n_trials_total, const double *u, int32_t n_u,
+                           double temperature, int32_t max_depth, int32_t *out_dev, void *stream, int32_t *out_host) {
+    return guarded(nullptr, [&] {
+        require(token && trial_start && n_trials && trials && u, SP_EINVAL, "NULL pointer");
+        require(n_nodes >= 1 && n_nodes <= ACC_MAX_NODES, SP_EINVAL, "n_nodes must be in [1, 64]");
+        require(n_trials_total >= 0 && n_trials_total <= ACC_MAX_TRIALS, SP_EINVAL, "n_trials_total must be in [0, 1024]");
+        require(n_u >= 1 && n_u <= (1 << 20), SP_EINVAL, "n_u must be in [1, 2^20]");
+        // per device: a pinned staging block the kernel reads the tree and the uniforms from (no copy on the stream),
+        // and an event after the last walk that read it (waited on before the block is refilled)
+        struct Stage { unsigned char *buf; size_t cap; hipEvent_t done; bool used; };
+        static std::map<int, Stage> stage_of;
+        int dev = 0;
+        HIPCHK(hipGetDevice(&dev));
+        Stage &sg = stage_of[dev];
+        const size_t ints = (size_t)3 * n_nodes + std::max(n_trials_total, 1);
+        const size_t need = (size_t)n_u * sizeof(double) + ints * sizeof(int32_t);
+        if (!sg.done) HIPCHK(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
+        if (sg.used) HIPCHK(hipEventSynchronize(sg.done));
+        if (sg.cap < need) {
+            if (sg.buf) HIPCHK(hipHostFree(sg.buf));
+            sg.buf = nullptr;
+            sg.cap = 0;
+            const size_t cap = std::max<size_t>(need, 64 * 1024);
+            HIPCHK(hipHostMalloc((void **)&sg.buf, cap, hipHostMallocCoherent));
+            sg.cap = cap;
+        }
+        double *su = (double *)sg.buf;
+        int32_t *si = (int32_t *)(sg.buf + (size_t)n_u * sizeof(double));
+        std::memcpy(su, u, (size_t)n_u * sizeof(double));
+        std::memcpy(si, token, (size_t)n_nodes * sizeof(int32_t));
+        std::memcpy(si + n_nodes, trial_start, (size_t)n_nodes * sizeof(int32_t));
+        std::memcpy(si + 2 * n_nodes, n_trials, (size_t)n_nodes * sizeof(int32_t));
+        if (n_trials_total > 0) std::memcpy(si + 3 * n_nodes, trials, (size_t)n_trials_total * sizeof(int32_t));
+        else si[3 * n_nodes] = 0;
+        sg.used = true;
+        accept_tree_run(p_logits_dev, q_logits_dev, vocab, ld, n_nodes, si, si + n_nodes, si + 2 * n_nodes,
+                        si + 3 * n_nodes, n_trials_total, su, n_u, temperature, max_depth, out_dev, (hipStream_t)stream,
+                        out_host, sg.done);
     });
 }
 

@@ -157,6 +157,10 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(const float *logits, int
 // rejection costs one reduction instead of a rewrite of the distribution.  All arithmetic is float64 with explicit
 // single roundings (no contraction): w = exp((l - m) * (1/T)), p_i = w_i / Z, d_i = p_i - c * q_i.
 constexpr int ACC_NB = 64, ACC_T = 256, ACC_PER = 16;
+// Tree inputs staged in LDS by every block at the start (one round of independent loads, also from pinned host
+// memory): up to ACC_MAX_NODES nodes, ACC_MAX_TRIALS trials and the first ACC_U_LDS uniforms (later ones are read
+// where they lie).
+constexpr int ACC_MAX_NODES = 64, ACC_MAX_TRIALS = 1024, ACC_U_LDS = 256;
 
 struct AcceptArgs {
     const float *p_logits;   // target logits [nodes][ld]
@@ -342,21 +346,33 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
     // contract them into fused multiply-adds; __dmul_rn / __dsub_rn are plain operators in HIP)
 #pragma clang fp contract(off)
     __shared__ AccShared sh;
+    __shared__ int s_token[ACC_MAX_NODES], s_tstart[ACC_MAX_NODES], s_ntr[ACC_MAX_NODES], s_trials[ACC_MAX_TRIALS];
+    __shared__ double s_u[ACC_U_LDS];
     const int C = (a.V + ACC_NB * ACC_T - 1) / (ACC_NB * ACC_T);
     const int lo = (blockIdx.x * ACC_T + threadIdx.x) * C;
     const int n = max(0, min(C, a.V - lo));
+    // the tree and the uniforms into LDS (independent loads, all in flight together)
+    for (int i = threadIdx.x; i < a.n_nodes; i += ACC_T) {
+        s_token[i] = a.token[i];
+        s_tstart[i] = a.trial_start[i];
+        s_ntr[i] = a.n_trials[i];
+    }
+    for (int i = threadIdx.x; i < a.n_trials_total; i += ACC_T) s_trials[i] = a.trials[i];
+    for (int i = threadIdx.x; i < min(a.n_u, ACC_U_LDS); i += ACC_T) s_u[i] = a.u[i];
+    __syncthreads();
+    auto uni = [&](int i) { return i < a.n_u ? (i < ACC_U_LDS ? s_u[i] : a.u[i]) : 0.5; };
     double wp[ACC_PER], wq[ACC_PER], w[ACC_PER];
     unsigned ex = 0;
     int cur = 0, k = 0, ui = 0, final_tok = -1, bonus = 0;
     bool alive = true;
     for (;;) {
         const float *pl = a.p_logits + (size_t)cur * a.ld;
-        const int nt = a.n_trials[cur];
-        const int t0 = a.trial_start[cur];
+        const int nt = s_ntr[cur];
+        const int t0 = s_tstart[cur];
         if (nt < 0 || t0 < 0 || t0 > a.n_trials_total - nt) { alive = acc_bad(a); break; }
         for (int j = t0; j < t0 + nt && alive; ++j) {
-            const int child = a.trials[j];
-            if (child <= 0 || child >= a.n_nodes || a.token[child] < 0 || a.token[child] >= a.V) alive = acc_bad(a);
+            const int child = s_trials[j];
+            if (child <= 0 || child >= a.n_nodes || s_token[child] < 0 || s_token[child] >= a.V) alive = acc_bad(a);
         }
         if (!alive) break;
         const bool draw_bonus = nt == 0 || k >= a.max_depth;
@@ -385,7 +401,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         if (draw_bonus) {
             // thread chunk sums of wp back into sh.tsum for the draw (block partials of wp are in sh.bpart0)
             (void)acc_block_sum(sp, sh);
-            final_tok = acc_draw(wp, lo, n, ui < a.n_u ? a.u[ui] : 0.5, sh.bpart0, sh);
+            final_tok = acc_draw(wp, lo, n, uni(ui), sh.bpart0, sh);
             ++ui;
             bonus = 1;
             break;
@@ -399,8 +415,8 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         int accepted = -1, J = 0;
         double c = 0.0, S = 0.0;
         for (int j = t0; j < t0 + nt; ++j) {
-            const int child = a.trials[j];
-            const int x = a.token[child];
+            const int child = s_trials[j];
+            const int x = s_token[child];
             const double px0 = __ddiv_rn(d_w(pl[x], Mp, a.invT), Zp);
             const double qx = __ddiv_rn(d_w(ql[x], Mq, a.invT), Zq);
             double px = px0;
@@ -408,7 +424,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
                 const double dx = __dsub_rn(px0, __dmul_rn(c, qx));
                 px = dx > 0.0 ? __ddiv_rn(dx, S) : 0.0;
             }
-            const double uu = ui < a.n_u ? a.u[ui] : 0.5;
+            const double uu = uni(ui);
             ++ui;
             if (uu < __ddiv_rn(px, qx)) { accepted = child; break; }
             // rejection: next residual numerator max(p - c q, 0) with c = 1 (first) or c + S
@@ -436,7 +452,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
             continue;
         }
         // every trial rejected: draw from the last residual (weights w, block partials in sh.bpart0)
-        final_tok = acc_draw(w, lo, n, ui < a.n_u ? a.u[ui] : 0.5, sh.bpart0, sh);
+        final_tok = acc_draw(w, lo, n, uni(ui), sh.bpart0, sh);
         ++ui;
         break;
     }

@@ -273,7 +273,6 @@ class TreeVerifier:
         self._lib = _lib
         self.torch = torch
         self._out = {}
-        self._stage = {}
 
     def forward(self, cache, tree: FlatTree, logits_out=None, graph=False, ids=True):
         """One pass over every node: node i is written at cache position cache.length + i, RoPE position
@@ -353,14 +352,14 @@ class TreeVerifier:
         return v
 
     def accept(self, p_logits, q_logits, tree: FlatTree, u, temperature):
-        """GPU acceptance walk (see sp_op_accept_tree).  p_logits / q_logits: device tensors [nodes, vocab].
+        """GPU acceptance walk (sp_op_accept_tree_host: the tree arrays and uniforms go from host memory straight to
+        the kernel, no copy on the stream).  p_logits / q_logits: device tensors [nodes, vocab].
         Returns (accepted node ids, final token, uniforms used, bonus)."""
         torch = self.torch
         dev = p_logits.device
         V = p_logits.shape[1]
         md = max(1, tree.max_depth)
-        # one host->device copy from a reused pinned buffer: float64 uniforms first (8-byte aligned), then the int32
-        # tree arrays (concatenated once per tree; the call is synchronous, so the buffer is free again when it returns)
+        # the int32 tree arrays, concatenated once per tree
         acc = getattr(tree, '_acc', None)
         if acc is None:
             ints = [tree.token, tree.trial_start, tree.n_trials, tree.trials if len(tree.trials) else [0]]
@@ -368,35 +367,22 @@ class TreeVerifier:
             acc = tree._acc = (np.concatenate([np.asarray(x, dtype=np.int32) for x in ints]),
                                [int(o) for o in np.cumsum([0] + sizes[:-1])])
         flat, rel = acc
-        nu = len(u)
-        total = nu * 2 + len(flat)
-        stage = self._stage.get(dev)
-        if stage is None or stage[0].numel() < total:
-            cap = max(total, 4096)
-            stage = self._stage[dev] = (torch.empty(cap, dtype=torch.int32, pin_memory=True),
-                                        torch.empty(cap, dtype=torch.int32, device=dev))
-        pinned, buf = stage
-        host = pinned.numpy()
-        host[:nu * 2] = np.asarray(u, dtype=np.float64).view(np.int32)
-        host[nu * 2:total] = flat
-        offs = [nu * 2 + o for o in rel]
-        buf[:total].copy_(pinned[:total], non_blocking=True)
+        uu = np.ascontiguousarray(u, dtype=np.float64)
         out = self._out.get((dev, md))
         if out is None:
             out = self._out[(dev, md)] = torch.empty(md + 4, dtype=torch.int32, device=dev)
         res = np.empty(md + 4, dtype=np.int32)
-        base = buf.data_ptr()
+        base = flat.ctypes.data
         at = lambda o: ctypes.c_void_p(base + 4 * o)
         ptr = lambda t: ctypes.c_void_p(t.data_ptr())
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        self._lib.check(self.engine.lib.sp_op_accept_tree(
-            ptr(p_logits), ptr(q_logits), V, p_logits.stride(0), tree.size, at(offs[0]), at(offs[1]), at(offs[2]),
-            at(offs[3]), len(tree.trials), at(0), nu, float(temperature), md, None, ptr(out), stream,
-            res.ctypes.data_as(ctypes.c_void_p)))
+        self._lib.check(self.engine.lib.sp_op_accept_tree_host(
+            ptr(p_logits), ptr(q_logits), V, p_logits.stride(0), tree.size, at(rel[0]), at(rel[1]), at(rel[2]),
+            at(rel[3]), len(tree.trials), ctypes.c_void_p(uu.ctypes.data), len(uu), float(temperature), md, ptr(out),
+            stream, res.ctypes.data_as(ctypes.c_void_p)))
         o = res.tolist()
         k = o[0]
         return o[1:1 + k], o[md + 1], o[md + 2], bool(o[md + 3])
-
 
 def sample_rows(lib_engine, logits, rows, u, temperature):
     """Seeded inverse-CDF draws from softmax(logits[rows[s]] / T) on the GPU (sp_op_sample)."""

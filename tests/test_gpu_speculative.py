@@ -74,6 +74,59 @@ def test_accept_tree_matches_oracle(model, V):
     assert accepted_total > 0       # the cases exercise acceptance, not only rejection
 
 
+
+def _accept_device_entry(eng, pd, qd, tree, u, T):
+    """sp_op_accept_tree with the tree arrays and uniforms in device memory."""
+    dev = eng.device
+    md = max(1, tree.max_depth)
+    arrs = [torch.tensor(np.asarray(x, dtype=np.int32), device=dev)
+            for x in (tree.token, tree.trial_start, tree.n_trials, tree.trials if len(tree.trials) else [0])]
+    ud = torch.tensor(np.asarray(u, dtype=np.float64), device=dev)
+    out = torch.empty(md + 4, dtype=torch.int32, device=dev)
+    res = np.empty(md + 4, dtype=np.int32)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    _lib.check(eng.lib.sp_op_accept_tree(ptr(pd), ptr(qd), pd.shape[1], pd.stride(0), tree.size, *[ptr(a) for a in arrs],
+                                         len(tree.trials), ptr(ud), len(u), float(T), md, None, ptr(out), stream,
+                                         res.ctypes.data_as(ctypes.c_void_p)))
+    torch.cuda.synchronize()
+    o = res.tolist()
+    assert o == out.cpu().tolist()
+    return o[1:1 + o[0]], o[md + 1], o[md + 2], bool(o[md + 3])
+
+
+@pytest.mark.parametrize('V', [64, 151936])
+def test_accept_tree_entries_agree(model, V):
+    """The device-array and host-array entry points take the same decisions (and the oracle's), including (small
+    vocabulary) a walk that consumes more uniforms than the kernel stages in LDS: 300 rejected trials of one child.
+    (With q = p off that child every other token has the same ratio p / q, so once c_j reaches it the residual is
+    rounding noise of p - c_j q; at 151936 entries that noise, not the rule, would pick the final token.)"""
+    cfg, w, eng, _ = model
+    verifier = TreeVerifier(eng)
+    rng = np.random.default_rng(V + 1)
+    dev = eng.device
+    cases = [_random_case(rng, V) for _ in range(3)]
+    if V < 1000:
+        # one child drawn 300 times, far more likely under q than under p: every trial is rejected
+        tree = flatten(1, [[2]] * 300)
+        p = rng.normal(size=(tree.size, V)).astype(np.float32)
+        q = p.copy()
+        p[0, 2] -= 8.0
+        q[0, 2] += 8.0
+        cases.append((tree, p, q))
+    for case, (tree, p, q) in enumerate(cases):
+        print(f'entries V={V} case={case}', flush=True)
+        u = sref.uniforms(11, case, 400)
+        pd, qd = torch.from_numpy(p).to(dev), torch.from_numpy(q).to(dev)
+        got_dev = _accept_device_entry(eng, pd, qd, tree, u, 0.8)
+        got_host = verifier.accept(pd, qd, tree, u, 0.8)
+        t = dict(token=tree.token, trial_start=tree.trial_start, n_trials=tree.n_trials, trials=tree.trials)
+        path, final, used, bonus, margin = sref.accept_tree(p, q, t, u, 0.8, tree.max_depth)
+        assert margin > MARGIN
+        assert tuple(got_dev) == tuple(got_host) == (path, final, used, bonus)
+        if case == 3:
+            assert path == [] and used == 301
+
 def test_tree_pass_equals_linear_paths(model):
     cfg, w, eng, _ = model
     prefix = random_prompt(12, cfg['vocab_size'], seed=4)
