@@ -880,33 +880,52 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
     // ---- mask, chunk-local max / exp / sum per row.  The key codes of the lane's 4 slot tiles and the range / tree
     // bits of its 4 rows are read once; the mask is selects only (ring key: inside the column's range; tree key:
     // its bit set in the column's ancestor mask; padding key: never).
-    int kpv[NST];
-#pragma unroll
-    for (int st = 0; st < NST; ++st) kpv[st] = kpos_s[16 * st + r16];
-    int clo[4], chi[4], ctc[4];
-    unsigned long long cmk[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = rt * 16 + 4 * g4 + j;
-        const int col = row < R ? row / G : 0;
-        clo[j] = clo_s[col]; chi[j] = chi_s[col]; ctc[j] = ctc_s[col]; cmk[j] = cmask_s[col];
+    // A chunk of ring keys that every column of the group sees whole (the prefix of a tree pass): the mask keeps
+    // every key, so only rows past R are masked (the same scores as the per-key test below gives there).
+    bool whole = v0 + CH <= gr.nlin;
+    if (whole) {
+        const int k_lo = gr.lo + v0, k_hi = gr.lo + v0 + CH - 1;
+        whole = __all(lane >= gr.ncols || (clo_s[lane] <= k_lo && chi_s[lane] >= k_hi));
     }
     float mrow[4], lrow[4];
+    if (whole) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool live = rt * 16 + 4 * g4 + j < R;
+#pragma unroll
+            for (int st = 0; st < NST; ++st) sc[st][j] = live ? sc[st][j] : -INFINITY;
+        }
+    } else {
+        int kpv[NST];
+#pragma unroll
+        for (int st = 0; st < NST; ++st) kpv[st] = kpos_s[16 * st + r16];
+        int clo[4], chi[4], ctc[4];
+        unsigned long long cmk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = rt * 16 + 4 * g4 + j;
+            const int col = row < R ? row / G : 0;
+            clo[j] = clo_s[col]; chi[j] = chi_s[col]; ctc[j] = ctc_s[col]; cmk[j] = cmask_s[col];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = rt * 16 + 4 * g4 + j;
+#pragma unroll
+            for (int st = 0; st < NST; ++st) {
+                const int kp = kpv[st];
+                const int tj = ~kp;                      // tree index of a tree key (kp = ~tj < 0)
+                const bool in_ring = (kp >= clo[j]) & (kp <= chi[j]);
+                const bool in_tree = (tj < ctc[j]) & (((cmk[j] >> (tj & 63)) & 1ull) != 0);
+                const bool ok = (row < R) & (kp != INT_MIN) & (kp >= 0 ? in_ring : in_tree);
+                sc[st][j] = ok ? sc[st][j] : -INFINITY;
+            }
+        }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int row = rt * 16 + 4 * g4 + j;
         float m = -INFINITY;
 #pragma unroll
-        for (int st = 0; st < NST; ++st) {
-            const int kp = kpv[st];
-            const int tj = ~kp;                      // tree index of a tree key (kp = ~tj < 0)
-            const bool in_ring = (kp >= clo[j]) & (kp <= chi[j]);
-            const bool in_tree = (tj < ctc[j]) & (((cmk[j] >> (tj & 63)) & 1ull) != 0);
-            const bool ok = (row < R) & (kp != INT_MIN) & (kp >= 0 ? in_ring : in_tree);
-            const float v = ok ? sc[st][j] : -INFINITY;
-            sc[st][j] = v;
-            m = fmaxf(m, v);
-        }
+        for (int st = 0; st < NST; ++st) m = fmaxf(m, sc[st][j]);
         m = row16_max(m);
         float l = 0.f;
 #pragma unroll
