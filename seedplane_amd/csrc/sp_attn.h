@@ -930,7 +930,8 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
         float l = 0.f;
 #pragma unroll
         for (int st = 0; st < NST; ++st) {
-            const float e = (m == -INFINITY || sc[st][j] == -INFINITY) ? 0.f : expf(sc[st][j] - m);
+            // the hardware exponential (one v_exp_f32 of x log2 e): P is rounded to fp16 before P V anyway
+            const float e = (m == -INFINITY || sc[st][j] == -INFINITY) ? 0.f : __expf(sc[st][j] - m);
             sc[st][j] = e;
             l += e;
         }
