@@ -1601,7 +1601,13 @@ static void accept_tree_run(const float *p_logits_dev, const float *q_logits_dev
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token, trial_start, n_trials, trials, u,
                      n_u, 1.0 / temperature, sc.xbuf, sc.err, tag, n_nodes, n_trials_total, out_dev, max_depth, sc.host};
         volatile int32_t *hb = sc.host;
-        hipLaunchKernelGGL(k_accept_tree, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
+        // entries per thread as a compile-time count (151936 entries: 10)
+        const int C = (vocab + ACC_NB * ACC_T - 1) / (ACC_NB * ACC_T);
+        if (C <= 2) hipLaunchKernelGGL(k_accept_tree<2>, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
+        else if (C <= 4) hipLaunchKernelGGL(k_accept_tree<4>, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
+        else if (C <= 8) hipLaunchKernelGGL(k_accept_tree<8>, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
+        else if (C <= 10) hipLaunchKernelGGL(k_accept_tree<10>, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
+        else hipLaunchKernelGGL(k_accept_tree<ACC_PER>, dim3(ACC_NB), dim3(ACC_T), 0, st, a);
         HIPCHK(hipGetLastError());
         if (staged) HIPCHK(hipEventRecord(staged, st));
         auto wait_tag = [&](int i) {

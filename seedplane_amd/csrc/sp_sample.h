@@ -279,6 +279,7 @@ __device__ float acc_block_max(float v, AccShared &sh) {
 // partials in bp).  Three levels, each "first entry whose running sum exceeds the target, else the last positive
 // entry": block (every block, redundantly), thread (thread 0 of the owning block), element (the owning thread).
 // If no weight is positive at all the token is 0.  Returns the token in the owning block, -1 in the others.
+template <int CP>
 __device__ int acc_draw(const double *w, int lo, int n, double u, const double *bp, AccShared &sh) {
     double total = 0.0;
     for (int b = 0; b < ACC_NB; ++b) total += bp[b];
@@ -315,7 +316,7 @@ __device__ int acc_draw(const double *w, int lo, int n, double u, const double *
         const double tl = sh.tl;
         double acc = 0.0;
         int pick = -1, lastpos = -1;
-        for (int i = 0; i < ACC_PER; ++i) {
+        for (int i = 0; i < CP; ++i) {
             if (i < n) {
                 if (w[i] > 0.0) lastpos = lo + i;
                 acc += w[i];
@@ -341,6 +342,9 @@ __device__ __forceinline__ void acc_put(const AcceptArgs &a, int i, int v) {
     if (a.host) a.host[ACC_HOST_OUT + i] = v;
 }
 
+// CP >= C: the entries per thread as a compile-time count, so every per-entry loop is straight-line code whose loads
+// and exponentials are independent (entries past the thread's n are read from a clamped index and masked).
+template <int CP>
 __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
     // p - c q products and differences are rounded separately, as the definition writes them (hipcc would otherwise
     // contract them into fused multiply-adds; __dmul_rn / __dsub_rn are plain operators in HIP)
@@ -361,7 +365,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
     for (int i = threadIdx.x; i < min(a.n_u, ACC_U_LDS); i += ACC_T) s_u[i] = a.u[i];
     __syncthreads();
     auto uni = [&](int i) { return i < a.n_u ? (i < ACC_U_LDS ? s_u[i] : a.u[i]) : 0.5; };
-    double wp[ACC_PER], wq[ACC_PER], w[ACC_PER];
+    double wp[CP], wq[CP], w[CP];
     unsigned ex = 0;
     int cur = 0, k = 0, ui = 0, final_tok = -1, bonus = 0;
     bool alive = true;
@@ -377,20 +381,39 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         if (!alive) break;
         const bool draw_bonus = nt == 0 || k >= a.max_depth;
         const float *ql = a.q_logits + (size_t)cur * a.ld;
-        // ---- global maxima
+        // ---- the node's logits (one batch of loads, clamped indices) and their global maxima
+        float lp[CP], lq[CP];
+#pragma unroll
+        for (int i = 0; i < CP; ++i) {
+            const int kk = min(lo + i, a.V - 1);
+            lp[i] = pl[kk];
+            lq[i] = ql[kk];
+        }
         float mp = -INFINITY, mq = -INFINITY;
-        for (int i = 0; i < n; ++i) { mp = fmaxf(mp, pl[lo + i]); if (!draw_bonus) mq = fmaxf(mq, ql[lo + i]); }
+#pragma unroll
+        for (int i = 0; i < CP; ++i) {
+            if (i < n) { mp = fmaxf(mp, lp[i]); mq = fmaxf(mq, lq[i]); }
+        }
+        if (draw_bonus) mq = -INFINITY;
         mp = acc_block_max(mp, sh);
         mq = acc_block_max(mq, sh);
         if (!(alive = acc_exchange(a, ex, (double)mp, (double)mq, sh))) break;
         float Mp = -INFINITY, Mq = -INFINITY;
         for (int b = 0; b < ACC_NB; ++b) { Mp = fmaxf(Mp, (float)sh.bpart0[b]); Mq = fmaxf(Mq, (float)sh.bpart1[b]); }
-        // ---- weights and normalisers
+        // ---- weights (every exponential independent) and normalisers (sequential sums of the thread's entries)
+        double ep[CP], eq[CP];
+#pragma unroll
+        for (int i = 0; i < CP; ++i) ep[i] = d_w(lp[i], Mp, a.invT);
+        if (!draw_bonus) {
+#pragma unroll
+            for (int i = 0; i < CP; ++i) eq[i] = d_w(lq[i], Mq, a.invT);
+        }
         double sp = 0.0, sq = 0.0;
-        for (int i = 0; i < ACC_PER; ++i) {
+#pragma unroll
+        for (int i = 0; i < CP; ++i) {
             if (i < n) {
-                wp[i] = d_w(pl[lo + i], Mp, a.invT); sp += wp[i];
-                if (!draw_bonus) { wq[i] = d_w(ql[lo + i], Mq, a.invT); sq += wq[i]; }
+                wp[i] = ep[i]; sp += wp[i];
+                if (!draw_bonus) { wq[i] = eq[i]; sq += wq[i]; }
             } else { wp[i] = 0.0; wq[i] = 0.0; }
         }
         const double bsp = acc_block_sum(sp, sh);
@@ -401,7 +424,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         if (draw_bonus) {
             // thread chunk sums of wp back into sh.tsum for the draw (block partials of wp are in sh.bpart0)
             (void)acc_block_sum(sp, sh);
-            final_tok = acc_draw(wp, lo, n, uni(ui), sh.bpart0, sh);
+            final_tok = acc_draw<CP>(wp, lo, n, uni(ui), sh.bpart0, sh);
             ++ui;
             bonus = 1;
             break;
@@ -409,9 +432,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         // ---- trials in draw order.  The normalised weights p_i / Zp and q_i / Zq are formed once per node (the
         // residual of every trial uses the same quotients)
 #pragma unroll
-        for (int i = 0; i < ACC_PER; ++i) {
-            if (i < n) { wp[i] = __ddiv_rn(wp[i], Zp); wq[i] = __ddiv_rn(wq[i], Zq); }
-        }
+        for (int i = 0; i < CP; ++i) { wp[i] = __ddiv_rn(wp[i], Zp); wq[i] = __ddiv_rn(wq[i], Zq); }
         int accepted = -1, J = 0;
         double c = 0.0, S = 0.0;
         for (int j = t0; j < t0 + nt; ++j) {
@@ -431,13 +452,14 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
             c = J == 0 ? 1.0 : c + S;
             ++J;
             double sr = 0.0;
-            for (int i = 0; i < ACC_PER; ++i) {
-                if (i < n) {
-                    const double d = __dsub_rn(wp[i], __dmul_rn(c, wq[i]));
-                    w[i] = d > 0.0 ? d : 0.0;
-                    sr += w[i];
-                } else w[i] = 0.0;
+#pragma unroll
+            for (int i = 0; i < CP; ++i) {
+                const double d = __dsub_rn(wp[i], __dmul_rn(c, wq[i]));
+                w[i] = (i < n && d > 0.0) ? d : 0.0;
             }
+#pragma unroll
+            for (int i = 0; i < CP; ++i)
+                if (i < n) sr += w[i];
             // leaves this residual's thread chunk sums in sh.tsum for a possible final draw
             const double bsr = acc_block_sum(sr, sh);
             if (!(alive = acc_exchange(a, ex, bsr, 0.0, sh))) break;
@@ -452,7 +474,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
             continue;
         }
         // every trial rejected: draw from the last residual (weights w, block partials in sh.bpart0)
-        final_tok = acc_draw(w, lo, n, uni(ui), sh.bpart0, sh);
+        final_tok = acc_draw<CP>(w, lo, n, uni(ui), sh.bpart0, sh);
         ++ui;
         break;
     }
