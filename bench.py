@@ -15,7 +15,7 @@ The JSON line also carries:
   roofline       the dominant kernel (the SwiGLU gate_up GEMV, the largest launch of the step), HIP-event timed
   cpu_baseline   the CPU oracle (fp32, dequantised weights) on a bounded sample of the same workload
   latency        per-token latency quantiles with one host synchronisation per token, the decode / draw split of a
-                 T > 0 token, and dispatches_per_token (kernels of the replayed step graph)
+                 T > 0 token, and dispatches_per_token (kernels of the recorded step)
   burst16_05b    Qwen2-0.5B fp16, 16 ragged requests x 32 tokens decoded as one batch
   spec           the full speculative loop (0.5B fp16 drafter, 8 x 4 drafts, T 0.8) on the 1.5B int8 target
   batch32_7b     Qwen2-7B int4, batch 32 at 8192 positions of fp16 KV each
@@ -209,7 +209,7 @@ def measured_traffic():
 def token_latency(eng, cache, token, n=64, warm=4):
     """Per-token latency as a caller sees it that needs each id before the next step (one host synchronisation per
     token, the reference's session loop, native/vulkan_decode/qwen_vk.cpp:883-897): quantiles over n tokens, the
-    kernels one step launches (the replayed graph's kernel nodes), and the split of a T > 0 token into the decode step
+    kernels one step launches (the recorded step's kernel nodes), and the split of a T > 0 token into the decode step
     and the GPU draw (top-k 50 / top-p 0.9 at T = 0.8 over the step's logits row, HIP events)."""
     import torch
     from seedplane_amd.speculative import uniforms

@@ -61,7 +61,7 @@ enum {
 enum {
     SP_F_LOGITS = 1,      /* run the final norm + LM head and produce fp32 logits for every column   */
     SP_F_ARGMAX = 2,      /* also produce the greedy id per column (first index on ties)             */
-    SP_F_GRAPH = 4,       /* capture the step into a hipGraph on first use and replay it afterwards  */
+    SP_F_GRAPH = 4,       /* record the step as graphs once; replayed when the caller waits per step */
     SP_F_PERSISTENT = 8,  /* accepted for compatibility; the step runs as the kernel chain (a whole-   */
                           /* step persistent kernel was slower than the chain and has been removed)  */
     SP_F_UNFUSED = 16,    /* one column: run every RMSNorm and attention combine as a kernel of its   */
@@ -143,8 +143,8 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
 int sp_engine_last_path(const sp_engine *e);
 
 /* Introspection (no counterpart in the reference; its decode report counts dispatches per token,
- * native/vulkan_decode/qwen_vk.cpp:866-870): kernels launched by the last sp_engine_forward call when it replayed a
- * graph (the kernel nodes of the recorded graph), -1 after an eager call. */
+ * native/vulkan_decode/qwen_vk.cpp:866-870): kernels launched by the last sp_engine_forward call with SP_F_GRAPH
+ * (the kernel nodes of its recorded step), -1 after a call without it. */
 int sp_engine_last_dispatches(const sp_engine *e);
 
 /* Device pointer to the engine's fp32 logits buffer [max_tokens][vocab] holding the last SP_F_LOGITS call. */

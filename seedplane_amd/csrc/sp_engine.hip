@@ -503,7 +503,7 @@ struct sp_engine {
     int *d_move = nullptr;
 
     std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;
-    std::map<std::tuple<int, int, int>, int> graph_kernels;     // kernel nodes of each recorded graph
+    std::map<std::tuple<int, int, int>, int> graph_kernels;     // kernel nodes of each recorded step part
     int last_dispatches = -1;                                   // kernels of the last graph replay (-1: eager call)
     void drop_graphs() {
         for (auto &kv : graphs) (void)hipGraphExecDestroy(kv.second);
@@ -1121,9 +1121,16 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
         e->upload(n, toks, ap);
         if (use_graph) {
-            // The step runs in up to three parts: a short first part (the embedding and layer 0, as plain launches)
-            // starts the GPU while the host is still submitting the rest as two graphs, which a caller that waits for
-            // every call (tree verification) would otherwise see as idle GPU time.
+            // The step's three parts (the embedding and layer 0, layers 1-4, the rest) are recorded as graphs once per
+            // (columns, flags, attention plan); their kernel nodes are the reported dispatch count.  The first part
+            // always runs as plain launches (the GPU starts after the first of them, not after a graph launch's
+            // set-up).  The others run as plain launches too when the host runs ahead of the GPU -- a fed greedy loop,
+            // or several columns, whose kernels each take longer than their launch -- because a replayed graph costs
+            // the GPU more per kernel than in-order launches (A/B of whole steps: fed bs1 0.974 -> 0.968 ms/token, tree
+            // pass 1.499 -> 1.490 ms, 16-request 0.5B burst 18.0k -> 18.2k tok/s, bs16 1.442 -> 1.430 ms); a single
+            // column whose caller waits for every token replays them (plain launches there leave the GPU waiting for
+            // the host: 0.995 -> 1.02-1.05 ms per token).
+            const bool plain = (sflags & SP_F_FEED) || n > 1;
             const int L = d.n_layers;
             const int cuts[4] = {0, std::min(1, L), std::min(5, L), L};
             const int plan_code = ap.mq ? (ap.mq_ch == 128 ? 1 << 20 : 0) + ap.ngroups * 1024 + ap.splits
@@ -1166,13 +1173,8 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
                     it = e->graphs.emplace(key, ge).first;
                     e->graph_kernels[key] = kernels;
                 }
-                if (part == 0) {
-                    // the first part's kernels as plain launches (its graph is recorded for its kernel count): the
-                    // GPU starts after the first of them instead of after a graph launch's set-up (bs1 -0.5 %)
-                    e->step(n, sflags, ap, cuts[0], cuts[1]);
-                } else {
-                    HIPCHK(hipGraphLaunch(it->second, e->stream));
-                }
+                if (part == 0 || plain) e->step(n, sflags, ap, cuts[part], cuts[part + 1]);
+                else HIPCHK(hipGraphLaunch(it->second, e->stream));
                 total += e->graph_kernels[key];
             }
             e->last_dispatches = total;

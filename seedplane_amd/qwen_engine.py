@@ -214,7 +214,7 @@ class Qwen2Engine:
 
     @property
     def last_dispatches(self):
-        """Kernels the last engine call launched when it replayed a graph (-1 after an eager call)."""
+        """Kernels the last engine call with graph=True launched (its recorded step), -1 after a call without it."""
         return int(self.lib.sp_engine_last_dispatches(self.h))
 
     def fill_cache(self, cache, n_positions, seed=0, scale=1.0):
