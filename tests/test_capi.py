@@ -64,6 +64,26 @@ def test_null_arguments_are_rejected_with_einval():
         _lib.check(_lib.SP_EINVAL)
 
 
+def test_accept_tree_host_rejects_bad_arguments_before_any_gpu_call():
+    """The host-array acceptance entry point checks its arrays and sizes before it touches the GPU."""
+    lib = _lib.load()
+    ints = (ctypes.c_int32 * 1024)()
+    u = (ctypes.c_double * 4)(0.1, 0.2, 0.3, 0.4)
+    p = lambda a: ctypes.cast(a, ctypes.c_void_p)
+    out = (ctypes.c_int32 * 8)()
+
+    def call(token=ints, n_nodes=3, n_trials_total=2, uu=u, n_u=4):
+        return lib.sp_op_accept_tree_host(None, None, 1000, 1000, n_nodes, p(token) if token else None, p(ints),
+                                          p(ints), p(ints), n_trials_total, p(uu) if uu else None, n_u, 0.8, 1,
+                                          None, None, p(out))
+    assert call(token=None) == _lib.SP_EINVAL
+    assert call(uu=None) == _lib.SP_EINVAL
+    assert call(n_nodes=0) == _lib.SP_EINVAL
+    assert call(n_nodes=65) == _lib.SP_EINVAL
+    assert call(n_trials_total=1025) == _lib.SP_EINVAL
+    assert call(n_u=0) == _lib.SP_EINVAL
+
+
 def test_engine_create_without_gpu_fails_cleanly():
     import torch
     if torch.cuda.is_available():
