@@ -1139,8 +1139,8 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
             for (int part = 0; part < 3; ++part) {
                 if (cuts[part] >= cuts[part + 1]) continue;      // empty (short models); the head ran in its part
                 auto key = std::make_tuple(n, sflags | (part << 8), plan_code);
-                auto it = e->graphs.find(key);
-                if (it == e->graphs.end()) {
+                const bool replay = part > 0 && !plain;
+                if (!e->graph_kernels.count(key) || (replay && !e->graphs.count(key))) {
                     // record on the private stream (the caller's may be the null stream, which cannot capture)
                     hipGraph_t g;
                     hipStream_t run_stream = e->stream;
@@ -1167,14 +1167,19 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
                         HIPCHK(hipGraphNodeGetType(nd, &ty));
                         kernels += ty == hipGraphNodeTypeKernel;
                     }
-                    hipGraphExec_t ge;
-                    HIPCHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
-                    (void)hipGraphDestroy(g);
-                    it = e->graphs.emplace(key, ge).first;
+                    if (replay) {               // instantiated only for the parts that are replayed
+                        hipGraphExec_t ge;
+                        hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+                        (void)hipGraphDestroy(g);
+                        HIPCHK(ie);
+                        e->graphs[key] = ge;
+                    } else {
+                        (void)hipGraphDestroy(g);
+                    }
                     e->graph_kernels[key] = kernels;
                 }
-                if (part == 0 || plain) e->step(n, sflags, ap, cuts[part], cuts[part + 1]);
-                else HIPCHK(hipGraphLaunch(it->second, e->stream));
+                if (replay) HIPCHK(hipGraphLaunch(e->graphs[key], e->stream));
+                else e->step(n, sflags, ap, cuts[part], cuts[part + 1]);
                 total += e->graph_kernels[key];
             }
             e->last_dispatches = total;
