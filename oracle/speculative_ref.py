@@ -211,11 +211,44 @@ def _first_exceeding(parts, target):
     return last, run_last, gap
 
 
-def draw3(w, u):
+def block_weights(logits, temperature):
+    """Acceptance-walk weights of one row: group g (ACC_T consecutive chunks) takes its maximum m_g, its entries'
+    local weights e_i = exp((l_i - m_g) * (1/T)) (all 0 when m_g = -inf) and their sum s_g in chunk_sums3 order; with
+    M the row maximum, f_g = exp((m_g - M) * (1/T)), the normaliser Z is the sum of the partials s_g * f_g in group
+    order.  Returns (e, f per entry, partials, Z)."""
+    l = np.asarray(logits, dtype=np.float32)
+    V = len(l)
+    G = ACC_NB * ACC_T
+    C = -(-V // G)
+    padded = np.full(G * C, -np.inf, dtype=np.float32)
+    padded[:V] = l
+    m = padded.reshape(ACC_NB, ACC_T * C).max(axis=1).astype(np.float64)
+    inv_t = 1.0 / float(temperature)
+    mm = np.repeat(m, ACC_T * C)[:V]
+    live = mm > -np.inf
+    with np.errstate(invalid='ignore'):
+        e = np.where(live, np.exp((l.astype(np.float64) - mm) * inv_t), 0.0)
+    f = np.exp((m - m.max()) * inv_t)
+    parts = chunk_sums3(e)[1] * f
+    return e, np.repeat(f, ACC_T * C)[:V], parts, np.cumsum(parts)[-1]
+
+
+def walk_probs(logits, temperature):
+    """p_i = e_i * (f_g / Z), the acceptance walk's probabilities (block_weights)."""
+    e, f, _, Z = block_weights(logits, temperature)
+    return e * (f / Z)
+
+
+def draw3(w, u, bsum=None):
     """Inverse CDF over the acceptance-walk chunk tree (group, chunk, element), with its fallbacks: a level whose
     running sums never exceed the target (rounding) takes its last positive entry; with no positive weight at all
-    the token is 0.  Returns (token, margin) with margin the smallest relative gap at a compared boundary."""
-    tsum, bsum, total, C = chunk_sums3(w)
+    the token is 0.  bsum: group partials to use instead of the sums of w's chunks (a bonus draw takes
+    block_weights' partials).  Returns (token, margin) with margin the smallest relative gap at a compared boundary."""
+    tsum, own, total, C = chunk_sums3(w)
+    if bsum is None:
+        bsum = own
+    else:
+        total = np.cumsum(bsum)[-1]
     V = len(w)
     target = u * total
     scale = total if total > 0 else 1.0
@@ -244,27 +277,26 @@ def accept_tree(p_logits, q_logits, tree, u, temperature, max_depth):
     node are its children in draft-branch order, repeats included).  Each trial x is accepted when u < r(x) / q(x),
     r the current residual: p before any rejection, then max(p - c_j q, 0) / S_j after j rejections, c_1 = 1,
     c_{j+1} = c_j + S_j, S_j the sum of the numerator (equal to renormalising max(r - q, 0) after every rejection).
-    Float64 with the kernel's single roundings and chunk_sums3 order.  Returns (accepted node ids, final token,
-    uniforms used, bonus flag, smallest decision margin)."""
+    Float64 with the kernel's single roundings and chunk_sums3 order; p and q from walk_probs, a bonus draw over
+    block_weights' e * f.  Returns (accepted node ids, final token, uniforms used, bonus flag, smallest decision margin)."""
     cur, ui, path = 0, 0, []
     margin = np.inf
     take = lambda i: u[i] if i < len(u) else 0.5
     while True:
-        wp = softmax_weights(p_logits[cur], temperature)
         nt = tree['n_trials'][cur]
         if nt == 0 or len(path) >= max_depth:
-            tok, mg = draw3(wp, take(ui))
+            e, f, bp, _ = block_weights(p_logits[cur], temperature)
+            tok, mg = draw3(e * f, take(ui), bp)
             return path, tok, ui + 1, True, min(margin, mg)
-        wq = softmax_weights(q_logits[cur], temperature)
-        Zp = chunk_sums3(wp)[2]
-        Zq = chunk_sums3(wq)[2]
+        pp = walk_probs(p_logits[cur], temperature)
+        qq = walk_probs(q_logits[cur], temperature)
         c, S, J, accepted, w = 0.0, 0.0, 0, -1, None
         t0 = tree['trial_start'][cur]
         for j in range(t0, t0 + nt):
             child = tree['trials'][j]
             x = tree['token'][child]
-            px = wp[x] / Zp
-            qx = wq[x] / Zq
+            px = pp[x]
+            qx = qq[x]
             if J > 0:
                 dx = px - c * qx
                 px = dx / S if dx > 0.0 else 0.0
@@ -278,7 +310,7 @@ def accept_tree(p_logits, q_logits, tree, u, temperature, max_depth):
                 break
             c = 1.0 if J == 0 else c + S
             J += 1
-            d = wp / Zp - c * (wq / Zq)
+            d = pp - c * qq
             w = np.where(d > 0.0, d, 0.0)
             S = chunk_sums3(w)[2]
         if accepted >= 0:

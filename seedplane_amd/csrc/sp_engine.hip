@@ -1599,9 +1599,9 @@ static void accept_tree_run(const float *p_logits_dev, const float *q_logits_dev
         HIPCHK(hipGetDevice(&dev));
         auto it = scratch_of.find(dev);
         if (it == scratch_of.end()) {
-            unsigned long long *xb = dev_alloc<unsigned long long>(4 * ACC_NB * 4);
+            unsigned long long *xb = dev_alloc<unsigned long long>(4 * ACC_NB * ACC_XW);
             unsigned *err = dev_alloc<unsigned>(1);
-            HIPCHK(hipMemset(xb, 0, 4 * ACC_NB * 4 * sizeof(unsigned long long)));
+            HIPCHK(hipMemset(xb, 0, 4 * ACC_NB * ACC_XW * sizeof(unsigned long long)));
             HIPCHK(hipMemset(err, 0, sizeof(unsigned)));
             int32_t *host = nullptr;
             HIPCHK(hipHostMalloc((void **)&host, (ACC_HOST_OUT + 64 + 4) * sizeof(int32_t), hipHostMallocCoherent));

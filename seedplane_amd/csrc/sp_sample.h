@@ -152,11 +152,18 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(const float *logits, int
 // tagged 64-bit words (32-bit payload + 32-bit tag, single-copy atomic; relaxed agent-scope atomics, no fences), so
 // every block holds every partial and takes every accept / reject decision itself.
 //
+// Normalisers in one exchange per node: block b finds its maximum m_b, its entries' local weights
+// e_i = exp((l_i - m_b) * (1/T)) (all zero if m_b = -inf) and their sum s_b, and the exchange hands every block every
+// (m_b, s_b).  With M = max m_b and f_b = exp((m_b - M) * (1/T)): Z = sum over b of s_b * f_b in block order, the
+// probability of entry i of block b is p_i = e_i * (f_b / Z), and a bonus draw takes the weights e_i * f_b with block
+// partials s_b * f_b.
+//
 // Residual after j >= 1 rejections at a node: r_j = max(p - c_j q, 0) / S_j with c_1 = 1, S_j = sum of the numerator,
 // c_{j+1} = c_j + S_j -- algebraically the same as replacing p by norm(max(p - q, 0)) after each rejection, but each
 // rejection costs one reduction instead of a rewrite of the distribution.  All arithmetic is float64 with explicit
-// single roundings (no contraction): w = exp((l - m) * (1/T)), p_i = w_i / Z, d_i = p_i - c * q_i.
+// single roundings (no contraction): d_i = p_i - c * q_i.
 constexpr int ACC_NB = 64, ACC_T = 256, ACC_PER = 16;
+constexpr int ACC_XW = 6;   // exchange words per block: two doubles (two words each) and two floats
 // Tree inputs staged in LDS by every block at the start (one round of independent loads, also from pinned host
 // memory): up to ACC_MAX_NODES nodes, ACC_MAX_TRIALS trials and the first ACC_U_LDS uniforms (later ones are read
 // where they lie).
@@ -173,7 +180,7 @@ struct AcceptArgs {
     const double *u;         // uniforms, consumed in order
     int n_u;
     double invT;
-    unsigned long long *xbuf;   // exchange words [4][ACC_NB][4]
+    unsigned long long *xbuf;   // exchange words [4][ACC_NB][ACC_XW]
     unsigned *err;           // tag_base | 1 if an exchange timed out, tag_base | 2 for a malformed tree (words of
                              // earlier launches carry other tags, so the word is never cleared)
     unsigned tag_base;       // distinct per launch (low 12 bits are the exchange counter)
@@ -189,6 +196,8 @@ constexpr int ACC_HOST_OUT = 16;
 struct AccShared {
     double tsum[ACC_T];      // thread chunk sums
     double bpart0[ACC_NB], bpart1[ACC_NB];
+    float bmax0[ACC_NB], bmax1[ACC_NB];
+    double fac0[ACC_NB], fac1[ACC_NB];
     float fred[ACC_T / 64];
     double tl;
     int found;
@@ -199,49 +208,60 @@ __device__ __forceinline__ double d_w(float l, float m, double invT) {
     return exp(__dmul_rn(__dsub_rn((double)l, (double)m), invT));
 }
 
-// All-gather of two doubles per block.  Returns false on timeout (every block then stops).
 // Whether a block of this launch has reported a failure.
 __device__ __forceinline__ bool acc_failed(const AcceptArgs &a) {
     const unsigned e = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return (e & ~0xfffu) == a.tag_base && (e & 0xfffu) != 0;
 }
 
-__device__ bool acc_exchange(const AcceptArgs &a, unsigned &ex, double v0, double v1, AccShared &sh) {
+// All-gather of two doubles (and, with W = ACC_XW, two floats) per block into sh.bpart0 / bpart1 (bmax0 / bmax1).
+// Returns false on timeout (every block then stops).
+template <int W>
+__device__ bool acc_exchange(const AcceptArgs &a, unsigned &ex, double v0, double v1, float f0, float f1,
+                             AccShared &sh) {
+    static_assert(W == 4 || W == ACC_XW, "two doubles, or two doubles and two floats");
     const unsigned tag = a.tag_base | (ex & 0xfffu);
-    unsigned long long *slot = a.xbuf + (size_t)(ex & 3u) * ACC_NB * 4;
+    unsigned long long *slot = a.xbuf + (size_t)(ex & 3u) * ACC_NB * ACC_XW;
     ++ex;
     __syncthreads();
     if (threadIdx.x == 0) {
         const unsigned long long b0 = __double_as_longlong(v0), b1 = __double_as_longlong(v1);
         const unsigned long long t = (unsigned long long)tag << 32;
-        unsigned long long *w = slot + blockIdx.x * 4;
+        unsigned long long *w = slot + blockIdx.x * ACC_XW;
         __hip_atomic_store(w + 0, t | (b0 & 0xffffffffull), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(w + 1, t | (b0 >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(w + 2, t | (b1 & 0xffffffffull), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(w + 3, t | (b1 >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (W == ACC_XW) {
+            __hip_atomic_store(w + 4, t | __float_as_uint(f0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(w + 5, t | __float_as_uint(f1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     if (threadIdx.x == 0) sh.ok = 1;
     __syncthreads();
     if (threadIdx.x < ACC_NB) {
-        unsigned long long *w = slot + threadIdx.x * 4;
-        unsigned long long x0, x1, x2, x3;
+        unsigned long long *w = slot + threadIdx.x * ACC_XW;
+        unsigned long long x[W];
         long spins = 0;
         for (;;) {
-            x0 = __hip_atomic_load(w + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            x1 = __hip_atomic_load(w + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            x2 = __hip_atomic_load(w + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            x3 = __hip_atomic_load(w + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if ((unsigned)(x0 >> 32) == tag && (unsigned)(x1 >> 32) == tag && (unsigned)(x2 >> 32) == tag &&
-                (unsigned)(x3 >> 32) == tag)
-                break;
+            bool all = true;
+#pragma unroll
+            for (int i = 0; i < W; ++i) x[i] = __hip_atomic_load(w + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < W; ++i) all = all && (unsigned)(x[i] >> 32) == tag;
+            if (all) break;
             if (++spins > (1l << 22) || acc_failed(a)) {
                 __hip_atomic_store(a.err, a.tag_base | 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 sh.ok = 0;
                 break;
             }
         }
-        sh.bpart0[threadIdx.x] = __longlong_as_double((long long)((x0 & 0xffffffffull) | (x1 << 32)));
-        sh.bpart1[threadIdx.x] = __longlong_as_double((long long)((x2 & 0xffffffffull) | (x3 << 32)));
+        sh.bpart0[threadIdx.x] = __longlong_as_double((long long)((x[0] & 0xffffffffull) | (x[1] << 32)));
+        sh.bpart1[threadIdx.x] = __longlong_as_double((long long)((x[2] & 0xffffffffull) | (x[3] << 32)));
+        if (W == ACC_XW) {
+            sh.bmax0[threadIdx.x] = __uint_as_float((unsigned)x[W == ACC_XW ? 4 : 0]);
+            sh.bmax1[threadIdx.x] = __uint_as_float((unsigned)x[W == ACC_XW ? 5 : 0]);
+        }
     }
     __syncthreads();
     return sh.ok != 0;
@@ -365,7 +385,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
     for (int i = threadIdx.x; i < min(a.n_u, ACC_U_LDS); i += ACC_T) s_u[i] = a.u[i];
     __syncthreads();
     auto uni = [&](int i) { return i < a.n_u ? (i < ACC_U_LDS ? s_u[i] : a.u[i]) : 0.5; };
-    double wp[CP], wq[CP], w[CP];
+    double wp[CP], w[CP];
     unsigned ex = 0;
     int cur = 0, k = 0, ui = 0, final_tok = -1, bonus = 0;
     bool alive = true;
@@ -381,7 +401,9 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         if (!alive) break;
         const bool draw_bonus = nt == 0 || k >= a.max_depth;
         const float *ql = a.q_logits + (size_t)cur * a.ld;
-        // ---- the node's logits (one batch of loads, clamped indices) and their global maxima
+        // ---- the node's logits (one batch of loads, clamped indices), this block's maxima, its local weights
+        // e_i = exp((l_i - m_b) / T) (zero in a block without a finite logit) and their block sums s_b; one exchange
+        // of (s_b, m_b) for p and q
         float lp[CP], lq[CP];
 #pragma unroll
         for (int i = 0; i < CP; ++i) {
@@ -394,52 +416,71 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         for (int i = 0; i < CP; ++i) {
             if (i < n) { mp = fmaxf(mp, lp[i]); mq = fmaxf(mq, lq[i]); }
         }
-        if (draw_bonus) mq = -INFINITY;
         mp = acc_block_max(mp, sh);
-        mq = acc_block_max(mq, sh);
-        if (!(alive = acc_exchange(a, ex, (double)mp, (double)mq, sh))) break;
-        float Mp = -INFINITY, Mq = -INFINITY;
-        for (int b = 0; b < ACC_NB; ++b) { Mp = fmaxf(Mp, (float)sh.bpart0[b]); Mq = fmaxf(Mq, (float)sh.bpart1[b]); }
-        // ---- weights (every exponential independent) and normalisers (sequential sums of the thread's entries)
+        mq = draw_bonus ? -INFINITY : acc_block_max(mq, sh);
+        const bool livep = mp > -INFINITY, liveq = mq > -INFINITY;
         double ep[CP], eq[CP];
 #pragma unroll
-        for (int i = 0; i < CP; ++i) ep[i] = d_w(lp[i], Mp, a.invT);
+        for (int i = 0; i < CP; ++i) ep[i] = livep ? d_w(lp[i], mp, a.invT) : 0.0;
         if (!draw_bonus) {
 #pragma unroll
-            for (int i = 0; i < CP; ++i) eq[i] = d_w(lq[i], Mq, a.invT);
+            for (int i = 0; i < CP; ++i) eq[i] = liveq ? d_w(lq[i], mq, a.invT) : 0.0;
         }
         double sp = 0.0, sq = 0.0;
 #pragma unroll
         for (int i = 0; i < CP; ++i) {
             if (i < n) {
-                wp[i] = ep[i]; sp += wp[i];
-                if (!draw_bonus) { wq[i] = eq[i]; sq += wq[i]; }
-            } else { wp[i] = 0.0; wq[i] = 0.0; }
+                sp += ep[i];
+                if (!draw_bonus) sq += eq[i];
+            }
         }
         const double bsp = acc_block_sum(sp, sh);
         const double bsq = acc_block_sum(sq, sh);
-        if (!(alive = acc_exchange(a, ex, bsp, bsq, sh))) break;
-        double Zp = 0.0, Zq = 0.0;
-        for (int b = 0; b < ACC_NB; ++b) { Zp += sh.bpart0[b]; Zq += sh.bpart1[b]; }
+        if (!(alive = acc_exchange<ACC_XW>(a, ex, bsp, bsq, mp, mq, sh))) break;
+        float Mp = -INFINITY, Mq = -INFINITY;
+        for (int b = 0; b < ACC_NB; ++b) { Mp = fmaxf(Mp, sh.bmax0[b]); Mq = fmaxf(Mq, sh.bmax1[b]); }
+        // factors f_b = exp((m_b - M) / T) of the global maxima and the block partials s_b * f_b (thread b, block b)
+        if (threadIdx.x < ACC_NB) {
+            const int b = threadIdx.x;
+            const double fp = d_w(sh.bmax0[b], Mp, a.invT);
+            sh.fac0[b] = fp;
+            sh.bpart0[b] = __dmul_rn(sh.bpart0[b], fp);
+            if (!draw_bonus) {
+                const double fq = d_w(sh.bmax1[b], Mq, a.invT);
+                sh.fac1[b] = fq;
+                sh.bpart1[b] = __dmul_rn(sh.bpart1[b], fq);
+            }
+        }
+        __syncthreads();
         if (draw_bonus) {
-            // thread chunk sums of wp back into sh.tsum for the draw (block partials of wp are in sh.bpart0)
+            // weights e_i * f_b; thread chunk sums into sh.tsum, block partials s_b * f_b in sh.bpart0
+            const double f = sh.fac0[blockIdx.x];
+            sp = 0.0;
+#pragma unroll
+            for (int i = 0; i < CP; ++i) {
+                wp[i] = i < n ? __dmul_rn(ep[i], f) : 0.0;
+                if (i < n) sp += wp[i];
+            }
             (void)acc_block_sum(sp, sh);
             final_tok = acc_draw<CP>(wp, lo, n, uni(ui), sh.bpart0, sh);
             ++ui;
             bonus = 1;
             break;
         }
-        // ---- trials in draw order.  The normalised weights p_i / Zp and q_i / Zq are formed once per node (the
-        // residual of every trial uses the same quotients)
-#pragma unroll
-        for (int i = 0; i < CP; ++i) { wp[i] = __ddiv_rn(wp[i], Zp); wq[i] = __ddiv_rn(wq[i], Zq); }
+        double Zp = 0.0, Zq = 0.0;
+        for (int b = 0; b < ACC_NB; ++b) { Zp += sh.bpart0[b]; Zq += sh.bpart1[b]; }
+        // ---- trials in draw order, with p_i = e_i * (f_b / Zp) and q_i likewise (formed only after a rejection)
+        const double gp = __ddiv_rn(sh.fac0[blockIdx.x], Zp), gq = __ddiv_rn(sh.fac1[blockIdx.x], Zq);
+        const int span = ACC_T * C;     // entries per block
         int accepted = -1, J = 0;
         double c = 0.0, S = 0.0;
         for (int j = t0; j < t0 + nt; ++j) {
             const int child = s_trials[j];
             const int x = s_token[child];
-            const double px0 = __ddiv_rn(d_w(pl[x], Mp, a.invT), Zp);
-            const double qx = __ddiv_rn(d_w(ql[x], Mq, a.invT), Zq);
+            const int bx = x / span;
+            const float mpx = sh.bmax0[bx], mqx = sh.bmax1[bx];
+            const double px0 = mpx > -INFINITY ? __dmul_rn(d_w(pl[x], mpx, a.invT), __ddiv_rn(sh.fac0[bx], Zp)) : 0.0;
+            const double qx = mqx > -INFINITY ? __dmul_rn(d_w(ql[x], mqx, a.invT), __ddiv_rn(sh.fac1[bx], Zq)) : 0.0;
             double px = px0;
             if (J > 0) {
                 const double dx = __dsub_rn(px0, __dmul_rn(c, qx));
@@ -454,7 +495,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
             double sr = 0.0;
 #pragma unroll
             for (int i = 0; i < CP; ++i) {
-                const double d = __dsub_rn(wp[i], __dmul_rn(c, wq[i]));
+                const double d = __dsub_rn(__dmul_rn(ep[i], gp), __dmul_rn(c, __dmul_rn(eq[i], gq)));
                 w[i] = (i < n && d > 0.0) ? d : 0.0;
             }
 #pragma unroll
@@ -462,7 +503,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
                 if (i < n) sr += w[i];
             // leaves this residual's thread chunk sums in sh.tsum for a possible final draw
             const double bsr = acc_block_sum(sr, sh);
-            if (!(alive = acc_exchange(a, ex, bsr, 0.0, sh))) break;
+            if (!(alive = acc_exchange<4>(a, ex, bsr, 0.0, 0.f, 0.f, sh))) break;
             S = 0.0;
             for (int b = 0; b < ACC_NB; ++b) S += sh.bpart0[b];
         }
