@@ -147,6 +147,15 @@ int sp_engine_last_path(const sp_engine *e);
  * (the kernel nodes of its recorded step), -1 after a call without it. */
 int sp_engine_last_dispatches(const sp_engine *e);
 
+/* Host function, no GPU call (no counterpart in the reference, whose tree verification builds position ids and
+ * masks with torch ops on the host): fills the n columns of one tree pass over a cache of `length` positions.
+ * Node i (parents before children, depth[i] = its distance from the root, mask[i] = bit j set for every ancestor j
+ * and for i itself) gets pos = length + depth[i], slot = (length + i) mod n_slots, ctx = [max(0, pos - window + 1)
+ * (0 when window == 0, full attention), length - 1], tree_base = length mod n_slots, tree_count = n, and its token
+ * and mask.  n in [1, 64]; SP_EINVAL for NULL arrays or out-of-range sizes. */
+int sp_tree_columns(int32_t n, const int32_t *token, const int32_t *depth, const uint64_t *mask, int32_t seq,
+                    int64_t length, int32_t n_slots, int32_t window, sp_token *out);
+
 /* Device pointer to the engine's fp32 logits buffer [max_tokens][vocab] holding the last SP_F_LOGITS call. */
 int sp_engine_logits(sp_engine *e, float **logits_dev);
 

@@ -20,6 +20,7 @@ SP_F_LOGITS, SP_F_ARGMAX, SP_F_GRAPH, SP_F_PERSISTENT, SP_F_UNFUSED, SP_F_FEED =
 
 # Every function the header declares, with its ctypes signature.
 c_int, c_int32, c_size_t, c_uint64, c_float = ctypes.c_int, ctypes.c_int32, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float
+c_int64 = ctypes.c_int64
 c_void_p, c_char_p = ctypes.c_void_p, ctypes.c_char_p
 
 
@@ -50,7 +51,7 @@ SIGNATURES = {
     'sp_engine_load': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     'sp_engine_kv_reserve': (c_int, [c_void_p, c_int32, c_int32]),
     'sp_engine_kv_grow': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
-    'sp_engine_forward': (c_int, [c_void_p, c_int32, ctypes.POINTER(Token), c_int32, c_void_p, c_void_p]),
+    'sp_engine_forward': (c_int, [c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     'sp_engine_logits': (c_int, [c_void_p, ctypes.POINTER(c_void_p)]),
     'sp_engine_kv_move': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     'sp_engine_sync': (c_int, [c_void_p]),
@@ -63,6 +64,7 @@ SIGNATURES = {
     'sp_engine_kv_fill': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_uint64, c_float]),
     'sp_engine_time_gemv': (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(c_float),
                                     ctypes.POINTER(c_uint64)]),
+    'sp_tree_columns': (c_int, [c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int32, c_int32, c_void_p]),
     'sp_op_argmax_workspace': (c_size_t, [c_int32, c_int32]),
     'sp_op_argmax': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     'sp_op_argmax_noalloc': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),

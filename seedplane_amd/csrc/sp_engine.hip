@@ -1378,6 +1378,31 @@ int sp_engine_bytes(const sp_engine *e, uint64_t *wb, uint64_t *kb) {
     return SP_OK;
 }
 
+int sp_tree_columns(int32_t n, const int32_t *token, const int32_t *depth, const uint64_t *mask, int32_t seq,
+                    int64_t length, int32_t n_slots, int32_t window, sp_token *out) {
+    if (n < 1 || n > 64) { g_err = "a tree pass has 1 to 64 nodes"; return SP_EINVAL; }
+    if (!token || !depth || !mask || !out) { g_err = "tree column arrays are NULL"; return SP_EINVAL; }
+    if (n_slots < 1 || window < 0 || seq < 0 || length < 0 || length + 64 + 64 > INT32_MAX) {
+        g_err = "bad slot count, window, sequence or cache length";
+        return SP_EINVAL;
+    }
+    const int32_t P = (int32_t)length, base = (int32_t)(length % n_slots);
+    for (int i = 0; i < n; ++i) {
+        if (depth[i] < 0 || depth[i] >= 64) { g_err = "tree depth out of range"; return SP_EINVAL; }
+        sp_token &c = out[i];
+        c.token = token[i];
+        c.seq = seq;
+        c.pos = P + depth[i];
+        c.slot = (int32_t)((base + i) % n_slots);
+        c.ctx_lo = window > 0 ? std::max(0, c.pos - window + 1) : 0;
+        c.ctx_hi = P - 1;
+        c.tree_base = base;
+        c.tree_count = n;
+        c.tree_mask = mask[i];
+    }
+    return SP_OK;
+}
+
 // ---------------------------------------------------------------------------------------------- standalone ops
 size_t sp_op_argmax_workspace(int32_t rows, int32_t cols) {
     (void)cols;

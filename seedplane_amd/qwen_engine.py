@@ -305,6 +305,14 @@ class Qwen2Engine:
         else:
             n = len(cols)
             arr = (_lib.Token * n)(*[_lib.Token(*c) for c in cols])
+        return self._forward(n, arr, flags, logits_out, want_ids)
+
+    def run_raw(self, n, cols_addr, flags, logits_out=None, want_ids=False):
+        """run() over n TOKEN_DTYPE records at host address cols_addr (an int), for callers that fill the records
+        in place (TreeVerifier.forward)."""
+        return self._forward(n, cols_addr, flags, logits_out, want_ids)
+
+    def _forward(self, n, arr, flags, logits_out, want_ids):
         ids = np.zeros(n, dtype=np.int32) if want_ids else None
         if want_ids:
             flags |= _lib.SP_F_ARGMAX | _lib.SP_F_LOGITS

@@ -273,6 +273,8 @@ class TreeVerifier:
         self._lib = _lib
         self.torch = torch
         self._out = {}
+        self._colbuf = np.empty(64, dtype=_lib.TOKEN_DTYPE)       # the columns of the latest pass (forward)
+        self._colbuf_ptr = self._colbuf.ctypes.data
 
     def forward(self, cache, tree: FlatTree, logits_out=None, graph=False, ids=True):
         """One pass over every node: node i is written at cache position cache.length + i, RoPE position
@@ -283,9 +285,9 @@ class TreeVerifier:
         engine's next forward call)."""
         e = self.engine
         n = tree.size
-        cols = self.columns(cache, tree)
+        self._fill_columns(cache, tree, self._colbuf_ptr)
         flags = self._lib.SP_F_LOGITS | (self._lib.SP_F_GRAPH if graph else 0)
-        out = e.run(cols, flags, logits_out=logits_out, want_ids=ids)
+        out = e.run_raw(n, self._colbuf_ptr, flags, logits_out=logits_out, want_ids=ids)
         if ids:
             return out
         return logits_out if logits_out is not None else e.logits_view(n)
@@ -294,6 +296,12 @@ class TreeVerifier:
         """The engine columns of one tree pass (a numpy array of _lib.TOKEN_DTYPE): node i in slot
         (cache.length + i) mod slots, which is tree slot i of the pass, at RoPE position cache.length + depth[i],
         seeing the cached positions before the root (the window's part of them) and the tree nodes of its mask."""
+        cols = np.empty(tree.size, dtype=self._lib.TOKEN_DTYPE)
+        self._fill_columns(cache, tree, cols.ctypes.data)
+        return cols
+
+    def _fill_columns(self, cache, tree: FlatTree, dst):
+        """columns() into the TOKEN_DTYPE records at address dst (room for tree.size records)."""
         e = self.engine
         e._check_cache(cache)
         n = tree.size
@@ -302,20 +310,10 @@ class TreeVerifier:
         P = cache.length
         if cache.window is None and P + n > cache.capacity:
             raise ValueError(f'KV cache capacity {cache.capacity} exceeded')
-        S = e._pool_slots
-        tok, depth, masks = tree.column_arrays()
-        cols = np.empty(n, dtype=self._lib.TOKEN_DTYPE)
-        pos = P + depth
-        cols['token'] = tok
-        cols['seq'] = cache.seq
-        cols['pos'] = pos
-        cols['slot'] = (P + np.arange(n, dtype=np.int64)) % S
-        cols['ctx_lo'] = 0 if cache.window is None else np.maximum(0, pos - cache.window + 1)
-        cols['ctx_hi'] = P - 1
-        cols['tree_base'] = P % S
-        cols['tree_count'] = n
-        cols['tree_mask'] = masks
-        return cols
+        ptrs = getattr(tree, '_col_ptrs', None)
+        if ptrs is None:                               # addresses of the tree's arrays (they live with the tree)
+            ptrs = tree._col_ptrs = tuple(a.ctypes.data for a in tree.column_arrays())
+        self._lib.check(e.lib.sp_tree_columns(n, *ptrs, cache.seq, P, e._pool_slots, cache.window or 0, dst))
 
     def commit(self, cache, tree: FlatTree, path_nodes):
         """Keep the root and the accepted path nodes (in order) in the cache: their K/V move to consecutive slots

@@ -108,3 +108,51 @@ def test_engine_rejects_unsupported_shapes_before_touching_the_gpu():
     h = ctypes.c_void_p()
     assert lib.sp_engine_create(ctypes.byref(d), ctypes.byref(h)) == _lib.SP_EINVAL
     assert b'head_dim' in lib.sp_last_error()
+
+
+def _columns_numpy(tok, depth, masks, seq, P, S, window):
+    """The column rule written out with numpy: node i at pos P + depth[i], slot (P + i) mod S, context
+    [max(0, pos - window + 1) or 0, P - 1], tree block based at P mod S."""
+    import numpy as np
+    n = len(tok)
+    cols = np.zeros(n, dtype=_lib.TOKEN_DTYPE)
+    pos = P + depth
+    cols['token'], cols['seq'], cols['pos'] = tok, seq, pos
+    cols['slot'] = (P + np.arange(n)) % S
+    cols['ctx_lo'] = 0 if not window else np.maximum(0, pos - window + 1)
+    cols['ctx_hi'], cols['tree_base'], cols['tree_count'], cols['tree_mask'] = P - 1, P % S, n, masks
+    return cols
+
+
+@pytest.mark.parametrize('P,S,window', [(0, 4096, 0), (2048, 4096, 0), (4090, 4096, 0), (9000, 1088, 1024),
+                                        (3, 64, 2), (123456, 70000, 0)])
+def test_tree_columns_match_the_column_rule(P, S, window):
+    """sp_tree_columns (host only) against the rule for flattened random trees, with ring wrap-around and windows."""
+    import numpy as np
+    from seedplane_amd.speculative import flatten
+    lib = _lib.load()
+    rng = np.random.default_rng(P)
+    for nb, depth in [(1, 1), (8, 4), (5, 7), (3, 21)]:
+        tree = flatten(7, [list(rng.integers(0, 50, depth)) for _ in range(nb)])
+        tok, dep, masks = tree.column_arrays()
+        out = np.empty(tree.size, dtype=_lib.TOKEN_DTYPE)
+        rc = lib.sp_tree_columns(tree.size, tok.ctypes.data, dep.ctypes.data, masks.ctypes.data, 3, P, S, window,
+                                 out.ctypes.data)
+        assert rc == _lib.SP_OK
+        assert out.tobytes() == _columns_numpy(tok, dep, masks, 3, P, S, window).tobytes()
+
+
+def test_tree_columns_reject_bad_arguments():
+    import numpy as np
+    lib = _lib.load()
+    a = np.zeros(65, np.int32)
+    m = np.zeros(65, np.uint64)
+    out = np.empty(65, dtype=_lib.TOKEN_DTYPE)
+    call = lambda n=2, P=10, S=16, w=0, d=a: lib.sp_tree_columns(n, a.ctypes.data, d.ctypes.data, m.ctypes.data, 0,
+                                                                  P, S, w, out.ctypes.data)
+    assert call() == _lib.SP_OK
+    assert call(n=0) == _lib.SP_EINVAL and call(n=65) == _lib.SP_EINVAL
+    assert call(S=0) == _lib.SP_EINVAL and call(P=-1) == _lib.SP_EINVAL and call(w=-1) == _lib.SP_EINVAL
+    assert call(P=2 ** 31) == _lib.SP_EINVAL
+    assert call(d=np.full(65, 64, np.int32)) == _lib.SP_EINVAL
+    assert lib.sp_tree_columns(2, None, a.ctypes.data, m.ctypes.data, 0, 1, 16, 0, out.ctypes.data) == _lib.SP_EINVAL
