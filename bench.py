@@ -111,7 +111,8 @@ def verify_cost(eng, cfg, prefix=2048, n_branches=8, depth=4, reps=20):
         p = verifier.forward(cache, tree, graph=True, ids=False)   # logits for the acceptance walk (engine buffer)
     sync()
     t_verify = (time.perf_counter() - t0) / reps
-    q = p + 0.3 * torch.randn_like(p)
+    g = torch.Generator(device=p.device).manual_seed(0)     # a fixed drafter: every run walks the same way
+    q = p + 0.3 * torch.randn(p.shape, generator=g, device=p.device)
     u = uniforms(3, 0, 64)
     verifier.accept(p, q, tree, u, 0.8)
     sync()

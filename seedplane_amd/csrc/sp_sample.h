@@ -198,7 +198,7 @@ struct AccShared {
     double bpart0[ACC_NB], bpart1[ACC_NB];
     float bmax0[ACC_NB], bmax1[ACC_NB];
     double fac0[ACC_NB], fac1[ACC_NB];
-    float fred[ACC_T / 64];
+    float fred[ACC_T / 64], fred2[ACC_T / 64];
     double tl;
     int found;
     int ok;
@@ -283,6 +283,29 @@ __device__ double acc_block_sum(double mine, AccShared &sh) {
 #pragma unroll
     for (int j = 0; j < ACC_T / 64; ++j) t += wsum[j];
     return t;
+}
+
+// Block sums / maxima of two values at once (one barrier round for both); no thread sums are kept.
+__device__ void acc_block_sum2(double &a, double &b, AccShared &sh) {
+    __shared__ double w2[2][ACC_T / 64];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { a += __shfl_xor(a, o, SP_WAVE); b += __shfl_xor(b, o, SP_WAVE); }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) { w2[0][threadIdx.x >> 6] = a; w2[1][threadIdx.x >> 6] = b; }
+    __syncthreads();
+    a = 0.0; b = 0.0;
+#pragma unroll
+    for (int j = 0; j < ACC_T / 64; ++j) { a += w2[0][j]; b += w2[1][j]; }
+}
+
+__device__ void acc_block_max2(float &a, float &b, AccShared &sh) {
+    a = wave_max(a);
+    b = wave_max(b);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) { sh.fred[threadIdx.x >> 6] = a; sh.fred2[threadIdx.x >> 6] = b; }
+    __syncthreads();
+    a = sh.fred[0]; b = sh.fred2[0];
+    for (int j = 1; j < ACC_T / 64; ++j) { a = fmaxf(a, sh.fred[j]); b = fmaxf(b, sh.fred2[j]); }
 }
 
 __device__ float acc_block_max(float v, AccShared &sh) {
@@ -401,6 +424,9 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         if (!alive) break;
         const bool draw_bonus = nt == 0 || k >= a.max_depth;
         const float *ql = a.q_logits + (size_t)cur * a.ld;
+        // the first trial's logits, loaded with the rows (the tree was validated above)
+        const int x0 = nt > 0 ? s_token[s_trials[t0]] : 0;
+        const float lpx0 = pl[x0], lqx0 = ql[x0];
         // ---- the node's logits (one batch of loads, clamped indices), this block's maxima, its local weights
         // e_i = exp((l_i - m_b) / T) (zero in a block without a finite logit) and their block sums s_b; one exchange
         // of (s_b, m_b) for p and q
@@ -416,8 +442,8 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         for (int i = 0; i < CP; ++i) {
             if (i < n) { mp = fmaxf(mp, lp[i]); mq = fmaxf(mq, lq[i]); }
         }
-        mp = acc_block_max(mp, sh);
-        mq = draw_bonus ? -INFINITY : acc_block_max(mq, sh);
+        if (draw_bonus) mq = -INFINITY;
+        acc_block_max2(mp, mq, sh);
         const bool livep = mp > -INFINITY, liveq = mq > -INFINITY;
         double ep[CP], eq[CP];
 #pragma unroll
@@ -434,9 +460,8 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
                 if (!draw_bonus) sq += eq[i];
             }
         }
-        const double bsp = acc_block_sum(sp, sh);
-        const double bsq = acc_block_sum(sq, sh);
-        if (!(alive = acc_exchange<ACC_XW>(a, ex, bsp, bsq, mp, mq, sh))) break;
+        acc_block_sum2(sp, sq, sh);
+        if (!(alive = acc_exchange<ACC_XW>(a, ex, sp, sq, mp, mq, sh))) break;
         float Mp = -INFINITY, Mq = -INFINITY;
         for (int b = 0; b < ACC_NB; ++b) { Mp = fmaxf(Mp, sh.bmax0[b]); Mq = fmaxf(Mq, sh.bmax1[b]); }
         // factors f_b = exp((m_b - M) / T) of the global maxima and the block partials s_b * f_b (thread b, block b)
@@ -479,8 +504,10 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
             const int x = s_token[child];
             const int bx = x / span;
             const float mpx = sh.bmax0[bx], mqx = sh.bmax1[bx];
-            const double px0 = mpx > -INFINITY ? __dmul_rn(d_w(pl[x], mpx, a.invT), __ddiv_rn(sh.fac0[bx], Zp)) : 0.0;
-            const double qx = mqx > -INFINITY ? __dmul_rn(d_w(ql[x], mqx, a.invT), __ddiv_rn(sh.fac1[bx], Zq)) : 0.0;
+            float lpx = lpx0, lqx = lqx0;
+            if (j != t0) { lpx = pl[x]; lqx = ql[x]; }
+            const double px0 = mpx > -INFINITY ? __dmul_rn(d_w(lpx, mpx, a.invT), __ddiv_rn(sh.fac0[bx], Zp)) : 0.0;
+            const double qx = mqx > -INFINITY ? __dmul_rn(d_w(lqx, mqx, a.invT), __ddiv_rn(sh.fac1[bx], Zq)) : 0.0;
             double px = px0;
             if (J > 0) {
                 const double dx = __dsub_rn(px0, __dmul_rn(c, qx));
