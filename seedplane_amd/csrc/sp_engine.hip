@@ -45,6 +45,10 @@ struct Fail {
 inline void require(bool ok, int code, const std::string &msg) {
     if (!ok) throw Fail{code, msg};
 }
+// A literal message builds its string only on failure (per-column checks run on every call).
+inline void require(bool ok, int code, const char *msg) {
+    if (!ok) throw Fail{code, msg};
+}
 
 template <class T>
 T *dev_alloc(size_t count, uint64_t *acct = nullptr) {
