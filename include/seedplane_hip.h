@@ -147,8 +147,9 @@ int sp_engine_last_path(const sp_engine *e);
  * (the kernel nodes of its recorded step), -1 after a call without it. */
 int sp_engine_last_dispatches(const sp_engine *e);
 
-/* Host function, no GPU call (no counterpart in the reference, whose tree verification builds position ids and
- * masks with torch ops on the host): fills the n columns of one tree pass over a cache of `length` positions.
+/* Host function, no GPU call (no counterpart in the reference: its verification is a linear batch whose positions
+ * the engine derives from the cache length, qwen_engine.py:99-103): fills the n columns of one tree pass over a
+ * cache of `length` positions.
  * Node i (parents before children, depth[i] = its distance from the root, mask[i] = bit j set for every ancestor j
  * and for i itself) gets pos = length + depth[i], slot = (length + i) mod n_slots, ctx = [max(0, pos - window + 1)
  * (0 when window == 0, full attention), length - 1], tree_base = length mod n_slots, tree_count = n, and its token
