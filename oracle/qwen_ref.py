@@ -13,8 +13,12 @@ needs to be checked against:
                 projections, RoPE cos/sin, K/V cache and attention output are fp16 tensors, the norms compute in fp32
                 and cast their output (qwen_engine.py:90-92), logits are cast to fp32 (:143).  Emulated as fp32
                 arithmetic rounded to fp16 after every reference op (what fp16 GEMMs with fp32 accumulation give);
-      'hip'  -- fp16 where the HIP engine stores fp16 (normalised GEMV inputs, K/V cache, attention output, SwiGLU
-                activation), fp32 elsewhere (residual stream, projection outputs, RoPE, logits).
+      'hip'  -- fp16 at every point where a fp16-activation engine may store fp16: normalised GEMV inputs ('x', the
+                union of 'xq' before qkv, 'xg' before gate_up and 'xh' before the head), K/V cache ('kv'), attention
+                output ('attn'), SwiGLU activation ('act'); fp32 elsewhere (residual stream, projection outputs,
+                RoPE, logits);
+      a set of those point names -- fp16 at exactly those points (e.g. {'kv'}: only the K/V cache, the rounding
+                a fp16 cache mandates).
 The cache here is never a ring: it holds every position, and the window is applied through the mask.
 """
 import math
@@ -23,6 +27,8 @@ import torch
 import torch.nn.functional as F
 
 from .quant_ref import dequant_all
+
+HIP_POINTS = frozenset(('x', 'xq', 'xg', 'xh', 'kv', 'attn', 'act'))   # storage points a set may name
 
 
 class RefCache:
@@ -39,9 +45,16 @@ class RefCache:
 class RefQwen2:
     def __init__(self, cfg, tensors, storage=None):
         """qwen_engine.py:35-80: config fields, inv_freq, fused qkv / gate_up packing, fp32 norms."""
-        if storage not in (None, 'fp16', 'hip'):
+        if storage in (None, 'fp16'):
+            points = frozenset()
+        elif storage == 'hip':
+            points = HIP_POINTS
+        elif isinstance(storage, (set, frozenset, tuple, list)) and set(storage) <= HIP_POINTS:
+            points = frozenset(storage)
+        else:
             raise ValueError(f'unknown storage {storage!r}')
-        self.storage = storage
+        self.storage = storage if isinstance(storage, (str, type(None))) else points
+        self.points = points
         self.cfg = cfg
         self.n_layers = cfg['num_hidden_layers']
         self.n_heads = cfg['num_attention_heads']
@@ -76,14 +89,17 @@ class RefQwen2:
         return RefCache(self.n_layers, capacity, self.n_kv_heads, self.head_dim)
 
     def _r(self, t, *kinds):
-        """Round `t` to fp16 when the storage mode stores this tensor kind in fp16."""
-        return t.half().float() if self.storage in kinds else t
+        """Round `t` to fp16 when the storage mode stores this tensor kind in fp16 ('fp16': the reference's fp16
+        tensors; a point name: that fp16-activation storage point)."""
+        hit = (self.storage == 'fp16' and 'fp16' in kinds) or any(k in self.points for k in kinds)
+        return t.half().float() if hit else t
 
-    def _norm(self, x, weight):
-        """qwen_engine.py:90-92: fp32 x * rsqrt(mean(x^2) + eps), times the weight before the cast."""
+    def _norm(self, x, weight, point='x'):
+        """qwen_engine.py:90-92: fp32 x * rsqrt(mean(x^2) + eps), times the weight before the cast.  `point` names the
+        GEMV the output feeds ('xq' qkv, 'xg' gate_up, 'xh' the head; 'x' rounds all three)."""
         xf = x.float()
         z = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return self._r(z * weight, 'fp16', 'hip')
+        return self._r(z * weight, 'fp16', 'x', point)
 
     @staticmethod
     def _rotate_half(x):
@@ -113,27 +129,27 @@ class RefQwen2:
         x = F.embedding(ids, self.embed)[None]
         for l, ly in enumerate(self.layers):
             residual = x
-            h = self._norm(x, ly['in_norm'])
+            h = self._norm(x, ly['in_norm'], 'xq')
             qkv = r16(F.linear(h, ly['qkv_w'], ly['qkv_b']))
             q, k, v = qkv.split((H, NKV * HD, NKV * HD), dim=-1)
             q = q.view(1, qlen, NH, HD)
             k = k.view(1, qlen, NKV, HD)
             v = v.view(1, qlen, NKV, HD)
             q, k = self._rope(q, k, positions)
-            cache.keys[l][:, start:start + qlen].copy_(self._r(k, 'hip'))
-            cache.values[l][:, start:start + qlen].copy_(self._r(v, 'hip'))
+            cache.keys[l][:, start:start + qlen].copy_(self._r(k, 'kv'))
+            cache.values[l][:, start:start + qlen].copy_(self._r(v, 'kv'))
             kk = cache.keys[l][:, :start + qlen].repeat_interleave(NH // NKV, dim=2)
             vv = cache.values[l][:, :start + qlen].repeat_interleave(NH // NKV, dim=2)
             qt, kt, vt = (z.transpose(1, 2) for z in (q, kk, vv))
-            attn = self._r(F.scaled_dot_product_attention(qt, kt, vt, attn_mask=allowed), 'fp16', 'hip')
+            attn = self._r(F.scaled_dot_product_attention(qt, kt, vt, attn_mask=allowed), 'fp16', 'attn')
             x = r16(residual + r16(F.linear(attn.transpose(1, 2).reshape(1, qlen, H), ly['o_w'])))
             residual = x
-            h = self._norm(x, ly['post_norm'])
+            h = self._norm(x, ly['post_norm'], 'xg')
             gate, up = r16(F.linear(h, ly['gate_up_w'])).chunk(2, dim=-1)
-            act = self._r(r16(r16(F.silu(gate)) * up), 'hip')
+            act = self._r(r16(r16(F.silu(gate)) * up), 'act')
             x = r16(residual + r16(F.linear(act, ly['down_w'])))
         cache.length += qlen
-        x = self._norm(x, self.final_norm)
+        x = self._norm(x, self.final_norm, 'xh')
         logits = r16(F.linear(x if all_logits else x[:, -1:], self.head)).float()[0]
         return logits
 

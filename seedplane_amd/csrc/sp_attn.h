@@ -47,8 +47,9 @@ __global__ void __launch_bounds__(256) k_embed(const uint8_t *w, const f16 *sz, 
     }
 }
 
-// out[b][k] = fp16(x * rsqrt(mean(x^2) + eps) * w).  Replaces Qwen2Engine._norm (qwen_engine.py:90-92): the weight
-// multiply happens in fp32 before the cast.  One block of 1024 threads per column; every load (x, the weight and
+// out[b][k] = fp16(x * rsqrt(mean(x^2) + eps) * w), and with out_lo the fp16 remainder of that fp32 value (split_f16).
+// Replaces Qwen2Engine._norm (qwen_engine.py:90-92): the weight multiply happens in fp32 before the cast.  One block
+// of 1024 threads per column; every load (x, the weight and
 // the NP split-K slices) is issued before the first use.  With NP > 0 the residual update of a split-K GEMV is
 // completed first: x[b] += part[0][b] + ... + part[NP-1][b] (in slice order) and written back to x.
 constexpr int NORM_THREADS = 1024, NORM_PER_THREAD = 4;
@@ -57,7 +58,7 @@ constexpr int NORM_THREADS = 1024, NORM_PER_THREAD = 4;
 // indices (elements past H re-read element H - 1 and become zeros after loading), so they are in flight together.
 template <int NP, int NG>
 __device__ __forceinline__ void rmsnorm_body(float *x, int ldx, const float *part, size_t pstride, const float *w, int H,
-                                             float eps, f16 *out, int ldo, int mtp) {
+                                             float eps, f16 *out, f16 *out_lo, int ldo, int mtp) {
     __shared__ float red[16];
     const int b = blockIdx.x;
     float *xr = x + (size_t)b * ldx;
@@ -88,24 +89,32 @@ __device__ __forceinline__ void rmsnorm_body(float *x, int ldx, const float *par
             if (k < H) xr[k] = v[i];
         }
     }
+    // the sum of squares in one fixed rounding order (no contraction: each square rounded, then added in element
+    // order), which the GEMV norm prologue repeats bit for bit
     float ss = 0.f;
+    {
+#pragma clang fp contract(off)
 #pragma unroll
-    for (int i = 0; i < NORM_PER_THREAD; ++i) ss += v[i] * v[i];
+        for (int i = 0; i < NORM_PER_THREAD; ++i) ss += v[i] * v[i];
+    }
     ss = block_sum_dpp(ss, red);
     const float rs = 1.0f / sqrtf(ss / (float)H + eps);
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
         const int k = threadIdx.x + i * NORM_THREADS;
-        if (k < H) out[act_off(b, k, ldo, mtp)] = (f16)((v[i] * rs) * wk[i]);
+        f16 hi, lo;
+        split_f16((v[i] * rs) * wk[i], hi, lo);
+        if (k < H) out[act_off(b, k, ldo, mtp)] = hi;
+        if (k < H && out_lo) out_lo[act_off(b, k, ldo, mtp)] = lo;
     }
 }
 template <int NP>
 __global__ void __launch_bounds__(NORM_THREADS) k_rmsnorm(float *x, int ldx, const float *part, size_t pstride,
-                                                          const float *w, int H, float eps, f16 *out, int ldo,
-                                                          int mtp) {
-    if (H <= NORM_THREADS) rmsnorm_body<NP, 1>(x, ldx, part, pstride, w, H, eps, out, ldo, mtp);
-    else if (H <= 2 * NORM_THREADS) rmsnorm_body<NP, 2>(x, ldx, part, pstride, w, H, eps, out, ldo, mtp);
-    else rmsnorm_body<NP, NORM_PER_THREAD>(x, ldx, part, pstride, w, H, eps, out, ldo, mtp);
+                                                          const float *w, int H, float eps, f16 *out, f16 *out_lo,
+                                                          int ldo, int mtp) {
+    if (H <= NORM_THREADS) rmsnorm_body<NP, 1>(x, ldx, part, pstride, w, H, eps, out, out_lo, ldo, mtp);
+    else if (H <= 2 * NORM_THREADS) rmsnorm_body<NP, 2>(x, ldx, part, pstride, w, H, eps, out, out_lo, ldo, mtp);
+    else rmsnorm_body<NP, NORM_PER_THREAD>(x, ldx, part, pstride, w, H, eps, out, out_lo, ldo, mtp);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -485,9 +494,11 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
     };
     load_sub(0, 0);
     if (DEC_SUB > 1) load_sub(1, 1);
-    // Q fragments (rows = query heads of this kv head, scaled, fp16): unconditional vector loads from a clamped row
-    // (a load under a per-lane condition is issued and waited for one at a time)
-    f16x8 qa[ST];
+    // Q fragments (rows = query heads of this kv head, scaled, fp16 with their fp16 remainders: the scores take two
+    // MFMAs per step, so Q enters them at fp32-class precision -- the scores at long contexts are large, and a query
+    // rounded to fp16 alone moves the softmax weights by more than the fp16 logits bar): unconditional vector loads
+    // from a clamped row (a load under a per-lane condition is issued and waited for one at a time)
+    f16x8 qa[ST], ql[ST];
     {
         const float *qrow = a.q + (size_t)b * a.NH * HD + (size_t)(kvh * G + min(r16, G - 1)) * HD + g4 * 8;
         f32x4 qv[ST][2];
@@ -500,7 +511,12 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
 #pragma unroll
         for (int st = 0; st < ST; ++st)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qa[st][e] = (f16)(qv[st][e >> 2][e & 3] * qs);
+            for (int e = 0; e < 8; ++e) {
+                f16 hi, lo;
+                split_f16(qv[st][e >> 2][e & 3] * qs, hi, lo);
+                qa[st][e] = hi;
+                ql[st][e] = lo;
+            }
     }
     float mrow[4], lrow[4];
     f32x4 o[NDT];
@@ -522,7 +538,10 @@ __global__ void __launch_bounds__(64 * NWV) k_attn_dec(AttnArgs a, f16 *out, int
         for (int kt = 0; kt < 2; ++kt) {
             sc2[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int st = 0; st < ST; ++st) sc2[kt] = mfma16(qa[st], kf[slot][kt][st], sc2[kt]);
+            for (int st = 0; st < ST; ++st) {
+                sc2[kt] = mfma16(qa[st], kf[slot][kt][st], sc2[kt]);
+                sc2[kt] = mfma16(ql[st], kf[slot][kt][st], sc2[kt]);
+            }
         }
         if (sc + 2 < DEC_SUB) load_sub(sc + 2, slot);      // the slot's registers are consumed: refill them
         // online softmax: lane holds rows 4 g4 + j, keys v0 + kt * 16 + r16
@@ -817,8 +836,9 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
             vf[i][h] = *(const f16x8 *)(a.vc + (head_base + slot) * HD + ch * 8);
         }
     }
-    // Q fragments (A operand) of row rt*16 + r16, dims 32s + 8*g4 .. +8, from a clamped row; rows past R are zero
-    f16x8 qa[ST];
+    // Q fragments (A operand) of row rt*16 + r16, dims 32s + 8*g4 .. +8, from a clamped row; rows past R are zero.
+    // fp16 values and their fp16 remainders (split_f16), two MFMAs per score step: Q enters at fp32-class precision
+    f16x8 qa[ST], ql[ST];
     {
         const int row = rt * 16 + r16;
         const int rowc = row < R ? row : R - 1;
@@ -834,7 +854,12 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
 #pragma unroll
         for (int s = 0; s < ST; ++s)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qa[s][e] = (f16)(x[s][e >> 2][e & 3] * qs);
+            for (int e = 0; e < 8; ++e) {
+                f16 hi, lo;
+                split_f16(x[s][e >> 2][e & 3] * qs, hi, lo);
+                qa[s][e] = hi;
+                ql[s][e] = lo;
+            }
     }
     const sp_token ct = a.toks[gr.first_col + min(tid, gr.ncols - 1)];
 
@@ -874,6 +899,7 @@ __global__ void __launch_bounds__(256) k_attn_mq(AttnMqArgs a) {
         for (int s = 0; s < ST; ++s) {
             const f16x8 kb = *(const f16x8 *)&k_s[16 * st + r16][32 * s + 8 * g4];
             acc = mfma16(qa[s], kb, acc);
+            acc = mfma16(ql[s], kb, acc);
         }
         sc[st] = acc;
     }

@@ -103,7 +103,10 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v, float identity) {
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+// v is pinned as a register value first: otherwise a caller's product feeding v can fuse into the first DPP add
+// (fma(x, x, neighbour's rounded x * x)), and the two lanes of a pair then hold different bits.
 __device__ __forceinline__ float row16_sum(float v) {
+    asm volatile("" : "+v"(v));
     v += dpp_mov<0xB1>(v, 0.f);      // quad_perm [1,0,3,2]
     v += dpp_mov<0x4E>(v, 0.f);      // quad_perm [2,3,0,1]
     v += dpp_mov<0x141>(v, 0.f);     // row_half_mirror
@@ -172,3 +175,17 @@ __device__ __forceinline__ float block_sum_dpp(float v, float *red) {
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+// An fp32 activation as the unevaluated sum of two fp16 values: hi = fp16(v), lo = fp16(v - hi).  v - hi is exact in
+// fp32, so hi + lo holds about 22 significant bits where hi alone holds 11.  A GEMV that feeds both halves to the
+// matrix cores (a second MFMA, or MFMA row 1 of a one-column product) sums x * w with fp32-class inputs while the
+// operands stay fp16.  hi and lo must both come from v as rounded to fp32: otherwise the compiler may fold a caller's
+// product into the conversion (v_fma_mix: the exact product rounded once to fp16) or into the subtraction (an FMA),
+// and two kernels forming the same v could disagree in hi or lo.  The empty asm makes v an fp32 register value (it
+// emits no instruction), and contraction is off for the subtraction.
+__device__ __forceinline__ void split_f16(float v, f16 &hi, f16 &lo) {
+#pragma clang fp contract(off)
+    asm volatile("" : "+v"(v));
+    hi = (f16)v;
+    lo = (f16)(v - (float)hi);
+}

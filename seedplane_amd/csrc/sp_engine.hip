@@ -162,29 +162,36 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
     return p;
 }
 
-template <int FMT, int RG, int R>
-void launch_gemv_r(int mt, bool shallow, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+// LO: several columns whose inputs come with fp16 remainders (a.xlo): a second MFMA per fragment.  One column takes
+// its remainders in MFMA row 1 of the ONE variant instead.
+template <int FMT, int RG, int R, bool LO>
+void launch_gemv_r_lo(int mt, bool shallow, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
     if (mt == 1) {
         if constexpr (R == 4) {
             throw Fail{SP_EINVAL, "gemv plan: 4 units per wave need several column tiles"};
         } else {
             if (a.m == 1) hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R, true>), grid, block, smem, st, a);
-            else hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R>), grid, block, smem, st, a);
+            else hipLaunchKernelGGL((k_gemv<FMT, 1, RG, R, false, false, LO>), grid, block, smem, st, a);
         }
         return;
     }
     if constexpr (FMT == 2) {
         if (shallow) {
             require(mt == 3, SP_EINVAL, "gemv plan: shallow batches are built for 3 column tiles");
-            hipLaunchKernelGGL((k_gemv<FMT, 3, RG, R, false, true>), grid, block, smem, st, a);
+            hipLaunchKernelGGL((k_gemv<FMT, 3, RG, R, false, true, LO>), grid, block, smem, st, a);
             return;
         }
     }
     switch (mt) {
-        case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, RG, R>), grid, block, smem, st, a); break;
-        case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, RG, R>), grid, block, smem, st, a); break;
-        default: hipLaunchKernelGGL((k_gemv<FMT, 4, RG, R>), grid, block, smem, st, a); break;
+        case 2: hipLaunchKernelGGL((k_gemv<FMT, 2, RG, R, false, false, LO>), grid, block, smem, st, a); break;
+        case 3: hipLaunchKernelGGL((k_gemv<FMT, 3, RG, R, false, false, LO>), grid, block, smem, st, a); break;
+        default: hipLaunchKernelGGL((k_gemv<FMT, 4, RG, R, false, false, LO>), grid, block, smem, st, a); break;
     }
+}
+template <int FMT, int RG, int R>
+void launch_gemv_r(int mt, bool shallow, dim3 grid, dim3 block, size_t smem, hipStream_t st, const GemvArgs &a) {
+    if (a.xlo && a.m > 1) launch_gemv_r_lo<FMT, RG, R, true>(mt, shallow, grid, block, smem, st, a);
+    else launch_gemv_r_lo<FMT, RG, R, false>(mt, shallow, grid, block, smem, st, a);
 }
 template <int FMT>
 void launch_gemv_fmt(int mt, bool paired, int r, bool shallow, dim3 grid, dim3 block, size_t smem, hipStream_t st,
@@ -259,9 +266,12 @@ bool launch_gemv1_fmt(bool paired, int pro, int T, dim3 grid, dim3 block, size_t
 // split K: the kernel then writes raw slices to part[s][m][ldo] and the return value is the slice count that the
 // consumer must add (plus the bias, for EPI_STORE); otherwise the epilogue is applied and 0 is returned.  With a
 // prologue (pro != PRO_NONE, one column) the activations come from *pa instead of x.
+// `xlo` (optional): the fp16 remainders of x in x's layout; `out_lo` (optional, the SwiGLU pair): where the remainders
+// of the SwiGLU output go.
 int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, float *out_f32, f16 *out_f16, int ldo,
                 const float *bias, hipStream_t st, float *part = nullptr, size_t pstride = 0, int pro = PRO_NONE,
-                const ProArgs *pa = nullptr, int slices = 0, int waves = 0, int xmtp = 0, int omtp = 0) {
+                const ProArgs *pa = nullptr, int slices = 0, int waves = 0, int xmtp = 0, int omtp = 0,
+                const f16 *xlo = nullptr, f16 *out_lo = nullptr) {
     require(mcols >= 1 && mcols <= 16 * GEMV_MAX_MT, SP_EINVAL, "gemv columns out of range");
     require((epi == EPI_SILU) == m.paired, SP_EINVAL, "gemv epilogue does not match the matrix packing");
     require(pro == PRO_NONE || (mcols == 1 && pa), SP_EINVAL, "gemv prologue needs one column and its arguments");
@@ -276,6 +286,8 @@ int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, floa
     a.kslice = p.kslice; a.pstride = pstride; a.nwk = p.nw;
     require(xmtp == 0 || xmtp == mt, SP_EINVAL, "gemv input layout does not match the column count");
     a.xmtp = xmtp; a.omtp = omtp;
+    require(pro == PRO_NONE || xlo == nullptr, SP_EINVAL, "a prologue GEMV builds its own activations");
+    a.xlo = xlo; a.out_lo = m.paired ? out_lo : nullptr;
     if (p.s > 1) { a.epi = EPI_PART; a.out_f32 = part; a.bias = nullptr; }
     // one column of a layer matrix: k_gemv1 (row groups one per block; the prologues need their fixed block sizes)
     if (mcols == 1 && xmtp == 0 && p.units < 2048 && m.rows_pad / 16 / p.rg == p.units) {
@@ -309,7 +321,8 @@ int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, floa
         require(p.r == 1 && p.nw <= pro_threads(pro) / 64, SP_EINVAL, "gemv prologue plan out of range");
         const int kt = m.fmt == 1 ? 32 : (m.fmt == 2 ? 64 : 128);
         const size_t klen = ((size_t)p.kslice * kt + 7) & ~(size_t)7;
-        const size_t smem = (size_t)p.nw * p.rg * 1024 + klen * 2 + (size_t)pro_scratch_floats(pro, pa->H, pa->HD) * 4;
+        // activations and their remainders, then the prologue's scratch
+        const size_t smem = (size_t)p.nw * p.rg * 1024 + klen * 2 * 2 + (size_t)pro_scratch_floats(pro, pa->H, pa->HD) * 4;
         require(smem <= GEMV_MAX_LDS, SP_EINVAL, "gemv prologue LDS out of range");
         switch (m.fmt) {
             case 1: launch_gemv_pro_fmt<1>(m.paired, pro, grid, smem, st, a, *pa); break;
@@ -394,12 +407,12 @@ void by_slices(int np, F &&f) {
     }
 }
 
-// RMSNorm of n columns of x, first adding np pending split-K residual slices
+// RMSNorm of n columns of x, first adding np pending split-K residual slices; the fp16 output and its remainders
 void launch_rmsnorm(int n, float *x, int H, const float *part, int np, size_t ps, const float *w, float eps, f16 *out,
-                    hipStream_t st, int mtp) {
+                    f16 *out_lo, hipStream_t st, int mtp) {
     by_slices(np, [&](auto c) {
         hipLaunchKernelGGL((k_rmsnorm<decltype(c)::value>), dim3(n), dim3(NORM_THREADS), 0, st, x, H, part, ps, w, H, eps,
-                           out, H, mtp);
+                           out, out_lo, H, mtp);
     });
 }
 
@@ -487,6 +500,9 @@ struct sp_engine {
     // still being read
     float *x2 = nullptr, *gpart2 = nullptr;
     f16 *xn = nullptr, *attn = nullptr, *act = nullptr;
+    // the fp16 remainders (split_f16) of the normalised GEMV inputs (qkv always; gate_up in one-column steps) and of
+    // the SwiGLU activation of one-column steps
+    f16 *xn_lo = nullptr, *act_lo = nullptr;
     float *am_v = nullptr;
     int *am_i = nullptr, *am_out = nullptr;
     int argmax_cols = 0;         // columns whose argmax ids am_out holds (the last SP_F_ARGMAX call)
@@ -549,7 +565,7 @@ void sp_engine::free_all() {
     embed.release(); head.release();
     dev_free(final_norm); dev_free(inv_freq);
     for (void *p : {(void *)x, (void *)x2, (void *)qkv, (void *)q, (void *)rtab, (void *)logits, (void *)attn_part, (void *)gpart,
-                    (void *)gpart2, (void *)xn, (void *)attn,
+                    (void *)gpart2, (void *)xn, (void *)attn, (void *)xn_lo, (void *)act_lo,
                     (void *)act, (void *)am_v, (void *)am_i, (void *)am_out,
                     (void *)d_upload, (void *)d_kl, (void *)d_vl, (void *)d_move})
         dev_free(p);
@@ -575,6 +591,8 @@ void sp_engine::alloc_activations() {
     const size_t tpad = (size_t)(maxT + 15) / 16 * 16;       // fragment-major inputs hold whole 16-column tiles
     x = dev_alloc<float>((size_t)maxT * H);
     xn = dev_alloc<f16>(tpad * kmax);
+    xn_lo = dev_alloc<f16>(tpad * kmax);
+    act_lo = dev_alloc<f16>(I);
     qkv = dev_alloc<float>((size_t)maxT * Nqkv);
     gpart_stride = (size_t)maxT * std::max(H, Nqkv);
     gpart = dev_alloc<float>(GEMV_MAX_SLICES * gpart_stride);
@@ -604,6 +622,8 @@ void sp_engine::alloc_activations() {
     HIPCHK(hipEventCreateWithFlags(&upload_done, hipEventDisableTiming));
     d_move = dev_alloc<int>(2 * 64);
     HIPCHK(hipMemset(xn, 0, tpad * kmax * sizeof(f16)));
+    HIPCHK(hipMemset(xn_lo, 0, tpad * kmax * sizeof(f16)));
+    HIPCHK(hipMemset(act_lo, 0, I * sizeof(f16)));
     HIPCHK(hipMemset(attn, 0, tpad * d.n_heads * d.head_dim * sizeof(f16)));
     HIPCHK(hipMemset(act, 0, tpad * I * sizeof(f16)));
 }
@@ -806,7 +826,7 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
     if (l0 > 0) {
         // fused one-column steps alternate x / x2 every layer; the down GEMV of layer l0 - 1 left its slices pending
         res = fuse && (l0 & 1) ? x2 : x;
-        const GemvPlan dp = plan_gemv(layers[0].down, (n + 15) / 16, true, down_s, down_w);
+        const GemvPlan dp = plan_gemv(layers[l0 - 1].down, (n + 15) / 16, true, down_s, down_w);
         pend = dp.s > 1 ? dp.s : 0;
     }
     for (int l = l0; l < l1; ++l) {
@@ -821,9 +841,9 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
             sq = launch_gemv(ly.qkv, EPI_STORE, nullptr, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, qpart, ps, PRO_NORM, &pn,
                              qkv_s, qkv_w);
         } else {
-            launch_rmsnorm(n, res, H, gpart, pend, ps, ly.in_norm, d.rms_eps, xn, st, mtp);
+            launch_rmsnorm(n, res, H, gpart, pend, ps, ly.in_norm, d.rms_eps, xn, xn_lo, st, mtp);
             sq = launch_gemv(ly.qkv, EPI_STORE, xn, H, n, qkv, nullptr, Nqkv, ly.qkv_b, st, qpart, ps, PRO_NONE, nullptr,
-                             qkv_s, qkv_w, mtp);
+                             qkv_s, qkv_w, mtp, 0, xn_lo);
         }
         RopeArgs ra{qkv, Nqkv, NH, NKV, HD, rtab, dtoks, q, kc[l], vc[l], n_slots, qpart, ps, ly.qkv_b};
         const bool fused = ap.rope_fused && logits_on;
@@ -849,16 +869,24 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
             pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_NONE,
                                nullptr, 0, 0, mtp);
         }
-        launch_rmsnorm(n, rmid, H, gpart, pend, ps, ly.post_norm, d.rms_eps, xn, st, mtp);
+        // Remainders where they cost nothing (one column: MFMA row 1) or where the logits need them (the qkv input,
+        // above: its rounding reaches the attention scores).  Several columns would pay a second MFMA and twice the
+        // activation reads per fragment for the gate_up, down and head inputs, whose fp16 rounding moves the logits
+        // far less.
+        f16 *xlo = n == 1 ? xn_lo : nullptr, *alo = n == 1 ? act_lo : nullptr;
+        launch_rmsnorm(n, rmid, H, gpart, pend, ps, ly.post_norm, d.rms_eps, xn, xlo, st, mtp);
         launch_gemv(ly.gate_up, EPI_SILU, xn, H, n, nullptr, act, I, nullptr, st, nullptr, 0, PRO_NONE, nullptr, 0, 0, mtp,
-                    mtp);
+                    mtp, xlo, alo);
         pend = launch_gemv(ly.down, EPI_RESID, act, I, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_NONE, nullptr,
-                           down_s, down_w, mtp);
+                           down_s, down_w, mtp, 0, alo);
         res = rmid;
     }
     if (logits_on && l1 == d.n_layers) {
         const DevMat &hm = d.tied_head ? embed : head;
-        launch_rmsnorm(n, res, H, gpart, pend, ps, final_norm, d.rms_eps, xn, st, mtp);
+        // the head takes its input in fp16 alone: its rounding moves the logits by about 2.5e-4 max-rel at the
+        // 1.5B int8 workload (against 6.7e-2 for the qkv input), and its remainders would double the head's
+        // activation reads
+        launch_rmsnorm(n, res, H, gpart, pend, ps, final_norm, d.rms_eps, xn, nullptr, st, mtp);
         launch_gemv(hm, EPI_STORE, xn, H, n, logits, nullptr, d.vocab, nullptr, st, nullptr, 0, PRO_NONE, nullptr, 0, 0, mtp);
         if (flags & SP_F_ARGMAX) {
             hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, n), dim3(256), 0, st, logits, d.vocab, d.vocab, am_v, am_i);
@@ -1279,7 +1307,7 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
             case SP_T_QKV: m = &e->layers[cur].qkv;
                 launch = [&] { launch_gemv(e->layers[cur].qkv, EPI_STORE, e->xn, H, n_cols, e->qkv, nullptr, e->Nqkv,
                                            e->layers[cur].qkv_b, st, e->gpart, e->gpart_stride, PRO_NONE, nullptr, 0, 0,
-                                           tm); next_layer(); };
+                                           tm, 0, e->xn_lo); next_layer(); };
                 break;
             case SP_T_O: m = &e->layers[cur].o;
                 launch = [&] { launch_gemv(e->layers[cur].o, EPI_RESID, e->attn, NHD, n_cols, e->x, nullptr, H, nullptr,
@@ -1287,11 +1315,14 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
                 break;
             case SP_T_GATE_UP: m = &e->layers[cur].gate_up;
                 launch = [&] { launch_gemv(e->layers[cur].gate_up, EPI_SILU, e->xn, H, n_cols, nullptr, e->act, I,
-                                           nullptr, st, nullptr, 0, PRO_NONE, nullptr, 0, 0, tm, tm); next_layer(); };
+                                           nullptr, st, nullptr, 0, PRO_NONE, nullptr, 0, 0, tm, tm,
+                                           n_cols == 1 ? e->xn_lo : nullptr, n_cols == 1 ? e->act_lo : nullptr);
+                               next_layer(); };
                 break;
             case SP_T_DOWN: m = &e->layers[cur].down;
                 launch = [&] { launch_gemv(e->layers[cur].down, EPI_RESID, e->act, I, n_cols, e->x, nullptr, H, nullptr,
-                                           st, e->gpart, e->gpart_stride, PRO_NONE, nullptr, 0, 0, tm); next_layer(); };
+                                           st, e->gpart, e->gpart_stride, PRO_NONE, nullptr, 0, 0, tm, 0,
+                                           n_cols == 1 ? e->act_lo : nullptr); next_layer(); };
                 break;
             case SP_T_HEAD: case SP_T_EMBED: m = d.tied_head || kind == SP_T_EMBED ? &e->embed : &e->head;
                 launch = [&] { launch_gemv(*m, EPI_STORE, e->xn, H, n_cols, e->logits, nullptr, d.vocab, nullptr, st,

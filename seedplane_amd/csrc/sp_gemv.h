@@ -47,6 +47,8 @@ struct GemvArgs {
     int nwk;               // prologue kernels: waves that take k-tiles (the others only help with the prologue)
     int xmtp;              // x layout: 0 row-major [m][ldx], else fragment-major with xmtp column tiles (act_off)
     int omtp;              // EPI_SILU output layout, the same way
+    const f16 *xlo;        // optional: the fp16 remainders of x (split_f16), same layout; NULL = x is exact in fp16
+    f16 *out_lo;           // optional EPI_SILU output: the fp16 remainders of the SwiGLU values
 };
 template <int FMT>
 __device__ __forceinline__ f16x8 unpack_step(const u32x4 &t, int s) {
@@ -105,8 +107,12 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int unit, int m
     }
     if constexpr (RG == 2) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (live[j]) a.out_f16[act_off(mrow[j], n, a.ldo, a.omtp)] = (f16)(silu_f(v0[j]) * v1[j]);
+        for (int j = 0; j < 4; ++j) {
+            f16 hi, lo;
+            split_f16(silu_f(v0[j]) * v1[j], hi, lo);
+            if (live[j]) a.out_f16[act_off(mrow[j], n, a.ldo, a.omtp)] = hi;
+            if (live[j] && a.out_lo) a.out_lo[act_off(mrow[j], n, a.ldo, a.omtp)] = lo;
+        }
     } else if (a.epi == EPI_STORE) {
         const float bn = a.bias ? a.bias[n] : 0.f;
 #pragma unroll
@@ -140,7 +146,7 @@ __host__ __device__ constexpr int pro_threads(int pro) { return pro == PRO_NORM 
 constexpr int PRO_NORM_HMAX = 2048;         // hidden sizes the norm prologue takes (PRO_NORM_HMAX / 512 per thread)
 constexpr int PRO_MAX_SLICES = 8;           // pending residual slices
 struct ProArgs {
-    // PRO_NORM: v = res + part[0] + ... + part[np - 1] (slice order); act = fp16((v * rs) * w) with
+    // PRO_NORM: v = res + part[0] + ... + part[np - 1] (slice order); act, act_lo = split_f16((v * rs) * w) with
     // rs = 1 / sqrt(mean(v^2) + eps) (k_rmsnorm); block (0, 0) writes v to res_out, a buffer the blocks do not read
     const float *res;
     float *res_out;
@@ -182,8 +188,8 @@ __device__ __forceinline__ void pro_norm_load(const ProArgs &p, int klo, NormOps
         for (int q = 0; q < PRO_NORM_QMAX; ++q) o.pv[s][q] = p.part[so + min(tid + PRO_THREADS * q, H - 1)];
     }
 }
-__device__ __forceinline__ void pro_norm_finish(const ProArgs &p, const NormOps &o, f16 *act, int klo, int klen,
-                                                float *scr) {
+__device__ __forceinline__ void pro_norm_finish(const ProArgs &p, const NormOps &o, f16 *act, f16 *act_lo, int klo,
+                                                int klen, float *scr) {
     constexpr int PRO_THREADS = pro_threads(PRO_NORM), PRO_QMAX = PRO_NORM_QMAX;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, H = p.H;
     float *v_s = scr, *red = scr + H;
@@ -210,11 +216,14 @@ __device__ __forceinline__ void pro_norm_finish(const ProArgs &p, const NormOps 
     for (int j = 0; j < NORM_THREADS / PRO_THREADS; ++j) {
         const int vt = tid + PRO_THREADS * j;
         float ss = 0.f;
+        {
+#pragma clang fp contract(off)      // k_rmsnorm's rounding order: each square rounded, added in element order
 #pragma unroll
-        for (int i = 0; i < NORM_PER_THREAD; ++i) {
-            const int k = vt + NORM_THREADS * i;
-            const float v = k < H ? v_s[k] : 0.f;
-            ss += v * v;
+            for (int i = 0; i < NORM_PER_THREAD; ++i) {
+                const int k = vt + NORM_THREADS * i;
+                const float v = k < H ? v_s[k] : 0.f;
+                ss += v * v;
+            }
         }
         ss = wave_sum_dpp(ss);
         if (lane == 0) red[wv + (PRO_THREADS / 64) * j] = ss;
@@ -226,14 +235,19 @@ __device__ __forceinline__ void pro_norm_finish(const ProArgs &p, const NormOps 
 #pragma unroll
     for (int q = 0; q < PRO_QMAX; ++q) {
         const int e = tid + PRO_THREADS * q;
-        if (e < klen) act[e] = (f16)((v_s[klo + e] * rs) * wk[q]);
+        if (e < klen) {
+            f16 hi, lo;
+            split_f16((v_s[klo + e] * rs) * wk[q], hi, lo);
+            act[e] = hi;
+            act_lo[e] = lo;
+        }
     }
     __syncthreads();
 }
-__device__ __forceinline__ void pro_norm(const ProArgs &p, f16 *act, int klo, int klen, float *scr) {
+__device__ __forceinline__ void pro_norm(const ProArgs &p, f16 *act, f16 *act_lo, int klo, int klen, float *scr) {
     NormOps o;
     pro_norm_load(p, klo, o);
-    pro_norm_finish(p, o, act, klo, klen, scr);
+    pro_norm_finish(p, o, act, act_lo, klo, klen, scr);
 }
 
 // Heads overlapping the k-range, pro_threads(PRO_COMB) / HD at a time: thread group g of HD threads plays
@@ -297,9 +311,11 @@ __device__ __forceinline__ void pro_comb(const ProArgs &p, f16 *act, int klo, in
 
 // MT == 1 (up to 16 columns) with Q8 / Q4 codes: the MFMA takes the codes offset by QBias (no per-weight subtraction)
 // and each quant block's result is corrected by QBias (+ the Q4 zero) times the block's activation sums, one fp32 FMA
-// per output; ONE (a single column) keeps only output component 0 (the other rows of the MFMA A operand are zero).
+// per output; ONE (a single column) keeps only output components 0 and 1: row 0 of the MFMA A operand is the column,
+// row 1 its fp16 remainders (a.xlo, or the norm prologue's; a zero line without them), rows 2..15 zero, so the
+// remainders cost no extra MFMA.  LO (several columns): a second MFMA per fragment takes the remainders a.xlo.
 // Every column gets the same operations in either case, so one column and a batch give the same bits.
-template <int FMT, int MT, int RG, int R, int PRO, bool ONE = false, bool SHALLOW = false>
+template <int FMT, int MT, int RG, int R, int PRO, bool ONE = false, bool SHALLOW = false, bool LO = false>
 __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, unsigned char *smem_raw) {
     constexpr int KT = TileGeom<FMT>::KT, ST = TileGeom<FMT>::STEPS;
     constexpr int TB = PRO == PRO_NONE ? GemvBatch<FMT, MT, RG, SHALLOW>::TB : GemvBatch<FMT, MT, 1>::TB;
@@ -329,14 +345,16 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
         wbase[i] = a.w + grp * a.nkt * TILE_BYTES;
         sbase[i] = a.sz + grp * a.nkt * (FMT == 2 ? 32 : 128);
     }
-    const f16 *xrow[MT];
+    size_t xrow[MT];          // row-major offset of the lane's column (column 0 for lanes past m)
     bool xon[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         const int m = mt * 16 + r;
         xon[mt] = m < a.m;
-        xrow[mt] = a.x + (size_t)(xon[mt] ? m : 0) * a.ldx + 8 * g;
+        xrow[mt] = (size_t)(xon[mt] ? m : 0) * a.ldx + 8 * g;
     }
+    // ONE: the lanes of MFMA row 1 hold column 0's remainders (row-major input)
+    const bool lrow = ONE && r == 1 && a.xlo != nullptr && a.xmtp == 0;
     // LDS: [cross-wave reduction: NW x NR x MT x 1 KiB][prologue: activations of the k-range, scratch]
     f32x4 *red = (f32x4 *)smem_raw;
     f16 *act = (f16 *)(smem_raw + (size_t)NW * NR * MT * 1024);
@@ -358,10 +376,11 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
             }
         }
     };
+    f16 *act_lo = act + ((klen + 7) & ~7);      // the norm prologue's remainders
     if constexpr (PRO != PRO_NONE) {
         if (worker && k0 + wv < k1) load_weights(k0 + wv);
-        float *scr = (float *)(act + ((klen + 7) & ~7));
-        if constexpr (PRO == PRO_NORM) pro_norm(p, act, k0 * KT, klen, scr);
+        float *scr = (float *)(act_lo + ((klen + 7) & ~7));
+        if constexpr (PRO == PRO_NORM) pro_norm(p, act, act_lo, k0 * KT, klen, scr);
         else pro_comb(p, act, k0 * KT, klen, scr);
     }
 
@@ -370,6 +389,7 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
         // ---- issue the weight and activation loads of TB k-tiles before anything is consumed
         if (PRO == PRO_NONE || kb != k0 + wv) load_weights(kb);
         f16x8 xa[TB][MT][ST];
+        f16x8 xal[LO ? TB : 1][MT][ST];
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
             const int kt = kb + t * NW;
@@ -384,11 +404,16 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                         // fragment (fragment-major, xmtp == MT) or row slice (row-major).  One unconditional load
                         // from a selected address: no branch and no select on the value, so the loads of a batch
                         // stay in flight together.
-                        const f16 *xf = a.x + ((size_t)(kt * ST + s) * MT + mt) * 512 + lane * 8;
-                        const f16 *xr = xrow[mt] + kt * KT + s * 32;
-                        xa[t][mt][s] = *(const f16x8 *)(xon[mt] ? (a.xmtp ? xf : xr) : g_zero_line);
-                    } else
-                        xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(act + (kt - k0) * KT + s * 32 + 8 * g) : zero8;
+                        const size_t off = a.xmtp ? ((size_t)(kt * ST + s) * MT + mt) * 512 + lane * 8
+                                                  : xrow[mt] + kt * KT + s * 32;
+                        const f16 *src = xon[mt] ? a.x + off : (mt == 0 && lrow ? a.xlo + off : g_zero_line);
+                        xa[t][mt][s] = *(const f16x8 *)src;
+                        if constexpr (LO) xal[t][mt][s] = *(const f16x8 *)(xon[mt] ? a.xlo + off : g_zero_line);
+                    } else {
+                        const int e = (kt - k0) * KT + s * 32 + 8 * g;
+                        xa[t][mt][s] = xon[mt] ? *(const f16x8 *)(act + e)
+                                               : (PRO == PRO_NORM && mt == 0 && r == 1 ? *(const f16x8 *)(act_lo + e) : zero8);
+                    }
                 }
         }
         // ---- MFMA per quant block
@@ -401,7 +426,10 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                 f32x4 xs[MT];
                 if constexpr (FMT == 3 || (FMT == 2 && MT == 1)) {
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) xs[mt] = mfma16(xa[t][mt][s], ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                    for (int mt = 0; mt < MT; ++mt) {
+                        xs[mt] = mfma16(xa[t][mt][s], ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        if constexpr (LO) xs[mt] = mfma16(xal[t][mt][s], ones8, xs[mt]);
+                    }
                 }
                 if constexpr (FMT != 1 && MT == 1) {
                     // biased codes: acc_j += scale * (mfma(x, code + bias)_j - (bias + zero) * sum(x)_j)
@@ -410,8 +438,11 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                     // follows
                     f32x4 ddv[NR];
 #pragma unroll
-                    for (int i = 0; i < NR; ++i)
-                        ddv[i] = mfma16(xa[t][0][s], biased_step<FMT>(wt[t][i], s), (f32x4){0.f, 0.f, 0.f, 0.f});
+                    for (int i = 0; i < NR; ++i) {
+                        const f16x8 bq = biased_step<FMT>(wt[t][i], s);
+                        ddv[i] = mfma16(xa[t][0][s], bq, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        if constexpr (LO) ddv[i] = mfma16(xal[t][0][s], bq, ddv[i]);
+                    }
 #pragma unroll
                     for (int i = 0; i < NR; ++i) {
                         const f32x4 dd = ddv[i];
@@ -426,8 +457,12 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                             scale = (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
                             off = QBias<FMT>::V + (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
                         }
+                        if constexpr (ONE) {     // column 0 = row 0 (fp16 part) + row 1 (remainders)
+                            acc[i][0][0] = fmaf(scale, fmaf(-off, xs[0][0], dd[0]) + fmaf(-off, xs[0][1], dd[1]), acc[i][0][0]);
+                        } else {
 #pragma unroll
-                        for (int j = 0; j < NJ; ++j) acc[i][0][j] = fmaf(scale, fmaf(-off, xs[0][j], dd[j]), acc[i][0][j]);
+                            for (int j = 0; j < NJ; ++j) acc[i][0][j] = fmaf(scale, fmaf(-off, xs[0][j], dd[j]), acc[i][0][j]);
+                        }
                     }
                     continue;
                 }
@@ -436,13 +471,19 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                     const f16x8 b = unpack_step<FMT>(wt[t][i], s);
                     if constexpr (FMT == 1) {
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) acc[i][mt] = mfma16(xa[t][mt][s], b, acc[i][mt]);
+                        for (int mt = 0; mt < MT; ++mt) {
+                            acc[i][mt] = mfma16(xa[t][mt][s], b, acc[i][mt]);
+                            if constexpr (LO) acc[i][mt] = mfma16(xal[t][mt][s], b, acc[i][mt]);
+                        }
                     } else if constexpr (FMT == 2) {
                         const uint32_t d = sq8[t][i];
                         const float scale = (float)__builtin_bit_cast(f16, (uint16_t)(s == 0 ? (d & 0xffffu) : (d >> 16)));
                         f32x4 dd[MT];                  // every column tile's product first, then the scaling
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        for (int mt = 0; mt < MT; ++mt) {
+                            dd[mt] = mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+                            if constexpr (LO) dd[mt] = mfma16(xal[t][mt][s], b, dd[mt]);
+                        }
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt) acc[i][mt] += scale * dd[mt];
                     } else {
@@ -452,7 +493,10 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
                         const float zero = (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
                         f32x4 dd[MT];
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        for (int mt = 0; mt < MT; ++mt) {
+                            dd[mt] = mfma16(xa[t][mt][s], b, (f32x4){0.f, 0.f, 0.f, 0.f});
+                            if constexpr (LO) dd[mt] = mfma16(xal[t][mt][s], b, dd[mt]);
+                        }
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt) acc[i][mt] += scale * (dd[mt] - zero * xs[mt]);
                     }
@@ -462,6 +506,11 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
     }
     }
 
+    // ONE with fp16 weights: rows 0 and 1 accumulated the column's two parts separately
+    if constexpr (ONE && FMT == 1) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) acc[i][0][0] += acc[i][0][1];
+    }
     // ---- one wave: finish in registers; several: reduce through LDS in wave order, wave w finishing the (unit,
     // column tile) outputs w, w + NW, ...   Lane holds D[m = mt*16 + 4g + j][n = unit*16 + r].
     if (NW == 1) {
@@ -494,10 +543,10 @@ __device__ __forceinline__ void gemv_run(const GemvArgs &a, const ProArgs &p, un
     }
 }
 
-template <int FMT, int MT, int RG, int R, bool ONE = false, bool SHALLOW = false>
+template <int FMT, int MT, int RG, int R, bool ONE = false, bool SHALLOW = false, bool LO = false>
 __global__ void __launch_bounds__((GemvLimits<MT, RG, R>::MAX_THREADS)) k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    gemv_run<FMT, MT, RG, R, PRO_NONE, ONE, SHALLOW>(a, ProArgs{}, smem_raw);
+    gemv_run<FMT, MT, RG, R, PRO_NONE, ONE, SHALLOW, LO>(a, ProArgs{}, smem_raw);
 }
 
 // One column with an activation prologue (PRO_NORM before qkv / gate_up, PRO_COMB before o_proj).

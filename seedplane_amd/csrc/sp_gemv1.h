@@ -9,12 +9,13 @@
 //     re-read the slice's last tile and contribute zero), so the code is straight-line and each tile is consumed as
 //     soon as its own loads land (progressive vmcnt waits) instead of after a whole batch;
 //   * the activation column lives in LDS (staged once per block, or built there by the RMSNorm / attention-combine
-//     prologue), not in registers: an MFMA A operand is read just before use, lanes of rows 1..15 reading a zero
-//     line, so a wave holds only its weight tiles and the block's waves all fit on the CU at once;
+//     prologue), not in registers: an MFMA A operand is read just before use, so a wave holds only its weight
+//     tiles and the block's waves all fit on the CU at once;
 //   * Q8 / Q4 codes enter the MFMA offset by a constant (1152 / 1024: one perm or mask per pair, no subtraction) and
 //     each quant block's result is corrected by (offset + zero) * sum(x) in fp32, one FMA per output row;
-//   * only output component 0 is live (the A operand's rows 1..15 are zero), so the per-block scale work is one FMA
-//     per row group and quant block.
+//   * the A operand's row 0 is the column in fp16 and row 1 its fp16 remainders (split_f16: the norm prologue's, or
+//     a.xlo), rows 2..15 zero, so output components 0 + 1 are the product with fp32-class activations at no extra
+//     MFMA; the per-block scale work is one FMA per row group and quant block.
 // Work decomposition: one block per (16-row unit, k-slice); unit = 16 rows, or 16 gate + 16 up rows for the SwiGLU
 // pair (RG = 2); wave w of NW takes k-tiles w, w + NW, ... of the slice (T per wave); waves are reduced through LDS
 // in wave order (deterministic).  Epilogues: store (+bias), residual add, SwiGLU to fp16, or a raw k-slice partial
@@ -22,11 +23,12 @@
 #pragma once
 #include "sp_gemv.h"
 
-// Offset of x (fp16) in the block's LDS: the slice's activations, then 16 bytes of zeros read by the lanes whose MFMA
-// rows are not the column's.
+// The block's LDS: the slice's activations (fp16) and 16 bytes of zeros read by the lanes of MFMA rows 2..15
+// (g1_x_halves halves), then the same span for their remainders (MFMA row 1), the cross-wave reduction, the prologue's
+// scratch.
 __host__ __device__ inline size_t g1_x_halves(int kslice, int KT) { return ((size_t)kslice * KT + 7) / 8 * 8 + 8; }
 __host__ __device__ inline size_t g1_smem_bytes(int kslice, int KT, int nw, int rg, int pro_floats) {
-    return g1_x_halves(kslice, KT) * 2 + (size_t)nw * rg * 16 * 4 + (size_t)pro_floats * 4;
+    return g1_x_halves(kslice, KT) * 2 * 2 + (size_t)nw * rg * 16 * 4 + (size_t)pro_floats * 4;
 }
 
 template <int FMT, int RG, int T, int PRO>
@@ -41,18 +43,22 @@ __global__ void __launch_bounds__(1024) k_gemv1(GemvArgs a, ProArgs p) {
     const int klen = max(k1 - k0, 0) * KT;
     f16 *xs_lds = (f16 *)smem_raw;
     const size_t xh = g1_x_halves(a.kslice, KT);
-    float *red = (float *)(smem_raw + xh * 2);
+    f16 *xl_lds = xs_lds + xh;                      // remainders
+    float *red = (float *)(smem_raw + xh * 2 * 2);
     float *scr = red + NW * RG * 16;
+    const bool has_lo = PRO == PRO_NORM || (PRO == PRO_NONE && a.xlo != nullptr);
 
     // ---- 0. the activation side's own global loads first: loads complete in issue order, so the activation work
     // below then waits only for them and runs while the weight tiles are still streaming in
     const int nx = klen / 8;                         // 16-byte pieces of the slice's activations
-    uint4 xpre;
+    uint4 xpre, xpre_lo;
     NormOps npre;
     if constexpr (PRO == PRO_NONE) {
         // from a clamped base and index (an empty last slice reads the final piece and stores nothing)
-        const uint4 *src = (const uint4 *)(a.x + (size_t)min(k0, a.nkt - 1) * KT);
-        xpre = src[min((int)threadIdx.x, max(nx - 1, 0))];
+        const size_t base = (size_t)min(k0, a.nkt - 1) * KT;
+        const int pc = min((int)threadIdx.x, max(nx - 1, 0));
+        xpre = ((const uint4 *)(a.x + base))[pc];
+        xpre_lo = has_lo ? ((const uint4 *)(a.xlo + base))[pc] : ((const uint4 *)g_zero_line)[0];
     } else if constexpr (PRO == PRO_NORM) {
         pro_norm_load(p, k0 * KT, npre);
     }
@@ -87,20 +93,25 @@ __global__ void __launch_bounds__(1024) k_gemv1(GemvArgs a, ProArgs p) {
     // ---- 2. the activation column of the slice in LDS (+ the zero line)
     if constexpr (PRO == PRO_NONE) {
         const uint4 *src = (const uint4 *)(a.x + (size_t)k0 * KT);
-        uint4 *dst = (uint4 *)xs_lds;
-        // unconditional store (threads past the slice write the first piece of the reduction area, which is only
-        // written again after the barrier below), so the load above is not moved behind the weight loads
-        dst[(int)threadIdx.x < nx ? (int)threadIdx.x : (int)(xh / 8)] = xpre;
+        uint4 *dst = (uint4 *)xs_lds, *dstl = (uint4 *)xl_lds;
+        // unconditional stores (threads past the slice write the first pieces of the reduction area, which is only
+        // written again after the barrier below), so the loads above are not moved behind the weight loads
+        dst[(int)threadIdx.x < nx ? (int)threadIdx.x : (int)(xh / 4)] = xpre;          // red[0..3]
+        dstl[(int)threadIdx.x < nx ? (int)threadIdx.x : (int)(xh / 8) + 1] = xpre_lo;  // red[4..7]
         for (int i = threadIdx.x + blockDim.x; i < nx; i += blockDim.x) dst[i] = src[i];
+        if (has_lo) {
+            const uint4 *srcl = (const uint4 *)(a.xlo + (size_t)k0 * KT);
+            for (int i = threadIdx.x + blockDim.x; i < nx; i += blockDim.x) dstl[i] = srcl[i];
+        }
     } else if constexpr (PRO == PRO_NORM) {
-        pro_norm_finish(p, npre, xs_lds, k0 * KT, klen, scr);
+        pro_norm_finish(p, npre, xs_lds, xl_lds, k0 * KT, klen, scr);
     } else {
         pro_comb(p, xs_lds, k0 * KT, klen, scr);
     }
     if (threadIdx.x < 8) xs_lds[xh - 8 + threadIdx.x] = (f16)0.f;
     __syncthreads();
 
-    // ---- 3. MFMA per tile and quant block; lanes of rows 1..15 read the zero line
+    // ---- 3. MFMA per tile and quant block; lanes of row 1 read the remainders, rows 2..15 the zero line
     const f16x8 ones8 = (f16x8){1, 1, 1, 1, 1, 1, 1, 1};
     float acc[RG];
     f32x4 acc4[RG];
@@ -111,13 +122,14 @@ __global__ void __launch_bounds__(1024) k_gemv1(GemvArgs a, ProArgs p) {
         const int kt = k0 + wv + NW * t;
 #pragma unroll
         for (int s = 0; s < ST; ++s) {
-            const int off = (r == 0 && valid[t]) ? (kt - k0) * KT + s * 32 + 8 * g : (int)xh - 8;
+            const int xo = (kt - k0) * KT + s * 32 + 8 * g;
+            const int off = !valid[t] ? (int)xh - 8 : r == 0 ? xo : (r == 1 && has_lo ? (int)xh + xo : (int)xh - 8);
             const f16x8 xa = *(const f16x8 *)(xs_lds + off);
             if constexpr (FMT == 1) {
 #pragma unroll
                 for (int i = 0; i < RG; ++i) acc4[i] = mfma16(xa, __builtin_bit_cast(f16x8, wt[t][i]), acc4[i]);
             } else {
-                const float sx = mfma16(xa, ones8, (f32x4){0.f, 0.f, 0.f, 0.f})[0];
+                const f32x4 sx = mfma16(xa, ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                 for (int i = 0; i < RG; ++i) {
                     const f32x4 dd = mfma16(xa, biased_step<FMT>(wt[t][i], s), (f32x4){0.f, 0.f, 0.f, 0.f});
@@ -132,7 +144,7 @@ __global__ void __launch_bounds__(1024) k_gemv1(GemvArgs a, ProArgs p) {
                         scale = (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
                         offs = QBias<FMT>::V + (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
                     }
-                    acc[i] = fmaf(scale, fmaf(-offs, sx, dd[0]), acc[i]);
+                    acc[i] = fmaf(scale, fmaf(-offs, sx[0], dd[0]) + fmaf(-offs, sx[1], dd[1]), acc[i]);
                 }
             }
         }
@@ -141,7 +153,7 @@ __global__ void __launch_bounds__(1024) k_gemv1(GemvArgs a, ProArgs p) {
     // ---- 4. waves reduced in wave order; lanes 0..15 of wave 0 finish row unit * 16 + r
     if (g == 0) {
 #pragma unroll
-        for (int i = 0; i < RG; ++i) red[(wv * RG + i) * 16 + r] = FMT == 1 ? acc4[i][0] : acc[i];
+        for (int i = 0; i < RG; ++i) red[(wv * RG + i) * 16 + r] = FMT == 1 ? acc4[i][0] + acc4[i][1] : acc[i];
     }
     __syncthreads();
     if (threadIdx.x >= 16) return;
@@ -155,7 +167,10 @@ __global__ void __launch_bounds__(1024) k_gemv1(GemvArgs a, ProArgs p) {
         v[i] = t;
     }
     if constexpr (RG == 2) {
-        a.out_f16[n] = (f16)(silu_f(v[0]) * v[1]);
+        f16 hi, lo;
+        split_f16(silu_f(v[0]) * v[1], hi, lo);
+        a.out_f16[n] = hi;
+        if (a.out_lo) a.out_lo[n] = lo;
     } else if (a.epi == EPI_STORE) {
         a.out_f32[n] = v[0] + (a.bias ? a.bias[n] : 0.f);
     } else if (a.epi == EPI_RESID) {

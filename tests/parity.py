@@ -29,14 +29,14 @@ def check_greedy(tokens, ref_rows, tol=TOL, what=''):
 
 
 def check_rows(gpu_rows, ref_rows, tol=TOL, what=''):
-    """Row-wise max-rel of GPU logits vs oracle logits; returns the worst row's value."""
-    worst = 0.0
+    """Row-wise max-rel of GPU logits vs oracle logits (every row printed, then checked); returns the worst row's
+    value."""
     assert gpu_rows.shape == ref_rows.shape, (gpu_rows.shape, ref_rows.shape)
-    for i in range(ref_rows.shape[0]):
-        e = max_rel(gpu_rows[i], ref_rows[i])
+    errs = [max_rel(gpu_rows[i], ref_rows[i]) for i in range(ref_rows.shape[0])]
+    print(f'{what} max-rel per row: ' + ' '.join(f'{e:.2e}' for e in errs), flush=True)
+    for i, e in enumerate(errs):
         assert e < tol, f'{what} row {i}: max-rel {e:.3e}'
-        worst = max(worst, e)
-    return worst
+    return max(errs)
 
 
 def clone_cache(ref, rc, capacity):

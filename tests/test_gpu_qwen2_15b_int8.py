@@ -1,5 +1,6 @@
 """Oracle parity of the HIP engine at the full Qwen2-1.5B shape (28 layers, hidden 1536, 12 / 2 heads, head_dim 128,
-GQA group 6, SwiGLU 8960, tied 151936-row head) with int8 block-32 weights (codes U[-127, 127], fp16 block scales):
+GQA group 6, SwiGLU 8960, tied 151936-row head) with int8 block-32 weights at the benchmark's own recipe (codes
+U[-127, 127], fp16 block scales |N(0, 0.002)|):
   * batch 1 over a 1024-position sliding window, the context past the window and past the 1088-slot ring: decode logits
     of every step and the greedy ids vs the oracle (reference qwen_engine.py:105-166; window rule of transformers'
     sliding window);
@@ -7,10 +8,11 @@ GQA group 6, SwiGLU 8960, tied 151936-row head) with int8 block-32 weights (code
   * the 1 + 8 x 4 draft tree over a 2048-position prefix with a Qwen2-0.5B fp16 drafter: tree-masked logits vs the
     oracle's forward_masked with the ancestor mask, greedy ids per node, then the acceptance walk on those logits vs
     the oracle walk (bit-exact, every decision outside rounding of its threshold).
-These run with block scales |N(0, 0.0005)|.  With the benchmark's |N(0, 0.002)| the model is so sensitive to rounding
-that fp16 storage alone moves its logits by more than the fp16 bar: the reference's own fp16 path (qwen_engine.py:39-41,
-dtype float16) lies about 0.1 max-rel from its fp32 path.  For that recipe the test below requires the HIP engine to be
-no further from the fp32 oracle than the reference's fp16 path is.
+The workload keeps its K/V cache in fp16, and at this recipe that rounding alone moves the fp32 oracle's logits by
+about 3.7e-2 max-rel (more than the fp16 bar).  So the oracle here is the fp32 restatement with exactly that rounding
+(storage={'kv'}): the K/V cache in fp16, everything else fp32.  The engine carries every other activation the GEMVs
+read as an fp16 value plus its fp16 remainder, so it must meet the 2e-2 bar against that oracle at bs1, bs16 and on
+the tree; the bs1 test also reports (and bounds) its distance to the all-fp32 oracle.
 The sequences share a 1024-token prefix that the oracle runs once; its cache is cloned per sequence."""
 import numpy as np
 import pytest
@@ -30,14 +32,15 @@ pytestmark = pytest.mark.gpu
 W = 1024            # sliding window
 PREFIX = 1024       # shared prompt prefix
 MARGIN = 1e-12
+KV = {'kv'}         # the oracle's only fp16 storage point: the workload's fp16 K/V cache
 
 
 @pytest.fixture(scope='module')
 def m15(gpu_device):
     print('qwen2-1.5b int8: weights, engine, oracle prefix', flush=True)
-    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0, scale_std=0.0005)
+    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
     eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
-    ref = RefQwen2(cfg, w)
+    ref = RefQwen2(cfg, w, storage=KV)
     del w
     prefix = random_prompt(PREFIX, cfg['vocab_size'], seed=1)
     rc = ref.new_cache(PREFIX)
@@ -59,14 +62,26 @@ def test_bs1_windowed_decode_past_the_wrap(m15):
     for s in range(1, steps):
         toks.append(int(eng.decode([toks[-1]], [cache], logits_out=rows[s:s + 1])[0]))
     assert list(eng.generate(prompt, steps, window=W)) == toks      # device-side feed: same ids
-    print('1.5b bs1: oracle', flush=True)
+    print('1.5b bs1: oracle (fp16 K/V)', flush=True)
     oc = clone_cache(ref, rc, len(prompt) + steps)
     ref_rows = torch.cat([ref.forward(suffix, oc, window=W)[-1:],
                           ref.forward(toks[:-1], oc, all_logits=True, window=W)])
-    worst = check_rows(rows.cpu(), ref_rows, what='bs1')
+    gpu = rows.cpu()
+    worst = check_rows(gpu, ref_rows, what='bs1')
     same = check_greedy(toks, ref_rows, what='bs1')
-    print(f'1.5b bs1: worst max-rel {worst:.2e}, {same}/{steps} ids equal the oracle argmax', flush=True)
+    print(f'1.5b bs1: worst max-rel {worst:.2e} vs the oracle with a fp16 K/V cache, {same}/{steps} ids equal its argmax',
+          flush=True)
     assert same >= 0.75 * steps          # the margin rule allows close races; most steps are not close
+    # the all-fp32 oracle: the engine is no further from it than the fp16 cache alone puts the oracle, plus the bar
+    print('1.5b bs1: oracle (all fp32)', flush=True)
+    f32 = RefQwen2(cfg, make_weights(preset('qwen2-1.5b'), 'q8', seed=0)[1])
+    seq = prompt + toks[:-1]
+    f32_rows = f32.forward(seq, f32.new_cache(len(seq)), all_logits=True, window=W)[len(prompt) - 1:]
+    del f32
+    e_gpu = max(max_rel(gpu[i], f32_rows[i]) for i in range(steps))
+    e_kv = max(max_rel(ref_rows[i], f32_rows[i]) for i in range(steps))
+    print(f'1.5b bs1: HIP vs all-fp32 oracle {e_gpu:.3e}; fp16-K/V oracle vs all-fp32 oracle {e_kv:.3e}', flush=True)
+    assert e_gpu <= e_kv + TOL
 
 
 def test_bs16_windowed_decode_each_sequence_vs_oracle(m15):
@@ -130,6 +145,7 @@ def test_tree_verify_8x4_over_2048_prefix_vs_oracle(m15, drafter):
     worst = check_rows(p.cpu(), ref_rows, what='tree')
     same = check_greedy([int(t) for t in ids], ref_rows, what='tree')
     print(f'1.5b tree: worst max-rel {worst:.2e}, {same}/{tree.size} node ids equal the oracle argmax', flush=True)
+    assert same >= 0.75 * tree.size
     q = q_rows_for_tree(tree, drows, V, eng.device)
     got = verifier.accept(p, q, tree, u[used:], 0.8)
     t = dict(token=tree.token, trial_start=tree.trial_start, n_trials=tree.n_trials, trials=tree.trials)
@@ -137,35 +153,3 @@ def test_tree_verify_8x4_over_2048_prefix_vs_oracle(m15, drafter):
                                                        tree.max_depth)
     assert margin > MARGIN
     assert (got[0], got[1], got[2], got[3]) == (path, final, n_u, bonus)
-
-
-def test_benchmark_recipe_no_further_from_fp32_than_reference_fp16(gpu_device):
-    """Scales |N(0, 0.002)|: the HIP engine's logits lie no further from the fp32 oracle than the reference's own fp16
-    execution does (per decode step, worst row), and its greedy ids follow the fp32 oracle wherever the top-2 margin
-    exceeds that distance."""
-    print('1.5b benchmark recipe: weights, engine', flush=True)
-    cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
-    V, steps = cfg['vocab_size'], 16
-    eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
-    prompt = random_prompt(1100, V, seed=2)
-    cache = eng.new_cache(4096, window=W)
-    lg, cache = eng.forward(prompt, cache)
-    rows = torch.empty((steps, V), dtype=torch.float32, device=eng.device)
-    rows[0].copy_(lg[0])
-    toks = [int(lg[0].argmax())]
-    for s in range(1, steps):
-        toks.append(int(eng.decode([toks[-1]], [cache], logits_out=rows[s:s + 1])[0]))
-    gpu = rows.cpu()
-    del eng, cache
-    seq = prompt + toks[:-1]
-    out = {}
-    for mode in (None, 'fp16'):
-        print(f'1.5b benchmark recipe: oracle storage={mode}', flush=True)
-        ref = RefQwen2(cfg, w, storage=mode)
-        out[mode] = ref.forward(seq, ref.new_cache(len(seq)), all_logits=True, window=W)[len(prompt) - 1:]
-        del ref
-    e_gpu = max(max_rel(gpu[i], out[None][i]) for i in range(steps))
-    e_f16 = max(max_rel(out['fp16'][i], out[None][i]) for i in range(steps))
-    print(f'1.5b benchmark recipe: HIP vs fp32 {e_gpu:.3e}; reference fp16 path vs fp32 {e_f16:.3e}', flush=True)
-    assert e_gpu <= max(TOL, e_f16)
-    check_greedy(toks, out[None], tol=max(TOL, e_f16), what='benchmark recipe')

@@ -191,6 +191,30 @@ def test_storage_modes_round_where_they_say(tiny_f32):
             assert torch.equal(t, t.half().float()), mode
     with pytest.raises(ValueError):
         RefQwen2(cfg, w, storage='bf16')
+    with pytest.raises(ValueError):
+        RefQwen2(cfg, w, storage={'kv', 'logits'})
+
+
+def test_storage_points_compose(tiny_f32):
+    # a set of storage points rounds exactly there: {'kv'} keeps fp16 values in the cache and differs from fp32;
+    # 'x' is the union of its three consumers ('xq', 'xg', 'xh'); 'hip' is the union of every point
+    cfg, w = tiny_f32
+    ids = [1, 2, 3, 4, 5, 6, 7, 49, 0]
+
+    def run(storage):
+        ref = RefQwen2(cfg, w, storage=storage)
+        c = ref.new_cache(16)
+        return ref.forward(ids, c, all_logits=True), c
+
+    base, c0 = run(None)
+    kv, c1 = run({'kv'})
+    assert not torch.equal(kv, base)
+    for t in c1.keys + c1.values:
+        assert torch.equal(t, t.half().float())
+    assert any(not torch.equal(t, t.half().float()) for t in c0.keys)
+    assert torch.equal(run({'x'})[0], run({'xq', 'xg', 'xh'})[0])
+    assert not torch.equal(run({'xq'})[0], run({'x'})[0])
+    assert torch.equal(run('hip')[0], run({'x', 'kv', 'attn', 'act'})[0])
 
 
 def test_fp16_storage_matches_transformers_in_fp16(tiny_f32):
