@@ -1655,8 +1655,10 @@ static void accept_tree_run(const float *p_logits_dev, const float *q_logits_dev
         struct AccScratch { unsigned long long *xbuf; unsigned *err; int32_t *host; };
         static std::map<int, AccScratch> scratch_of;
         static unsigned launches = 0;
+        static std::mutex mu;        // the map and the tag counter are shared by every host thread
         int dev = 0;
         HIPCHK(hipGetDevice(&dev));
+        std::unique_lock<std::mutex> lock(mu);
         auto it = scratch_of.find(dev);
         if (it == scratch_of.end()) {
             unsigned long long *xb = dev_alloc<unsigned long long>(4 * ACC_NB * ACC_XW);
@@ -1668,9 +1670,10 @@ static void accept_tree_run(const float *p_logits_dev, const float *q_logits_dev
             std::memset(host, 0, (ACC_HOST_OUT + 64 + 4) * sizeof(int32_t));
             it = scratch_of.emplace(dev, AccScratch{xb, err, host}).first;
         }
-        const AccScratch &sc = it->second;
+        const AccScratch sc = it->second;
         launches = launches % 0xFFFFFu + 1;
         const unsigned tag = launches << 12;
+        lock.unlock();
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token, trial_start, n_trials, trials, u,
                      n_u, 1.0 / temperature, sc.xbuf, sc.err, tag, n_nodes, n_trials_total, out_dev, max_depth, sc.host};
         volatile int32_t *hb = sc.host;
@@ -1729,9 +1732,15 @@ int sp_op_accept_tree_host(const float *p_logits_dev, const float *q_logits_dev,
         // and an event after the last walk that read it (waited on before the block is refilled)
         struct Stage { unsigned char *buf; size_t cap; hipEvent_t done; bool used; };
         static std::map<int, Stage> stage_of;
+        static std::mutex mu;        // guards the map; calls that overlap on one device race as documented
         int dev = 0;
         HIPCHK(hipGetDevice(&dev));
-        Stage &sg = stage_of[dev];
+        Stage *sgp;
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            sgp = &stage_of[dev];    // std::map references stay valid across inserts
+        }
+        Stage &sg = *sgp;
         const size_t ints = (size_t)3 * n_nodes + std::max(n_trials_total, 1);
         const size_t need = (size_t)n_u * sizeof(double) + ints * sizeof(int32_t);
         if (!sg.done) HIPCHK(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
