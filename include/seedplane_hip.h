@@ -62,13 +62,14 @@ enum {
     SP_F_LOGITS = 1,      /* run the final norm + LM head and produce fp32 logits for every column   */
     SP_F_ARGMAX = 2,      /* also produce the greedy id per column (first index on ties)             */
     SP_F_GRAPH = 4,       /* record the step as graphs once; replayed when the caller waits per step */
-    SP_F_PERSISTENT = 8,  /* accepted for compatibility; the step runs as the kernel chain (a whole-   */
-                          /* step persistent kernel was slower than the chain and has been removed)  */
+    SP_F_PERSISTENT = 8,  /* accepted for compatibility: one plain decode column runs the persistent  */
+                          /* step by default wherever sp_engine_persistent_status says it applies    */
     SP_F_UNFUSED = 16,    /* one column: run every RMSNorm and attention combine as a kernel of its   */
                           /* own instead of inside the next GEMV (same results; for checking)        */
-    SP_F_FEED = 32        /* column b's token is the argmax id of column b of the last SP_F_ARGMAX   */
+    SP_F_FEED = 32,       /* column b's token is the argmax id of column b of the last SP_F_ARGMAX   */
                           /* call (on the device; the token field is ignored), so a greedy loop     */
                           /* needs no host round trip per step                                       */
+    SP_F_CHAIN = 64       /* run the kernel chain even where the persistent one-column step applies  */
 };
 
 typedef struct sp_model_desc {
@@ -139,8 +140,24 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
                       int32_t *argmax_host);
 
 /* Introspection (no counterpart in the reference): which implementation ran the last sp_engine_forward call:
- * 0 = the kernel chain (the only one), -1 = none yet. */
+ * 0 = the kernel chain, 1 = the persistent one-column step (one kernel launch for every layer, then the head
+ * GEMV and the argmax), -1 = none yet. */
 int sp_engine_last_path(const sp_engine *e);
+
+/* Introspection (no counterpart in the reference; the reference records its whole one-token step once and submits
+ * it once per token, native/vulkan_decode/qwen_vk.cpp:372-412): 1 when a plain decode column (one column, no tree
+ * block, writing the slot of its newest visible position) runs the persistent step on this engine's weights and KV
+ * pool, 0 when it runs the kernel chain -- `why` (why_len bytes, may be NULL) then receives the reason -- and -1 on
+ * an error.  Prepares the step's buffers on the first call after a weight load or pool change. */
+int sp_engine_persistent_status(sp_engine *e, char *why, int32_t why_len);
+
+/* Host function, no GPU call (no counterpart in the reference): the persistent step's work split for a model shape
+ * on n_blocks blocks (one per CU) and n_slots KV slots, after the bounds walk that precedes every launch (every
+ * item's block, tagged words, weight tiles and staged counts).  info receives 12 values: qkv tiles, attention chunks,
+ * combiners, o_proj tiles, gate_up units, down items, gate_up units of the busiest block, first attention block,
+ * first o_proj block, first down block, tagged words, LDS bytes per block.  SP_EINVAL (with sp_last_error) when the
+ * step does not apply. */
+int sp_persistent_geometry(const sp_model_desc *desc, int32_t n_slots, int32_t n_blocks, int32_t *info);
 
 /* Introspection (no counterpart in the reference; its decode report counts dispatches per token,
  * native/vulkan_decode/qwen_vk.cpp:866-870): kernels launched by the last sp_engine_forward call with SP_F_GRAPH

@@ -16,7 +16,7 @@ SP_OK, SP_EINVAL, SP_ENOMEM, SP_EHIP, SP_ESTATE, SP_ECAPACITY = range(6)
 SP_FMT_F32, SP_FMT_F16, SP_FMT_Q8, SP_FMT_Q4 = range(4)
 (SP_T_EMBED, SP_T_HEAD, SP_T_FINAL_NORM, SP_T_IN_NORM, SP_T_POST_NORM, SP_T_QKV, SP_T_QKV_BIAS, SP_T_O,
  SP_T_GATE_UP, SP_T_DOWN) = range(10)
-SP_F_LOGITS, SP_F_ARGMAX, SP_F_GRAPH, SP_F_PERSISTENT, SP_F_UNFUSED, SP_F_FEED = 1, 2, 4, 8, 16, 32
+SP_F_LOGITS, SP_F_ARGMAX, SP_F_GRAPH, SP_F_PERSISTENT, SP_F_UNFUSED, SP_F_FEED, SP_F_CHAIN = 1, 2, 4, 8, 16, 32, 64
 
 # Every function the header declares, with its ctypes signature.
 c_int, c_int32, c_size_t, c_uint64, c_float = ctypes.c_int, ctypes.c_int32, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float
@@ -57,6 +57,8 @@ SIGNATURES = {
     'sp_engine_sync': (c_int, [c_void_p]),
     'sp_engine_copy_ids': (c_int, [c_void_p, c_int32, c_void_p]),
     'sp_engine_last_path': (c_int, [c_void_p]),
+    'sp_engine_persistent_status': (c_int, [c_void_p, c_char_p, c_int32]),
+    'sp_persistent_geometry': (c_int, [ctypes.POINTER(ModelDesc), c_int32, c_int32, ctypes.POINTER(c_int32)]),
     'sp_engine_last_dispatches': (c_int, [c_void_p]),
     'sp_engine_time_attention': (c_int, [c_void_p, c_int32, ctypes.POINTER(Token), c_int32, ctypes.POINTER(c_float),
                                          ctypes.POINTER(c_uint64)]),

@@ -21,6 +21,7 @@
 
 #include "../../include/seedplane_hip.h"
 #include "sp_attn.h"
+#include "sp_decode1.h"
 #include "sp_gemv.h"
 #include "sp_gemv1.h"
 #include "sp_pack.h"
@@ -469,6 +470,28 @@ void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x,
                        inv_freq, half, rtab);
 }
 
+// Instantiations of the persistent one-column step: (format, head_dim, k-tiles per wave for K = hidden, k-tiles per
+// wave of a down item).  Shapes without one run the chain.
+struct D1Kernel {
+    int fmt, hd, th, t5;
+    const void *fn;
+};
+const D1Kernel D1_KERNELS[] = {
+    {2, 128, 3, 9, (const void *)d1::k_decode1<2, 128, 3, 9>},     // Qwen2-1.5B int8
+    {3, 128, 2, 5, (const void *)d1::k_decode1<3, 128, 2, 5>},     // Qwen2-1.5B int4
+    {1, 64, 4, 10, (const void *)d1::k_decode1<1, 64, 4, 10>},     // Qwen2-0.5B fp16
+    {2, 64, 2, 5, (const void *)d1::k_decode1<2, 64, 2, 5>},       // Qwen2-0.5B int8
+    {1, 64, 1, 1, (const void *)d1::k_decode1<1, 64, 1, 1>},       // small test shapes
+    {2, 64, 1, 1, (const void *)d1::k_decode1<2, 64, 1, 1>},
+    {3, 64, 1, 1, (const void *)d1::k_decode1<3, 64, 1, 1>},
+};
+const D1Kernel *find_d1_kernel(const d1::Geom &g) {
+    const int th = std::max(d1::cdiv(g.nkt_h, d1::NW), d1::cdiv(g.nkt_a, d1::NW)), t5 = d1::cdiv(g.nk5, d1::NW);
+    for (const D1Kernel &k : D1_KERNELS)
+        if (k.fmt == g.fmt && k.hd == g.HD && k.th == th && k.t5 == t5) return &k;
+    return nullptr;
+}
+
 }  // namespace
 
 // ============================================================================================== engine
@@ -533,6 +556,21 @@ struct sp_engine {
 
     int last_path = -1;
 
+    // persistent one-column step (sp_decode1.h): geometry for the current pool, tagged words, the error word
+    int d1_state = 0;            // 0: to be prepared, 1: ready, -1: does not apply (d1_why says why)
+    std::string d1_why;
+    d1::Geom d1g{};
+    const D1Kernel *d1k = nullptr;
+    unsigned long long *d1_ll = nullptr;
+    unsigned *d1_err = nullptr, *h_d1err = nullptr;
+    d1::LayerPtr *d1_layers = nullptr;
+    d1::Static *d1_static = nullptr;
+    unsigned d1_seq = 0;
+    bool d1_plain = false;       // the runtime refused a cooperative launch once: plain launches from then on
+    bool prepare_d1();
+    bool run_d1(const sp_token &t, int flags);
+    void check_d1_error();
+
     // attention plan of one forward call: same-sequence column groups (multi-query kernel) or one block row per column
     struct AttnPlan {
         bool mq = false;
@@ -557,6 +595,9 @@ struct sp_engine {
 
 void sp_engine::free_all() {
     drop_graphs();
+    dev_free(d1_ll); dev_free(d1_err); dev_free(d1_layers); dev_free(d1_static);
+    if (h_d1err) (void)hipHostFree(h_d1err);
+    d1_ll = nullptr; d1_err = nullptr; d1_layers = nullptr; d1_static = nullptr; h_d1err = nullptr; d1_state = 0;
     for (auto &l : layers) {
         l.qkv.release(); l.o.release(); l.gate_up.release(); l.down.release();
         dev_free(l.qkv_b); dev_free(l.in_norm); dev_free(l.post_norm);
@@ -896,6 +937,109 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
     HIPCHK(hipGetLastError());
 }
 
+// The persistent step for the current weights and KV pool: geometry, bounds walk, instantiation, co-residency, the
+// tagged-word area and the per-layer pointer table.  Returns false (d1_why set) when the step does not apply.
+bool sp_engine::prepare_d1() {
+    if (d1_state != 0) return d1_state > 0;
+    d1_state = -1;
+    int nb = 0;
+    HIPCHK(hipDeviceGetAttribute(&nb, hipDeviceAttributeMultiprocessorCount, device));
+    const char *why = "";
+    if (n_slots < 1 || !d1::make_geom(d, n_slots, nb, d1g, &why)) { d1_why = why; return false; }
+    d1k = find_d1_kernel(d1g);
+    if (!d1k) { d1_why = "no instantiation for this shape"; return false; }
+    if (!d1::check_geom(d1g, d1k->th, d1k->t5, &why)) { d1_why = why; return false; }
+    for (auto &l : layers)
+        if (l.qkv.fmt != d.weight_format || l.o.fmt != d.weight_format || l.gate_up.fmt != d.weight_format ||
+            l.down.fmt != d.weight_format) { d1_why = "mixed weight formats"; return false; }
+    if (embed.fmt != d.weight_format) { d1_why = "mixed weight formats"; return false; }
+    int per_cu = 0;
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, d1k->fn, d1::NT, sizeof(d1::Smem)));
+    if (per_cu < 1) { d1_why = "the block does not fit a CU"; return false; }
+    dev_free(d1_ll); dev_free(d1_layers); dev_free(d1_static);
+    d1_ll = nullptr; d1_layers = nullptr; d1_static = nullptr;
+    d1_ll = dev_alloc<unsigned long long>(d1g.words);
+    HIPCHK(hipMemset(d1_ll, 0, d1g.words * sizeof(unsigned long long)));     // tag 0 is never current
+    if (!d1_err) {
+        d1_err = dev_alloc<unsigned>(1);
+        HIPCHK(hipMemset(d1_err, 0, sizeof(unsigned)));
+        HIPCHK(hipHostMalloc((void **)&h_d1err, sizeof(unsigned), hipHostMallocDefault));
+        *h_d1err = 0;
+    }
+    std::vector<d1::LayerPtr> lp(d.n_layers);
+    for (int l = 0; l < d.n_layers; ++l) {
+        const Layer &ly = layers[l];
+        const DevMat *m[4] = {&ly.qkv, &ly.o, &ly.gate_up, &ly.down};
+        for (int i = 0; i < 4; ++i) { lp[l].w[i] = m[i]->w; lp[l].sz[i] = m[i]->sz; }
+        lp[l].qkv_b = ly.qkv_b; lp[l].n_in = ly.in_norm; lp[l].n_post = ly.post_norm;
+        lp[l].kc = kc[l]; lp[l].vc = vc[l];
+    }
+    d1_layers = dev_alloc<d1::LayerPtr>(d.n_layers);
+    HIPCHK(hipMemcpy(d1_layers, lp.data(), lp.size() * sizeof(d1::LayerPtr), hipMemcpyHostToDevice));
+    d1::Static sa{};
+    sa.g = d1g;
+    sa.layers = d1_layers;
+    sa.emb_w = embed.w; sa.emb_sz = embed.sz;
+    sa.final_norm = final_norm; sa.inv_freq = inv_freq;
+    sa.eps = d.rms_eps; sa.scale = 1.0f / std::sqrt((float)d.head_dim);
+    sa.ll = d1_ll;
+    sa.err = d1_err;
+    sa.xn = xn;
+    d1_static = dev_alloc<d1::Static>(1);
+    HIPCHK(hipMemcpy(d1_static, &sa, sizeof(sa), hipMemcpyHostToDevice));
+    d1_state = 1;
+    d1_why.clear();
+    return true;
+}
+
+// One column through the persistent kernel, then the LM head GEMV and the argmax as in the chain.
+// The kernel needs its blocks co-resident (one per CU; the LDS size allows no second one, checked in prepare_d1) but
+// no grid barrier.  It is launched cooperatively; where the runtime refuses that (a second process on the device can
+// find the cooperative-launch resources taken), as a plain launch of the same grid, which an otherwise idle device
+// also places one block per CU.  Either way every wait in the kernel is bounded: a grid that is not all resident
+// ends with the error word set, never a hang.  Returns false, with nothing enqueued, if both launches fail (the step
+// is then marked as not applying and the caller runs the chain).
+bool sp_engine::run_d1(const sp_token &t, int flags) {
+    d1::Step a{};
+    a.tok = t;
+    a.feed = (flags & SP_F_FEED) ? am_out : nullptr;
+    d1_seq = (d1_seq + 1) & 0xFFFFFFu;
+    if (d1_seq == 0) d1_seq = 1;
+    a.seq = d1_seq;
+    const d1::Static *sp = d1_static;
+    void *args[] = {(void *)&sp, &a};
+    hipError_t le = d1_plain ? hipErrorNotSupported
+                             : hipLaunchCooperativeKernel(d1k->fn, dim3(d1g.nb), dim3(d1::NT), args, sizeof(d1::Smem), stream);
+    if (le != hipSuccess) {
+        (void)hipGetLastError();
+        d1_plain = true;
+        le = hipLaunchKernel(d1k->fn, dim3(d1g.nb), dim3(d1::NT), args, sizeof(d1::Smem), stream);
+    }
+    if (le != hipSuccess) {
+        (void)hipGetLastError();
+        d1_state = -1;
+        d1_why = std::string("launch refused: ") + hipGetErrorString(le);
+        return false;
+    }
+    HIPCHK(hipMemcpyAsync(h_d1err, d1_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream));
+    const DevMat &hm = d.tied_head ? embed : head;
+    launch_gemv(hm, EPI_STORE, xn, d.hidden, 1, logits, nullptr, d.vocab, nullptr, stream);
+    if (flags & SP_F_ARGMAX) {
+        hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, 1), dim3(256), 0, stream, logits, d.vocab, d.vocab, am_v, am_i);
+        hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(64), 0, stream, am_v, am_i, am_out);
+    }
+    HIPCHK(hipGetLastError());
+    return true;
+}
+
+// After a synchronisation: a persistent step whose block gave up (a hand-off that never arrived) is reported once.
+void sp_engine::check_d1_error() {
+    if (!h_d1err || *(volatile unsigned *)h_d1err == 0) return;
+    *(volatile unsigned *)h_d1err = 0;
+    (void)hipMemsetAsync(d1_err, 0, sizeof(unsigned), stream);
+    throw Fail{SP_EHIP, "persistent decode step: a block hand-off timed out (the step's results are invalid)"};
+}
+
 // ============================================================================================== C ABI
 namespace {
 int fail_engine(sp_engine *e, const Fail &f) {
@@ -1011,6 +1155,7 @@ int sp_engine_load(sp_engine *e, int32_t kind, int32_t layer, int32_t fmt, int32
             default: throw Fail{SP_EINVAL, "unknown tensor kind"};
         }
         e->drop_graphs();
+        e->d1_state = 0;
     });
 }
 
@@ -1056,6 +1201,7 @@ void install_pool(sp_engine *e, int n_seq, int n_slots, std::vector<f16 *> &k, s
     e->attn_part = dev_alloc<float>((size_t)e->maxT * e->d.n_heads * e->max_nchunk * part_floats(e->d.head_dim));
     e->n_seq = n_seq; e->n_slots = n_slots;
     e->drop_graphs();
+    e->d1_state = 0;
 }
 }  // namespace
 
@@ -1147,9 +1293,27 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         require(!feed || n <= e->argmax_cols, SP_ESTATE,
                 "SP_F_FEED needs a previous SP_F_ARGMAX call over at least as many columns");
         e->check_columns(n, toks, feed);
+        e->check_d1_error();
         const bool use_graph = flags & SP_F_GRAPH;
         const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX | SP_F_UNFUSED | SP_F_FEED);
-        e->last_path = 0;                  // SP_F_PERSISTENT is accepted; every step runs as the kernel chain
+        // one plain decode column: the persistent step, where the shape and the pool allow it
+        const sp_token &t0 = toks[0];
+        if (n == 1 && (flags & SP_F_LOGITS) && !(flags & (SP_F_UNFUSED | SP_F_CHAIN)) && t0.tree_count == 0 &&
+            t0.ctx_hi >= t0.ctx_lo && t0.slot == t0.ctx_hi % e->n_slots && e->prepare_d1() && e->run_d1(t0, sflags)) {
+            e->last_path = 1;
+            e->last_dispatches = (sflags & SP_F_ARGMAX) ? 4 : 2;
+            if (sflags & SP_F_ARGMAX) e->argmax_cols = 1;
+            if (logits_dev)
+                HIPCHK(hipMemcpyAsync(logits_dev, e->logits, (size_t)d.vocab * sizeof(float), hipMemcpyDeviceToDevice, e->stream));
+            if (argmax_host) {
+                HIPCHK(hipMemcpyAsync(e->h_ids, e->am_out, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
+                HIPCHK(hipStreamSynchronize(e->stream));
+                e->check_d1_error();
+                std::memcpy(argmax_host, e->h_ids, sizeof(int32_t));
+            }
+            return;
+        }
+        e->last_path = 0;
         const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
         e->upload(n, toks, ap);
         if (use_graph) {
@@ -1282,7 +1446,36 @@ int sp_engine_copy_ids(sp_engine *e, int32_t n, int32_t *host) {
 
 int sp_engine_sync(sp_engine *e) {
     if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
-    return guarded(e, [&] { HIPCHK(hipStreamSynchronize(e->stream)); });
+    return guarded(e, [&] {
+        HIPCHK(hipStreamSynchronize(e->stream));
+        e->check_d1_error();
+    });
+}
+
+int sp_persistent_geometry(const sp_model_desc *desc, int32_t n_slots, int32_t n_blocks, int32_t *info) {
+    if (!desc || !info) { g_err = "NULL argument"; return SP_EINVAL; }
+    d1::Geom g;
+    const char *why = "";
+    if (!d1::make_geom(*desc, n_slots, n_blocks, g, &why)) { g_err = why; return SP_EINVAL; }
+    const D1Kernel *k = find_d1_kernel(g);
+    if (!k) { g_err = "no instantiation for this shape"; return SP_EINVAL; }
+    if (!d1::check_geom(g, k->th, k->t5, &why)) { g_err = why; return SP_EINVAL; }
+    const int32_t v[12] = {g.NQ, g.NKV * g.CM, g.NH, g.NO, g.NU, g.ND, g.nu_max, g.B2, g.B3, g.B5,
+                           (int32_t)g.words, (int32_t)sizeof(d1::Smem)};
+    std::memcpy(info, v, sizeof(v));
+    return SP_OK;
+}
+
+int sp_engine_persistent_status(sp_engine *e, char *why, int32_t why_len) {
+    if (!e) { g_err = "engine is NULL"; return -1; }
+    int ok = 0;
+    int rc = guarded(e, [&] { ok = e->n_seq > 0 && e->prepare_d1() ? 1 : 0; });
+    if (rc != SP_OK) return -1;
+    if (why && why_len > 0) {
+        std::strncpy(why, e->d1_why.c_str(), (size_t)why_len - 1);
+        why[why_len - 1] = 0;
+    }
+    return ok;
 }
 
 int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_cols, int32_t iters, float *avg_us,

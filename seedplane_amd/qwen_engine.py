@@ -357,8 +357,18 @@ class Qwen2Engine:
 
     @property
     def last_path(self):
-        """0 once an engine call ran (every step is the kernel chain), -1 before the first."""
+        """Which implementation ran the last engine call: 0 the kernel chain, 1 the persistent one-column step, -1
+        none yet."""
         return int(self.lib.sp_engine_last_path(self.h))
+
+    def persistent_status(self):
+        """(True, '') when a plain one-column decode step on this engine's weights and KV pool runs the persistent
+        kernel, else (False, the reason); the pool must be reserved."""
+        buf = ctypes.create_string_buffer(256)
+        rc = int(self.lib.sp_engine_persistent_status(self.h, buf, 256))
+        if rc < 0:
+            _lib.check(_lib.SP_EHIP, self.h)
+        return rc == 1, buf.value.decode()
 
     def logits_view(self, n):
         """The engine's own fp32 logits of the first n columns of the last SP_F_LOGITS call, as a [n, vocab] CUDA tensor
@@ -381,7 +391,8 @@ class Qwen2Engine:
     @torch.inference_mode()
     def decode(self, tokens, caches, logits_out=None, graph=True):
         """One batched decode step: token i appended to caches[i] (all distinct sequences).  Returns greedy ids.
-        The step runs as the kernel chain, captured as a graph when `graph`."""
+        One sequence runs the persistent one-column step where it applies (persistent_status()); otherwise the step
+        runs as the kernel chain, captured as a graph when `graph`."""
         if len(tokens) != len(caches) or not tokens:
             raise ValueError('one token per cache')
         cols = []

@@ -24,8 +24,9 @@ def _step(eng, cache, tok, flags, buf):
 
 
 def _compare(eng, cache, tokens, graph):
-    """Each token through the unfused step, then (cache rolled back: the step rewrites the same slot) the fused one."""
-    base = _lib.SP_F_GRAPH if graph else 0
+    """Each token through the unfused step, then (cache rolled back: the step rewrites the same slot) the fused one,
+    both as the kernel chain (a plain one-column step would otherwise take the persistent kernel)."""
+    base = (_lib.SP_F_GRAPH if graph else 0) | _lib.SP_F_CHAIN
     ba = torch.empty((1, eng.vocab), dtype=torch.float32, device=eng.device)
     bb = torch.empty_like(ba)
     for i, t in enumerate(tokens):
