@@ -67,6 +67,10 @@ constexpr int MAX_CM = 64;              // attention chunks per kv head (one lan
 // Tag of (launch sequence, layer, phase): unique per launch and per (layer, phase) within it.
 enum { PH_QKV = 1, PH_PART = 2, PH_ATT = 3, PH_XM = 4, PH_ACT = 5, PH_DP = 6 };
 __host__ __device__ inline unsigned tag_of(unsigned seq, int l, int p) { return (seq << 8) | (unsigned)(l * 8 + p); }
+// 16-bit tag of the packed activation words of (launch, layer): never 0 (the words' initial state) and different for
+// consecutive launches.  Every activation word is rewritten in every layer of every launch, so a word that carries
+// the current tag was written in this layer of this launch.
+__host__ __device__ inline unsigned tag16_of(unsigned seq, int l) { return (((seq % 2047u) + 1u) << 5) | (unsigned)l; }
 
 struct LayerPtr {
     const uint8_t *w[4];        // packed qkv, o, gate_up, down
@@ -121,13 +125,15 @@ __host__ __device__ inline int blk_p2b(const Geom &g, int qh) { return g.B2b + q
 __host__ __device__ inline int blk_p3(const Geom &g, int i) { return g.B3 + i; }
 __host__ __device__ inline int blk_p4(const Geom &g, int u) { return u < MAXU * g.B3 ? u % g.B3 : g.B3 + (u - MAXU * g.B3); }
 // Units of block b: b + i * B3 (i < MAXU) below B3; above, the one overflow unit MAXU * B3 + (b - B3).
-__host__ __device__ inline int p4_units(const Geom &g, int b, int *u) {
+__host__ __device__ inline int p4_unit(const Geom &g, int b, int i) {
+    return b < g.B3 ? b + i * g.B3 : MAXU * g.B3 + (b - g.B3);
+}
+__host__ __device__ inline int p4_count(const Geom &g, int b) {
     int n = 0;
     if (b < g.B3) {
-        for (int i = 0; i < MAXU; ++i)
-            if (b + i * g.B3 < g.NU) u[n++] = b + i * g.B3;
-    } else if (MAXU * g.B3 + (b - g.B3) < g.NU) {
-        u[n++] = MAXU * g.B3 + (b - g.B3);
+        for (int i = 0; i < MAXU; ++i) n += b + i * g.B3 < g.NU;
+    } else {
+        n = MAXU * g.B3 + (b - g.B3) < g.NU;
     }
     return n;
 }
@@ -140,6 +146,7 @@ __host__ __device__ inline size_t w_part(const Geom &g, int qh, int c, int j) {
 }
 __host__ __device__ inline size_t w_att(const Geom &g, int i) { return g.o_att + i; }
 __host__ __device__ inline size_t w_xm(const Geom &g, int i) { return g.o_xm + i; }
+// Activation words hold two values each: word i = activations 2i, 2i + 1.
 __host__ __device__ inline size_t w_act(const Geom &g, int i) { return g.o_act + i; }
 __host__ __device__ inline size_t w_dp(const Geom &g, int s, int i) { return g.o_dp + (size_t)s * g.H + i; }
 
@@ -256,9 +263,90 @@ __device__ bool gather(unsigned *err, const Range (&rg)[NR]) {
     return !bad;
 }
 
-// LDS of one block (phases reuse it; more than 80 KiB keeps one block per CU).
+// One range of tagged words whose payloads stay in the registers of the threads that poll them: the tag is the word's
+// bits from `shift` up (32: one fp32 payload; 48: two 24-bit payloads).
+struct RRange {
+    const u64 *src;
+    int n;
+    unsigned tag;
+    int shift = 32;
+};
+// The block waits for every word of NR ranges, as gather does, but thread tid keeps word tid + NT * j of range r in
+// out[r][j] (the tag alone where that word is past the range): no LDS copy and no barrier before the caller uses its
+// values.  Returns false (after writing the error word) when the words stay stale for POLL_LIMIT rounds.
+template <int NPT, int NR>
+__device__ bool gather_w(unsigned *err, const RRange (&rg)[NR], u64 (&out)[NR][NPT], int tid) {
+    // While the producers are still at work, each thread polls one word only (its last element of range 0) and
+    // issues its other loads once that word is current: an early block does not stream its whole input through the
+    // memory system once per round trip.  (Every word's own tag is still checked below.)
+    bool ok = true;
+    {
+        int js = -1;
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) js = tid + NT * j < rg[0].n ? j : js;
+        if (js >= 0) {
+            const u64 *p = rg[0].src + tid + NT * js;
+            long spins = 0;
+            while ((unsigned)(ld_word(p) >> rg[0].shift) != rg[0].tag) {
+                if (++spins > POLL_LIMIT) { ok = false; break; }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    u64 w[NR][NPT];
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+            const int k = tid + NT * j;
+            w[r][j] = k < rg[r].n ? ld_word(rg[r].src + k) : ((u64)rg[r].tag << rg[r].shift);
+        }
+    long spins = 0;
+    while (ok) {
+        bool all = true;
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+            for (int j = 0; j < NPT; ++j) all = all && (unsigned)(w[r][j] >> rg[r].shift) == rg[r].tag;
+        if (all) break;
+        if (++spins > POLL_LIMIT) { ok = false; break; }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+            for (int j = 0; j < NPT; ++j)
+                if ((unsigned)(w[r][j] >> rg[r].shift) != rg[r].tag) w[r][j] = ld_word(rg[r].src + tid + NT * j);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) out[r][j] = w[r][j];
+    const int bad = __syncthreads_or(!ok);
+    if (bad && threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return !bad;
+}
+// gather_w with fp32 payloads: out[r][j] = element tid + NT * j of range r (0 past the range).
+template <int NPT, int NR>
+__device__ bool gather_r(unsigned *err, const RRange (&rg)[NR], float (&out)[NR][NPT], int tid) {
+    u64 w[NR][NPT];
+    const bool ok = gather_w<NPT, NR>(err, rg, w, tid);
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) out[r][j] = __uint_as_float((unsigned)w[r][j]);
+    return ok;
+}
+
+// fp32 -> the 24 high bits of its encoding, rounded to nearest even (sign, exponent, 15 fraction bits; finite values
+// of the activations' range stay finite), and back (exact).
+__device__ __forceinline__ uint32_t f24_of(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u + 0x7Fu + ((u >> 8) & 1u)) >> 8;
+}
+__device__ __forceinline__ float f32_of24(uint32_t b) { return __uint_as_float(b << 8); }
+
+// LDS of one block (phases reuse it).
 struct Smem {
-    float xf[MAX_H];                          // the residual row (P1 / P4) or the attention output (P3, fp32)
     float red[NW * MAXU * 2 * 16];            // per-wave row sums
     float wsum[32];                           // block reductions
     __align__(16) f16 xh[MAX_K + 8];          // GEMV input (fp16) + a zero line
@@ -271,10 +359,12 @@ struct Smem {
     float cs[MAX_HD];                         // cos, then sin, of the RoPE phases
     float knew[MAX_HD], vnew[MAX_HD];
     float cw[MAX_CM];                         // the combine's chunk weights
-    float stage[MAX_K + 16];                  // gathered words (residual parts, qkv rows, chunk records, activations)
-    float xr[2][16];                          // the residual parts of an o_proj tile's rows / a down tile's XM rows
+    float stage[MAX_K + 16];                  // gathered words (the attention's qkv rows, the combine's chunk records)
 };
-static_assert(MAX_K >= 2 * MAX_H, "the staging area holds both residual parts");
+// Dynamic LDS of a launch: at least 84 KiB, so that no CU (160 KiB of LDS) can hold two blocks and the grid of one
+// block per CU is spread over every CU.
+constexpr size_t SMEM_BYTES = sizeof(Smem) > 84 * 1024 ? sizeof(Smem) : 84 * 1024;
+static_assert(SMEM_BYTES <= 160 * 1024, "one block's LDS fits a CU");
 
 // Block-wide sum of one value per thread, in a fixed order (DPP per wave, then the wave sums in wave order).
 __device__ __forceinline__ float block_sum_fixed(float v, float *wsum) {
@@ -298,27 +388,29 @@ struct NormW {
         for (int j = 0; j < NPT; ++j) w[j] = wp[min(tid + NT * j, n - 1)];
     }
 };
-// x (fp32, LDS, n elements) -> RMSNorm with the preloaded weights -> fp16 pairs in s.xh / s.xl; sum of squares with
-// each square rounded and the elements of a thread added in index order.
-__device__ __forceinline__ void norm_to_pairs(Smem &s, const float *x, int n, const NormW &nw, float eps, int tid) {
+// The RMSNorm scale of a GEMV input is one scalar, so W (x rs w) = rs (W (x w)): the GEMV takes x w (x[j] = element
+// tid + NT * j in registers, n elements) as fp16 pairs and the scale is applied to its sums.  prenorm_pairs writes
+// the pairs and each wave's sum of squares of x (each square rounded, the thread's elements in index order, DPP within
+// the wave) and ends with a block barrier; norm_scale then adds the wave sums in wave order: rs = 1 / sqrt(ss / n +
+// eps), the same value as a norm computed before the GEMV.
+__device__ __forceinline__ void prenorm_pairs(Smem &s, const float (&x)[NPT], int n, const NormW &nw, int tid) {
     float ss = 0.f;
     {
 #pragma clang fp contract(off)
 #pragma unroll
         for (int j = 0; j < NPT; ++j) {
-            const int k = tid + NT * j;
-            const float v = k < n ? x[k] : 0.f;
+            const float v = tid + NT * j < n ? x[j] : 0.f;
             ss += v * v;
         }
     }
-    const float tot = block_sum_fixed(ss, s.wsum);
-    const float rs = 1.0f / sqrtf(tot / (float)n + eps);
+    ss = wave_sum_dpp(ss);
+    if ((tid & 63) == 0) s.wsum[tid >> 6] = ss;
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
         const int k = tid + NT * j;
         if (k < n) {
             f16 hi, lo;
-            split_f16((x[k] * rs) * nw.w[j], hi, lo);
+            split_f16(x[j] * nw.w[j], hi, lo);
             s.xh[k] = hi;
             s.xl[k] = lo;
         }
@@ -326,13 +418,23 @@ __device__ __forceinline__ void norm_to_pairs(Smem &s, const float *x, int n, co
     if (tid < 8) s.xh[MAX_K + tid] = (f16)0.f;
     __syncthreads();
 }
-// fp32 values (LDS) -> fp16 pairs
-__device__ __forceinline__ void to_pairs(Smem &s, const float *x, int n, int tid) {
-    for (int k = tid; k < n; k += NT) {
-        f16 hi, lo;
-        split_f16(x[k], hi, lo);
-        s.xh[k] = hi;
-        s.xl[k] = lo;
+__device__ __forceinline__ float norm_scale(const Smem &s, int n, float eps) {
+    float t = 0.f;
+    for (int j = 0; j < NW; ++j) t += s.wsum[j];
+    return 1.0f / sqrtf(t / (float)n + eps);
+}
+// x[j] = element tid + NT * j (registers, n elements) -> fp16 pairs
+template <int N>
+__device__ __forceinline__ void pairs(Smem &s, const float (&x)[N], int n, int tid) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const int k = tid + NT * j;
+        if (k < n) {
+            f16 hi, lo;
+            split_f16(x[j], hi, lo);
+            s.xh[k] = hi;
+            s.xl[k] = lo;
+        }
     }
     if (tid < 8) s.xh[MAX_K + tid] = (f16)0.f;
     __syncthreads();
@@ -482,12 +584,10 @@ __device__ __forceinline__ float wave_total(const Smem &s, int nsum, int i, int 
     return t;
 }
 
-// The two residual parts of layer l's input rows [r0, r0 + n): DP0 and DP1 of layer l - 1 (l > 0), as ranges for
-// one gather into d0, d1.
-__device__ __forceinline__ void residual_ranges(const Geom &g, u64 *ll, unsigned seq, int l, int r0, int n, float *d0,
-                                                float *d1, Range *out) {
-    out[0] = Range{ll + w_dp(g, 0, r0), n, d0, tag_of(seq, l - 1, PH_DP)};
-    out[1] = Range{ll + w_dp(g, 1, r0), n, d1, tag_of(seq, l - 1, PH_DP)};
+// The two residual parts of layer l's input rows [r0, r0 + n): DP0 and DP1 of layer l - 1 (l > 0), as register ranges.
+__device__ __forceinline__ void residual_ranges(const Geom &g, u64 *ll, unsigned seq, int l, int r0, int n, RRange *out) {
+    out[0] = RRange{ll + w_dp(g, 0, r0), n, tag_of(seq, l - 1, PH_DP)};
+    out[1] = RRange{ll + w_dp(g, 1, r0), n, tag_of(seq, l - 1, PH_DP)};
 }
 
 // ------------------------------------------------------------------------------------------------------- kernel
@@ -519,24 +619,27 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                 const float bias = lp->qkv_b[item * 16 + r];
                 Tiles<FMT, TH> tl;
                 tl.load(lp->w[0], lp->sz[0], g.nkt_h, item, 0, g.nkt_h, wv, lane);
+                float x[NPT];
                 if (l == 0) {
                     const int token = stp.feed ? min(max(stp.feed[0], 0), g.V - 1) : tk.token;
-                    for (int k = tid; k < g.H; k += NT) s.xf[k] = packed_elem<FMT>(S->emb_w, S->emb_sz, g.nkt_h, token, k);
-                    __syncthreads();
+#pragma unroll
+                    for (int j = 0; j < NPT; ++j)
+                        x[j] = tid + NT * j < g.H ? packed_elem<FMT>(S->emb_w, S->emb_sz, g.nkt_h, token, tid + NT * j) : 0.f;
                 } else {
-                    Range rg[2];
-                    residual_ranges(g, ll, seq, l, 0, g.H, s.stage, s.stage + MAX_H, rg);
-                    if (!gather<MAX_H * 2 / NT, 2>(S->err, rg)) return;
-                    for (int k = tid; k < g.H; k += NT) s.xf[k] = s.stage[k] + s.stage[MAX_H + k];
-                    __syncthreads();
+                    RRange rg[2];
+                    residual_ranges(g, ll, seq, l, 0, g.H, rg);
+                    float v[2][NPT];
+                    if (!gather_r<NPT, 2>(S->err, rg, v, tid)) return;
+#pragma unroll
+                    for (int j = 0; j < NPT; ++j) x[j] = v[0][j] + v[1][j];
                 }
-                norm_to_pairs(s, s.xf, g.H, nw, S->eps, tid);
+                prenorm_pairs(s, x, g.H, nw, tid);
                 const float v = stream_dot<FMT, TH>(s, tl, wv, lane);
                 if (lane < 16) s.red[wv * 16 + lane] = v;
                 __syncthreads();
-                if (tid < 16) {
-                    st_word(ll + w_qkv(g, item * 16 + r), wave_total(s, 1, 0, r) + bias, tag_of(seq, l, PH_QKV));
-                }
+                if (tid < 16)
+                    st_word(ll + w_qkv(g, item * 16 + r), norm_scale(s, g.H, S->eps) * wave_total(s, 1, 0, r) + bias,
+                            tag_of(seq, l, PH_QKV));
             }
         }
         // ---------------------------------------------------------------- P2: attention over one chunk of keys
@@ -693,26 +796,28 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                 const int item = b - g.B3;
                 Tiles<FMT, TH> tl;
                 tl.load(lp->w[1], lp->sz[1], g.nkt_a, item, 0, g.nkt_a, wv, lane);
-                // the attention output and (l > 0) the residual parts of the tile's rows, in one hand-off
-                Range rg[3];
-                rg[0] = Range{ll + w_att(g, 0), g.NH * HD, s.xf, tag_of(seq, l, PH_ATT)};
+                // the attention output and (l > 0) the residual parts of the tile's rows, in one hand-off (threads
+                // 0..15 hold the residual parts of row tid)
+                RRange rg[3];
+                rg[0] = RRange{ll + w_att(g, 0), g.NH * HD, tag_of(seq, l, PH_ATT)};
                 if (l == 0) {
-                    if (tid < 16) {
-                        const int token = stp.feed ? min(max(stp.feed[0], 0), g.V - 1) : tk.token;
-                        s.xr[0][tid] = packed_elem<FMT>(S->emb_w, S->emb_sz, g.nkt_h, token, item * 16 + tid);
-                        s.xr[1][tid] = 0.f;
-                    }
-                    rg[1] = rg[2] = Range{ll, 0, s.xf, 0u};
+                    rg[1] = rg[2] = RRange{ll, 0, 0u};
                 } else {
-                    residual_ranges(g, ll, seq, l, item * 16, 16, s.xr[0], s.xr[1], rg + 1);
+                    residual_ranges(g, ll, seq, l, item * 16, 16, rg + 1);
                 }
-                if (!gather<(MAX_H + 32 + NT - 1) / NT, 3>(S->err, rg)) return;
-                to_pairs(s, s.xf, g.NH * HD, tid);
+                float v3[3][NPT];
+                if (!gather_r<NPT, 3>(S->err, rg, v3, tid)) return;
+                if (l == 0 && tid < 16) {
+                    const int token = stp.feed ? min(max(stp.feed[0], 0), g.V - 1) : tk.token;
+                    v3[1][0] = packed_elem<FMT>(S->emb_w, S->emb_sz, g.nkt_h, token, item * 16 + tid);
+                    v3[2][0] = 0.f;
+                }
+                pairs<NPT>(s, v3[0], g.NH * HD, tid);
                 const float v = stream_dot<FMT, TH>(s, tl, wv, lane);
                 if (lane < 16) s.red[wv * 16 + lane] = v;
                 __syncthreads();
                 if (tid < 16) {
-                    const float x = s.xr[0][r] + s.xr[1][r];
+                    const float x = v3[1][0] + v3[2][0];
                     st_word(ll + w_xm(g, item * 16 + r), x + wave_total(s, 1, 0, r), tag_of(seq, l, PH_XM));
                 }
             }
@@ -721,8 +826,7 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
         {
             CStatic *S = fresh(sp);
             const Geom g = S->g;
-            int units[MAXU];
-            const int nu = p4_units(g, b, units);
+            const int nu = p4_count(g, b);
             if (nu > 0) {
                 const int tid = fresh_tid(), lane = tid & 63, wv = tid >> 6, r = lane & 15;
                 CLayer *lp = layer_of(S, l);
@@ -734,14 +838,15 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
 #pragma unroll
                 for (int i = 0; i < MAXU; ++i) {
                     if (i < nu) {
-                        const int u = units[i];
+                        const int u = p4_unit(g, b, i);
                         tg[i].load(lp->w[2], lp->sz[2], g.nkt_h, 2 * u, 0, g.nkt_h, wv, lane);
                         tu[i].load(lp->w[2], lp->sz[2], g.nkt_h, 2 * u + 1, 0, g.nkt_h, wv, lane);
                     }
                 }
-                Range rg[1] = {Range{ll + w_xm(g, 0), g.H, s.xf, tag_of(seq, l, PH_XM)}};
-                if (!gather<MAX_H / NT, 1>(S->err, rg)) return;
-                norm_to_pairs(s, s.xf, g.H, nw, S->eps, tid);
+                RRange rg[1] = {RRange{ll + w_xm(g, 0), g.H, tag_of(seq, l, PH_XM)}};
+                float xm[1][NPT];
+                if (!gather_r<NPT, 1>(S->err, rg, xm, tid)) return;
+                prenorm_pairs(s, xm[0], g.H, nw, tid);
                 XOps<FMT, TH> xo;
                 xo.load(s, tg[0].nvalid, wv, lane);
                 // one row group at a time: group j + 1's products start after group j's sum
@@ -759,11 +864,18 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                     }
                 }
                 __syncthreads();
-                if (tid < 16) {
-                    for (int i = 0; i < nu; ++i) {
-                        const float gt = wave_total(s, 2 * MAXU, 2 * i, r), up = wave_total(s, 2 * MAXU, 2 * i + 1, r);
-                        st_word(ll + w_act(g, units[i] * 16 + r), silu_f(gt) * up, tag_of(seq, l, PH_ACT));
-                    }
+                if (tid < 64) {
+                    // lane 16 i + r: row r of unit i; rows r (even) and r + 1 go out as one word of two 24-bit values
+                    const int i = tid >> 4;
+                    const float rs = norm_scale(s, g.H, S->eps);
+                    const float gt = rs * wave_total(s, 2 * MAXU, 2 * min(i, MAXU - 1), r);
+                    const float up = rs * wave_total(s, 2 * MAXU, 2 * min(i, MAXU - 1) + 1, r);
+                    const uint32_t a = f24_of(silu_f(gt) * up);
+                    const uint32_t an = (uint32_t)__shfl_xor((int)a, 1);
+                    if (i < nu && (r & 1) == 0)
+                        __hip_atomic_store(ll + w_act(g, p4_unit(g, b, i) * 8 + r / 2),
+                                           ((u64)tag16_of(seq, l) << 48) | ((u64)an << 24) | a, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
                 }
                 __syncthreads();
             }
@@ -781,17 +893,33 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                 Tiles<FMT, T5> tl;
                 tl.load(lp->w[3], lp->sz[3], g.nkt_i, rt, kt0, kt1, wv, lane);
                 const int klen = (kt1 - kt0) * TileGeom<FMT>::KT;
-                // the activations of the k half and (k half 0) the o_proj rows of the tile, which it adds
-                Range rg[2] = {Range{ll + w_act(g, kt0 * TileGeom<FMT>::KT), klen, s.stage, tag_of(seq, l, PH_ACT)},
-                               Range{ll + w_xm(g, rt * 16), kh == 0 ? 16 : 0, s.xr[0], tag_of(seq, l, PH_XM)}};
-                if (!gather<(MAX_K + 16 + NT - 1) / NT, 2>(S->err, rg)) return;
-                to_pairs(s, s.stage, klen, tid);
+                // the activations of the k half and (k half 0) the o_proj rows of the tile, which it adds (threads
+                // 0..15 hold row tid's)
+                constexpr int NPK = (MAX_K / 2 + NT - 1) / NT;     // activation words (two values each) per thread
+                RRange rg[2] = {RRange{ll + w_act(g, kt0 * TileGeom<FMT>::KT / 2), klen / 2, tag16_of(seq, l), 48},
+                                RRange{ll + w_xm(g, rt * 16), kh == 0 ? 16 : 0, tag_of(seq, l, PH_XM)}};
+                u64 v5[2][NPK];
+                if (!gather_w<NPK, 2>(S->err, rg, v5, tid)) return;
+#pragma unroll
+                for (int j = 0; j < NPK; ++j) {
+                    const int m = tid + NT * j;
+                    if (m < klen / 2) {
+                        f16 h0, l0, h1, l1;
+                        split_f16(f32_of24((uint32_t)v5[0][j] & 0xFFFFFFu), h0, l0);
+                        split_f16(f32_of24((uint32_t)(v5[0][j] >> 24) & 0xFFFFFFu), h1, l1);
+                        *(f16x2 *)&s.xh[2 * m] = (f16x2){h0, h1};
+                        *(f16x2 *)&s.xl[2 * m] = (f16x2){l0, l1};
+                    }
+                }
+                if (tid < 8) s.xh[MAX_K + tid] = (f16)0.f;
+                __syncthreads();
                 const float v = stream_dot<FMT, T5>(s, tl, wv, lane);
                 if (lane < 16) s.red[wv * 16 + lane] = v;
                 __syncthreads();
                 if (tid < 16) {
                     const float dv = wave_total(s, 1, 0, r);
-                    st_word(ll + w_dp(g, kh, rt * 16 + r), kh == 0 ? s.xr[0][r] + dv : dv, tag_of(seq, l, PH_DP));
+                    st_word(ll + w_dp(g, kh, rt * 16 + r), kh == 0 ? __uint_as_float((unsigned)v5[1][0]) + dv : dv,
+                            tag_of(seq, l, PH_DP));
                 }
                 __syncthreads();
             }
@@ -804,19 +932,18 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
         const int tid = fresh_tid();
         NormW nw;
         nw.load(S->final_norm, g.H, tid);
-        Range rg[2];
-        residual_ranges(g, S->ll, seq, g.L, 0, g.H, s.stage, s.stage + MAX_H, rg);
-        if (!gather<MAX_H * 2 / NT, 2>(S->err, rg)) return;
-        for (int k = tid; k < g.H; k += NT) s.xf[k] = s.stage[k] + s.stage[MAX_H + k];
-        __syncthreads();
+        RRange rg[2];
+        residual_ranges(g, S->ll, seq, g.L, 0, g.H, rg);
+        float v[2][NPT], x[NPT];
+        if (!gather_r<NPT, 2>(S->err, rg, v, tid)) return;
         float ss = 0.f;
         {
 #pragma clang fp contract(off)
 #pragma unroll
             for (int j = 0; j < NPT; ++j) {
-                const int k = tid + NT * j;
-                const float v = k < g.H ? s.xf[k] : 0.f;
-                ss += v * v;
+                x[j] = v[0][j] + v[1][j];
+                const float xv = tid + NT * j < g.H ? x[j] : 0.f;
+                ss += xv * xv;
             }
         }
         const float tot = block_sum_fixed(ss, s.wsum);
@@ -825,7 +952,7 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
 #pragma unroll
         for (int j = 0; j < NPT; ++j) {
             const int k = tid + NT * j;
-            if (k < g.H) xn[k] = (f16)((s.xf[k] * rs) * nw.w[j]);
+            if (k < g.H) xn[k] = (f16)((x[j] * rs) * nw.w[j]);
         }
     }
 }
@@ -861,7 +988,7 @@ inline bool make_geom(const sp_model_desc &d, int n_slots, int nb, Geom &g, cons
     g.o_part = o; o += (size_t)g.NH * g.CM * (2 + g.HD);
     g.o_att = o; o += (size_t)g.NH * g.HD;
     g.o_xm = o; o += g.H;
-    g.o_act = o; o += g.I;
+    g.o_act = o; o += g.I / 2;
     g.o_dp = o; o += (size_t)KS * g.H;
     g.words = o;
     return true;
@@ -908,14 +1035,14 @@ inline bool check_geom(const Geom &g, int TH, int T5, const char **why) {
         const int bk = blk_p4(g, u);
         if (bk < 0 || bk >= g.nb) return no("gate_up block");
         if (++per[bk] > MAXU) return no("gate_up units per block");
-        if (!in(w_act(g, u * 16), 16, g.o_act, e_act) || 2 * u + 1 >= 2 * g.NU) return no("activation words");
+        if (!in(w_act(g, u * 8), 8, g.o_act, e_act) || 2 * u + 1 >= 2 * g.NU) return no("activation words");
     }
     for (int bk = 0; bk < g.nb; ++bk) {             // the kernel's per-block list is exactly the units mapped there
-        int u[MAXU];
-        const int n = p4_units(g, bk, u);
-        if (n != per[bk]) return no("gate_up unit list");
+        const int n = p4_count(g, bk);
+        if (n != per[bk] || n > MAXU) return no("gate_up unit list");
         for (int i = 0; i < n; ++i) {
-            if (u[i] < 0 || u[i] >= g.NU || blk_p4(g, u[i]) != bk || seen[u[i]]++) return no("gate_up unit list");
+            const int u = p4_unit(g, bk, i);
+            if (u < 0 || u >= g.NU || blk_p4(g, u) != bk || seen[u]++) return no("gate_up unit list");
         }
     }
     for (int dd = 0; dd < g.ND; ++dd) {
@@ -924,7 +1051,7 @@ inline bool check_geom(const Geom &g, int TH, int T5, const char **why) {
         const int rt = dd % g.NO, kh = dd / g.NO;
         const int kt0 = kh * g.nk5, kt1 = std::min(g.nkt_i, kt0 + g.nk5);
         if (kt0 >= kt1 || rt * 16 + 16 > g.H) return no("down item");
-        if (!in(w_act(g, kt0 * g.KT), (size_t)(kt1 - kt0) * g.KT, g.o_act, e_act)) return no("down input words");
+        if (!in(w_act(g, kt0 * g.KT / 2), (size_t)(kt1 - kt0) * g.KT / 2, g.o_act, e_act)) return no("down input words");
         if ((kt1 - kt0) * g.KT > MAX_K) return no("down input staging");
         if (!in(w_xm(g, rt * 16), 16, g.o_xm, e_xm)) return no("down residual words");
         if (!in(w_dp(g, kh, rt * 16), 16, g.o_dp, e_dp)) return no("down output words");

@@ -954,7 +954,7 @@ bool sp_engine::prepare_d1() {
             l.down.fmt != d.weight_format) { d1_why = "mixed weight formats"; return false; }
     if (embed.fmt != d.weight_format) { d1_why = "mixed weight formats"; return false; }
     int per_cu = 0;
-    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, d1k->fn, d1::NT, sizeof(d1::Smem)));
+    HIPCHK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, d1k->fn, d1::NT, d1::SMEM_BYTES));
     if (per_cu < 1) { d1_why = "the block does not fit a CU"; return false; }
     dev_free(d1_ll); dev_free(d1_layers); dev_free(d1_static);
     d1_ll = nullptr; d1_layers = nullptr; d1_static = nullptr;
@@ -1009,11 +1009,11 @@ bool sp_engine::run_d1(const sp_token &t, int flags) {
     const d1::Static *sp = d1_static;
     void *args[] = {(void *)&sp, &a};
     hipError_t le = d1_plain ? hipErrorNotSupported
-                             : hipLaunchCooperativeKernel(d1k->fn, dim3(d1g.nb), dim3(d1::NT), args, sizeof(d1::Smem), stream);
+                             : hipLaunchCooperativeKernel(d1k->fn, dim3(d1g.nb), dim3(d1::NT), args, d1::SMEM_BYTES, stream);
     if (le != hipSuccess) {
         (void)hipGetLastError();
         d1_plain = true;
-        le = hipLaunchKernel(d1k->fn, dim3(d1g.nb), dim3(d1::NT), args, sizeof(d1::Smem), stream);
+        le = hipLaunchKernel(d1k->fn, dim3(d1g.nb), dim3(d1::NT), args, d1::SMEM_BYTES, stream);
     }
     if (le != hipSuccess) {
         (void)hipGetLastError();
@@ -1461,7 +1461,7 @@ int sp_persistent_geometry(const sp_model_desc *desc, int32_t n_slots, int32_t n
     if (!k) { g_err = "no instantiation for this shape"; return SP_EINVAL; }
     if (!d1::check_geom(g, k->th, k->t5, &why)) { g_err = why; return SP_EINVAL; }
     const int32_t v[12] = {g.NQ, g.NKV * g.CM, g.NH, g.NO, g.NU, g.ND, g.nu_max, g.B2, g.B3, g.B5,
-                           (int32_t)g.words, (int32_t)sizeof(d1::Smem)};
+                           (int32_t)g.words, (int32_t)d1::SMEM_BYTES};
     std::memcpy(info, v, sizeof(v));
     return SP_OK;
 }

@@ -51,7 +51,7 @@ def test_model_shapes_fit_and_walk_clean(name, fmt, n_slots):
     assert b2 == nq and b3 == 256 - no and b5 == 256 - nd
     assert b2 + chunks + comb <= 256                      # qkv tiles, chunks and combiners on distinct blocks
     assert nu_max == min(3, -(-nu // b3)) and nu <= 3 * b3 + no   # <= 3 units per block, overflow on o_proj blocks
-    assert words == (NH + 2 * NKV) * HD + NH * (chunks // NKV) * (2 + HD) + NH * HD + H + I + 2 * H
+    assert words == (NH + 2 * NKV) * HD + NH * (chunks // NKV) * (2 + HD) + NH * HD + H + I // 2 + 2 * H
     assert 80 * 1024 < lds <= 160 * 1024                  # one block per CU
 
 
