@@ -45,6 +45,7 @@
 // most two tiles (or one row group) of MFMA results in flight.
 #pragma once
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "sp_gemv.h"
@@ -63,6 +64,7 @@ constexpr int MAX_K = 4608;             // widest GEMV input a block stages (hal
 constexpr int MAX_G = 8;                // query heads per kv head
 constexpr int MAX_HD = 128;
 constexpr int MAX_CM = 64;              // attention chunks per kv head (one lane each in the combine)
+constexpr int MAX_T5 = 9;               // k-tiles per wave of a down item whose tiles can wait in LDS
 
 // Tag of (launch sequence, layer, phase): unique per launch and per (layer, phase) within it.
 enum { PH_QKV = 1, PH_PART = 2, PH_ATT = 3, PH_XM = 4, PH_ACT = 5, PH_DP = 6 };
@@ -362,9 +364,15 @@ struct Smem {
     float stage[MAX_K + 16];                  // gathered words (the attention's qkv rows, the combine's chunk records)
 };
 // Dynamic LDS of a launch: at least 84 KiB, so that no CU (160 KiB of LDS) can hold two blocks and the grid of one
-// block per CU is spread over every CU.
+// block per CU is spread over every CU.  The kernel adds a static array for the down tiles (at most MAX_T5 KiB per
+// wave).
 constexpr size_t SMEM_BYTES = sizeof(Smem) > 84 * 1024 ? sizeof(Smem) : 84 * 1024;
-static_assert(SMEM_BYTES <= 160 * 1024, "one block's LDS fits a CU");
+static_assert(SMEM_BYTES + NW * MAX_T5 * TILE_BYTES <= 160 * 1024, "one block's LDS fits a CU");
+
+// Block barrier for LDS data only: waits for the wave's LDS (and scalar) operations, not for its vector memory loads,
+// so global-to-LDS weight copies issued earlier stay in flight across it (a __syncthreads() waits for those too).
+// The memory clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Block-wide sum of one value per thread, in a fixed order (DPP per wave, then the wave sums in wave order).
 __device__ __forceinline__ float block_sum_fixed(float v, float *wsum) {
@@ -416,7 +424,7 @@ __device__ __forceinline__ void prenorm_pairs(Smem &s, const float (&x)[NPT], in
         }
     }
     if (tid < 8) s.xh[MAX_K + tid] = (f16)0.f;
-    __syncthreads();
+    lds_barrier();
 }
 __device__ __forceinline__ float norm_scale(const Smem &s, int n, float eps) {
     float t = 0.f;
@@ -437,7 +445,7 @@ __device__ __forceinline__ void pairs(Smem &s, const float (&x)[N], int n, int t
         }
     }
     if (tid < 8) s.xh[MAX_K + tid] = (f16)0.f;
-    __syncthreads();
+    lds_barrier();
 }
 
 // Weight tiles of one row group: wave w takes the T consecutive k-tiles kt0 + w T .. (one address per row group, the
@@ -532,6 +540,89 @@ __device__ __forceinline__ float stream_dot(const Smem &s, Tiles<FMT, T> &tl, in
     return FMT == 1 ? acc4[0] + acc4[1] : acc;
 }
 
+// One 16-byte global-to-LDS copy per lane (global_load_lds_dwordx4): lane i's 16 bytes at g land at LDS byte address
+// lds + 16 i.  Written as inline asm so that the compiler does not track the copy: it would otherwise make every LDS
+// access of the block that it cannot prove disjoint from the copy, inside the layer loop all of them, wait for every
+// outstanding vector memory operation (the cache and hand-off stores included).  The copy completes in order with
+// the wave's other vector memory loads; the reader of the tiles waits for it explicitly (copy_wait).  M0 (the LDS
+// address) is set here; no other code of this kernel uses M0.
+__device__ __forceinline__ void lds_copy16(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(g), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void copy_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Weight tiles of one row group whose 16-byte lane slices wait in LDS (an array of their own; tile t of wave w at (w T
+// + t) KiB, the lane's slice at 16 lane) instead of registers.  The scales stay in registers.  Each wave reads only
+// the tiles it copied, after copy_wait.
+template <int FMT, int T>
+struct LdsTiles {
+    typename SideOf<FMT>::type sd[FMT == 1 ? 1 : T];
+    int nvalid;
+    uint8_t *lds;
+    __device__ __forceinline__ void load(uint8_t *wl, const uint8_t *w, const f16 *sz, int nkt, int grp, int kt0,
+                                         int kt1, int wv, int lane) {
+        lds = wl;
+        static_assert(T <= MAX_T5, "the LDS holds MAX_T5 tiles per wave");
+        const int first = kt0 + wv * T;
+        nvalid = max(0, min(T, kt1 - first));
+        const int base = nvalid > 0 ? first : kt0;
+        const uint8_t *wb = w + ((size_t)grp * nkt + base) * TILE_BYTES + lane * 16;
+        const int r = lane & 15;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int tt = t < nvalid ? t : 0;
+            const uint32_t la = (uint32_t)(size_t)((__attribute__((address_space(3))) uint8_t *)wl) + (wv * T + t) * TILE_BYTES;
+            lds_copy16(wb + tt * TILE_BYTES, __builtin_amdgcn_readfirstlane(la));
+            if constexpr (FMT == 2) sd[t] = *((const uint32_t *)(sz + ((size_t)grp * nkt + base + tt) * 32) + r);
+            if constexpr (FMT == 3) sd[t] = *((const u32x4 *)(sz + ((size_t)grp * nkt + base + tt) * 128) + r);
+        }
+    }
+};
+template <int FMT, int T>
+__device__ __forceinline__ float tile_scale(const LdsTiles<FMT, T> &tl, int t, int st, float &offs) {
+    if constexpr (FMT == 2) {
+        const uint32_t d = tl.sd[t];
+        offs = QBias<FMT>::V;
+        return (float)__builtin_bit_cast(f16, (uint16_t)(st == 0 ? (d & 0xffffu) : (d >> 16)));
+    } else {
+        uint32_t d;
+        if (st == 0) d = tl.sd[t].x; else if (st == 1) d = tl.sd[t].y; else if (st == 2) d = tl.sd[t].z; else d = tl.sd[t].w;
+        offs = QBias<FMT>::V + (float)__builtin_bit_cast(f16, (uint16_t)(d >> 16));
+        return (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
+    }
+}
+// stream_dot over LDS tiles: tile t + 2's weights and activations are read after tile t's sum.
+template <int FMT, int T>
+__device__ __forceinline__ float stream_dot(const Smem &s, const LdsTiles<FMT, T> &tl, int wv, int lane) {
+    constexpr int ST = TileGeom<FMT>::STEPS;
+    const f16x8 ones8 = (f16x8){1, 1, 1, 1, 1, 1, 1, 1};
+    float acc = 0.f;
+    f32x4 acc4 = (f32x4){0.f, 0.f, 0.f, 0.f};
+    int kdep[2] = {0, 0};
+    copy_wait();
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const bool live = t < tl.nvalid;
+        const u32x4 wt = *(const u32x4 *)(tl.lds + (wv * T + t) * TILE_BYTES + lane * 16 + 4 * kdep[t & 1]);
+#pragma unroll
+        for (int st = 0; st < ST; ++st) {
+            const f16x8 xa = x_operand<FMT, T>(s, t, st, live, wv, lane, kdep[t & 1]);
+            if constexpr (FMT == 1) {
+                acc4 = mfma16(xa, __builtin_bit_cast(f16x8, wt), acc4);
+            } else {
+                const f32x4 sx = mfma16(xa, ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                const f32x4 dd = mfma16(xa, biased_step<FMT>(wt, st), (f32x4){0.f, 0.f, 0.f, 0.f});
+                float offs;
+                const float scale = tile_scale<FMT, T>(tl, t, st, offs);
+                acc = fmaf(scale, fmaf(-offs, sx[0], dd[0]) + fmaf(-offs, sx[1], dd[1]), acc);
+            }
+        }
+        const float v = FMT == 1 ? acc4[0] : acc;
+        asm volatile("" : "+v"(kdep[t & 1]) : "v"(v));
+    }
+    return FMT == 1 ? acc4[0] + acc4[1] : acc;
+}
+
 // The A operands of the wave's T tiles, shared by several row groups over the same k range, and (quantized formats)
 // the block sums of A rows 0 and 1.
 template <int FMT, int T>
@@ -590,12 +681,80 @@ __device__ __forceinline__ void residual_ranges(const Geom &g, u64 *ll, unsigned
     out[1] = RRange{ll + w_dp(g, 1, r0), n, tag_of(seq, l - 1, PH_DP)};
 }
 
+// The down tiles of block b's P5 item (row tile, k half), into LDS.
+template <int FMT, int T5>
+__device__ __forceinline__ void down_tiles(uint8_t *wl, LdsTiles<FMT, T5> &t5, const Geom &g, CLayer *lp, int b, int wv,
+                                           int lane) {
+    const int d = b - g.B5, rt = d % g.NO, kh = d / g.NO;
+    const int kt0 = kh * g.nk5, kt1 = min(g.nkt_i, kt0 + g.nk5);
+    t5.load(wl, lp->w[3], lp->sz[3], g.nkt_i, rt, kt0, kt1, wv, lane);
+}
+template <int FMT, int T5>
+__device__ __forceinline__ void down_tiles(uint8_t *, Tiles<FMT, T5> &t5, const Geom &g, CLayer *lp, int b, int wv,
+                                           int lane) {
+    const int d = b - g.B5, rt = d % g.NO, kh = d / g.NO;
+    const int kt0 = kh * g.nk5, kt1 = min(g.nkt_i, kt0 + g.nk5);
+    t5.load(lp->w[3], lp->sz[3], g.nkt_i, rt, kt0, kt1, wv, lane);
+}
+
+// P4 of one block whose NU <= NG gate_up units' tiles are loaded: RMSNorm of the o_proj output XM (scale applied to
+// the sums), the gate and up row groups of every unit, SwiGLU, and the activations as packed words.  False when the
+// hand-off timed out (the caller leaves the kernel).
+template <int FMT, int TH, int NG>
+__device__ __forceinline__ bool gate_up(Smem &s, CStatic *S, const Geom &g, CLayer *lp, int l, unsigned seq, int b,
+                                        int nu, Tiles<FMT, TH> *tg, Tiles<FMT, TH> *tu, int tid) {
+    const int lane = tid & 63, wv = tid >> 6, r = lane & 15;
+    u64 *ll = S->ll;
+    NormW nw;
+    nw.load(lp->n_post, g.H, tid);
+    RRange rg[1] = {RRange{ll + w_xm(g, 0), g.H, tag_of(seq, l, PH_XM)}};
+    float xm[1][NPT];
+    if (!gather_r<NPT, 1>(S->err, rg, xm, tid)) return false;
+    prenorm_pairs(s, xm[0], g.H, nw, tid);
+    XOps<FMT, TH> xo;
+    xo.load(s, tg[0].nvalid, wv, lane);
+    // one row group at a time: group j + 1's products start after group j's sum (absent units are skipped by
+    // scalar branches: nu is block-uniform)
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        if (i < nu) {
+            const float vg = group_dot<FMT, TH>(xo, tg[i]);
+            tu[i].after_all(vg);
+            const float vu = group_dot<FMT, TH>(xo, tu[i]);
+            if (i + 1 < NG) tg[i + 1].after_all(vu);
+            if (lane < 16) {
+                s.red[(wv * 2 * MAXU + 2 * i) * 16 + lane] = vg;
+                s.red[(wv * 2 * MAXU + 2 * i + 1) * 16 + lane] = vu;
+            }
+        }
+    }
+    lds_barrier();
+    if (tid < 16 * NG) {
+        // lane 16 i + r: row r of unit i; rows r (even) and r + 1 go out as one word of two 24-bit values
+        const int i = tid >> 4;
+        const float rs = norm_scale(s, g.H, S->eps);
+        const float gt = rs * wave_total(s, 2 * MAXU, 2 * i, r), up = rs * wave_total(s, 2 * MAXU, 2 * i + 1, r);
+        const uint32_t a = f24_of(silu_f(gt) * up);
+        const uint32_t an = (uint32_t)__shfl_xor((int)a, 1);
+        if (i < nu && (r & 1) == 0)
+            __hip_atomic_store(ll + w_act(g, p4_unit(g, b, i) * 8 + r / 2),
+                               ((u64)tag16_of(seq, l) << 48) | ((u64)an << 24) | a, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    lds_barrier();
+    return true;
+}
+
 // ------------------------------------------------------------------------------------------------------- kernel
 // TH: k-tiles per wave for K = H (and K = NH * HD); T5: k-tiles per wave for one down item.
 template <int FMT, int HD, int TH, int T5>
 __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Smem &s = *(Smem *)smem_raw;
+    // the down tiles of a P5 item wait in LDS where they fit (else in registers, loaded in P5)
+    constexpr bool DMA5 = T5 <= MAX_T5;
+    typedef std::conditional_t<DMA5, LdsTiles<FMT, T5>, Tiles<FMT, T5>> T5T;
+    __shared__ __align__(16) uint8_t wt5[DMA5 ? NW * T5 * TILE_BYTES : 16];
     const int b = blockIdx.x;
     const unsigned seq = stp.seq;
     const sp_token &tk = stp.tok;
@@ -636,7 +795,7 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                 prenorm_pairs(s, x, g.H, nw, tid);
                 const float v = stream_dot<FMT, TH>(s, tl, wv, lane);
                 if (lane < 16) s.red[wv * 16 + lane] = v;
-                __syncthreads();
+                lds_barrier();
                 if (tid < 16)
                     st_word(ll + w_qkv(g, item * 16 + r), norm_scale(s, g.H, S->eps) * wave_total(s, 1, 0, r) + bias,
                             tag_of(seq, l, PH_QKV));
@@ -709,7 +868,7 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                             vdst[j] = vv;
                         }
                     }
-                    __syncthreads();
+                    lds_barrier();
                     // wave h (< G): query head kvh * G + h; lane j scores key j
                     if (wv < G) {
                         const int h = wv;
@@ -748,7 +907,7 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                             st_word(ll + w_part(g, qh, c, 1), lsum, tp);
                         }
                     }
-                    __syncthreads();
+                    lds_barrier();
                 }
             }
         }
@@ -775,16 +934,25 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                     if (tid < MAX_CM) s.cw[tid] = wc;
                     if (tid == 0) s.wsum[0] = L;
                 }
-                __syncthreads();
+                lds_barrier();
                 if (tid < HD) {
                     float acc = 0.f;
 #pragma unroll 4
                     for (int c = 0; c < C; ++c) acc += s.cw[c] * s.stage[c * rec + 2 + tid];
                     st_word(ll + w_att(g, qh * HD + tid), acc / s.wsum[0], tag_of(seq, l, PH_ATT));
                 }
-                __syncthreads();
+                lds_barrier();
             }
         }
+        // ---------------------------------------------------------------- P3, P4 and P5 share the down tiles.
+        // Loads complete in order, and a load issued between a hand-off's arrival and the block's own publishing
+        // stores delays those stores, so weights are issued only right before a phase's wait, and bulk loads at the
+        // start of a layer slow the attention phase (its loads and stores share the memory system with them).  A
+        // block with three gate_up units (P4 waits ~10 us for the o_proj output) copies the down tiles of its P5 item
+        // to LDS together with its gate_up tiles; its activation poll in P5 then does not queue behind 70 KiB of its
+        // own loads.  The other P5 blocks load the down tiles when P5 starts.
+        T5T t5;
+        bool have5 = false;                        // block-uniform
         // ---------------------------------------------------------------- P3: o_proj row tile + residual
         {
             CStatic *S = fresh(sp);
@@ -815,7 +983,7 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                 pairs<NPT>(s, v3[0], g.NH * HD, tid);
                 const float v = stream_dot<FMT, TH>(s, tl, wv, lane);
                 if (lane < 16) s.red[wv * 16 + lane] = v;
-                __syncthreads();
+                lds_barrier();
                 if (tid < 16) {
                     const float x = v3[1][0] + v3[2][0];
                     st_word(ll + w_xm(g, item * 16 + r), x + wave_total(s, 1, 0, r), tag_of(seq, l, PH_XM));
@@ -827,57 +995,32 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
             CStatic *S = fresh(sp);
             const Geom g = S->g;
             const int nu = p4_count(g, b);
+            const bool is5 = b >= g.B5 && b < g.B5 + g.ND;
             if (nu > 0) {
-                const int tid = fresh_tid(), lane = tid & 63, wv = tid >> 6, r = lane & 15;
+                const int tid = fresh_tid(), lane = tid & 63, wv = tid >> 6;
                 CLayer *lp = layer_of(S, l);
-                u64 *ll = S->ll;
-                // block-uniform unit count: the loads and products of absent units are skipped by scalar branches
-                NormW nw;
-                nw.load(lp->n_post, g.H, tid);
-                Tiles<FMT, TH> tg[MAXU], tu[MAXU];
+                if (b < g.B3) {
+                    Tiles<FMT, TH> tg[MAXU], tu[MAXU];
 #pragma unroll
-                for (int i = 0; i < MAXU; ++i) {
-                    if (i < nu) {
-                        const int u = p4_unit(g, b, i);
-                        tg[i].load(lp->w[2], lp->sz[2], g.nkt_h, 2 * u, 0, g.nkt_h, wv, lane);
-                        tu[i].load(lp->w[2], lp->sz[2], g.nkt_h, 2 * u + 1, 0, g.nkt_h, wv, lane);
-                    }
-                }
-                RRange rg[1] = {RRange{ll + w_xm(g, 0), g.H, tag_of(seq, l, PH_XM)}};
-                float xm[1][NPT];
-                if (!gather_r<NPT, 1>(S->err, rg, xm, tid)) return;
-                prenorm_pairs(s, xm[0], g.H, nw, tid);
-                XOps<FMT, TH> xo;
-                xo.load(s, tg[0].nvalid, wv, lane);
-                // one row group at a time: group j + 1's products start after group j's sum
-#pragma unroll
-                for (int i = 0; i < MAXU; ++i) {
-                    if (i < nu) {
-                        const float vg = group_dot<FMT, TH>(xo, tg[i]);
-                        tu[i].after_all(vg);
-                        const float vu = group_dot<FMT, TH>(xo, tu[i]);
-                        if (i + 1 < MAXU) tg[i + 1].after_all(vu);
-                        if (lane < 16) {
-                            s.red[(wv * 2 * MAXU + 2 * i) * 16 + lane] = vg;
-                            s.red[(wv * 2 * MAXU + 2 * i + 1) * 16 + lane] = vu;
+                    for (int i = 0; i < MAXU; ++i) {
+                        if (i < nu) {
+                            const int u = p4_unit(g, b, i);
+                            tg[i].load(lp->w[2], lp->sz[2], g.nkt_h, 2 * u, 0, g.nkt_h, wv, lane);
+                            tu[i].load(lp->w[2], lp->sz[2], g.nkt_h, 2 * u + 1, 0, g.nkt_h, wv, lane);
                         }
                     }
+                    if (DMA5 && is5) {
+                        down_tiles(wt5, t5, g, lp, b, wv, lane);
+                        have5 = true;
+                    }
+                    if (!gate_up<FMT, TH, MAXU>(s, S, g, lp, l, seq, b, nu, tg, tu, tid)) return;
+                } else {
+                    Tiles<FMT, TH> tg1, tu1;
+                    const int u = p4_unit(g, b, 0);
+                    tg1.load(lp->w[2], lp->sz[2], g.nkt_h, 2 * u, 0, g.nkt_h, wv, lane);
+                    tu1.load(lp->w[2], lp->sz[2], g.nkt_h, 2 * u + 1, 0, g.nkt_h, wv, lane);
+                    if (!gate_up<FMT, TH, 1>(s, S, g, lp, l, seq, b, 1, &tg1, &tu1, tid)) return;
                 }
-                __syncthreads();
-                if (tid < 64) {
-                    // lane 16 i + r: row r of unit i; rows r (even) and r + 1 go out as one word of two 24-bit values
-                    const int i = tid >> 4;
-                    const float rs = norm_scale(s, g.H, S->eps);
-                    const float gt = rs * wave_total(s, 2 * MAXU, 2 * min(i, MAXU - 1), r);
-                    const float up = rs * wave_total(s, 2 * MAXU, 2 * min(i, MAXU - 1) + 1, r);
-                    const uint32_t a = f24_of(silu_f(gt) * up);
-                    const uint32_t an = (uint32_t)__shfl_xor((int)a, 1);
-                    if (i < nu && (r & 1) == 0)
-                        __hip_atomic_store(ll + w_act(g, p4_unit(g, b, i) * 8 + r / 2),
-                                           ((u64)tag16_of(seq, l) << 48) | ((u64)an << 24) | a, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
-                __syncthreads();
             }
         }
         // ---------------------------------------------------------------- P5: down row tile, one k half
@@ -890,8 +1033,7 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                 u64 *ll = S->ll;
                 const int d = b - g.B5, rt = d % g.NO, kh = d / g.NO;
                 const int kt0 = kh * g.nk5, kt1 = min(g.nkt_i, kt0 + g.nk5);
-                Tiles<FMT, T5> tl;
-                tl.load(lp->w[3], lp->sz[3], g.nkt_i, rt, kt0, kt1, wv, lane);
+                if (!have5) down_tiles(wt5, t5, g, lp, b, wv, lane);
                 const int klen = (kt1 - kt0) * TileGeom<FMT>::KT;
                 // the activations of the k half and (k half 0) the o_proj rows of the tile, which it adds (threads
                 // 0..15 hold row tid's)
@@ -912,16 +1054,16 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                     }
                 }
                 if (tid < 8) s.xh[MAX_K + tid] = (f16)0.f;
-                __syncthreads();
-                const float v = stream_dot<FMT, T5>(s, tl, wv, lane);
+                lds_barrier();
+                const float v = stream_dot<FMT, T5>(s, t5, wv, lane);
                 if (lane < 16) s.red[wv * 16 + lane] = v;
-                __syncthreads();
+                lds_barrier();
                 if (tid < 16) {
                     const float dv = wave_total(s, 1, 0, r);
                     st_word(ll + w_dp(g, kh, rt * 16 + r), kh == 0 ? __uint_as_float((unsigned)v5[1][0]) + dv : dv,
                             tag_of(seq, l, PH_DP));
                 }
-                __syncthreads();
+                lds_barrier();
             }
         }
     }
