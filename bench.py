@@ -4,15 +4,16 @@
 Default workload (the `value`): Qwen2-1.5B shape, int8 weights in blocks of 32 along K with one fp16 scale per
 block (codes uniform in [-127, 127], scales |N(0, 0.002)|), fp16 KV in a sliding window of 1024 positions, a
 3840-token prompt prefilled K/V-only through the engine, then greedy decode at batch 1 -- one step = one token
-through all 28 layers, the LM head and the argmax, run as one captured hipGraph.  Synthetic random-init weights (no
-checkpoints offline); inputs resident in HBM before the timed region.
+through all 28 layers (the persistent one-column kernel), the LM head and the argmax.  Synthetic random-init weights
+(no checkpoints offline); inputs resident in HBM before the timed region.
 
 The JSON line also carries:
   hbm_frac_step  algorithmic bytes per token (packed weights + the KV window read) x tok/s / 8 TB/s
   bs16           the same model decoding 16 sequences at once (16 x 3840-token prompts)
   verify         tree verification on the same model over a 2048-position prefix: one pass over 1 + 32 nodes
                  (8 branches x 4 tokens) plus the acceptance kernel, divided by one decode step at that prefix
-  roofline       the dominant kernel (the SwiGLU gate_up GEMV, the largest launch of the step), HIP-event timed
+  roofline       the dominant kernel (the persistent step's kernel: every layer of the token, ~95% of the step),
+                 HIP-event timed on the engine's stream, with its rocprofv3-measured HBM traffic
   cpu_baseline   the CPU oracle (fp32, dequantised weights) on a bounded sample of the same workload
   latency        per-token latency quantiles with one host synchronisation per token, the decode / draw split of a
                  T > 0 token, and dispatches_per_token (kernels of the recorded step)
@@ -175,23 +176,25 @@ def sampling_cost(eng, V, rows=16, reps=20):
     return res
 
 
-TRAFFIC_FILE = ROOT / 'profiles' / 'k_gemv_q8_gate_up_traffic.md'
-GEMV_SOURCES = ('sp_gemv1.h', 'sp_gemv.h', 'sp_device.h', 'sp_pack.h')
+TRAFFIC_FILE = ROOT / 'profiles' / 'k_decode1_q8_15b_bs1_traffic.md'
+KERNEL_SOURCES = ('sp_decode1.h', 'sp_gemv.h', 'sp_attn.h', 'sp_device.h', 'sp_pack.h')
 
 
-def gemv_source_hash():
-    """First 16 hex digits of the SHA-256 over the GEMV kernel's sources (kernel, device helpers, tile packing)."""
+def kernel_source_hash():
+    """First 16 hex digits of the SHA-256 over the persistent kernel's sources (kernel, GEMV tiles, attention and
+    device helpers, tile packing)."""
     import hashlib
     h = hashlib.sha256()
-    for name in GEMV_SOURCES:
+    for name in KERNEL_SOURCES:
         h.update((ROOT / 'seedplane_amd' / 'csrc' / name).read_bytes())
     return h.hexdigest()[:16]
 
 
 def measured_traffic():
-    """HBM bytes per gate_up launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter
-    scaled by what it reads for a plain copy of known size), and whether it applies: the summary records the hash of
-    the kernel sources it was measured on, and a summary of other sources is reported as stale (traffic null)."""
+    """HBM bytes per persistent-kernel launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each
+    counter scaled by what it reads for a plain copy of known size), and whether it applies: the summary records the
+    hash of the kernel sources it was measured on, and a summary of other sources is reported as stale (traffic
+    null)."""
     fields = {}
     try:
         for line in TRAFFIC_FILE.read_text().splitlines():
@@ -202,7 +205,7 @@ def measured_traffic():
         return None, 'no traffic summary'
     if 'traffic_bytes_per_launch' not in fields:
         return None, 'no traffic summary'
-    if fields.get('kernel_source_sha16') != gemv_source_hash():
+    if fields.get('kernel_source_sha16') != kernel_source_hash():
         return None, 'traffic summary measured on other kernel sources (stale)'
     return int(fields['traffic_bytes_per_launch']), f'{TRAFFIC_FILE.relative_to(ROOT)} (rocprofv3 --pmc, scaled)'
 
@@ -245,36 +248,40 @@ def kernel_frac(name, us, nbytes):
             'achieved_gbs': round(nbytes / (us * 1e-6) / 1e9, 1), 'frac': round(nbytes / (us * 1e-6) / PEAK_HBM, 4)}
 
 
-def gemv_roofline(eng):
-    """The dominant kernel: the SwiGLU gate_up GEMV (the largest launch of the step), launched on the engine's stream
-    cycling through all 28 layers (so its weights stream from HBM as in decode), HIP-event timed there."""
-    from seedplane_amd import _lib
-    us, gbytes = eng.time_gemv(_lib.SP_T_GATE_UP, layer=-1, n_cols=1, iters=280)
-    achieved = gbytes / (us * 1e-6) / 1e9
-    log(f'gate_up GEMV: {us:.2f} us/launch, {achieved:.0f} GB/s')
+def step_roofline(eng, cache, iters=50):
+    """The dominant kernel: the persistent one-column step's kernel (every layer of one token), launched for a
+    decode column of `cache` on the engine's stream, HIP-event timed there.  Algorithmic bytes per launch: all 28
+    layers' int8 codes and fp16 scales, norm weights and qkv bias, the window's K and V, the embedding row."""
+    us, nbytes = eng.time_persistent(cache, iters=iters)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    log(f'persistent step kernel: {us:.2f} us/launch, {nbytes} bytes, {achieved:.0f} GB/s')
     traffic, source = measured_traffic()
     return {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM / 1e9, 'unit': 'GB/s',
             'frac': round(achieved * 1e9 / PEAK_HBM, 4), 'traffic': traffic, 'traffic_source': source,
-            'kernel': 'k_gemv1<Q8, gate+up pair, 3 k-tiles per wave> (SwiGLU gate_up, 17920x1536 int8 + scales, 1 column)',
-            'bytes_per_launch': gbytes, 'avg_launch_us': round(us, 3)}
+            'kernel': 'd1::k_decode1<Q8, head_dim 128> (persistent one-column step: 28 layers of Qwen2-1.5B int8, '
+                      'one block per CU)',
+            'bytes_per_launch': nbytes, 'avg_launch_us': round(us, 3)}
 
 
 def workload_roofline(args, out):
-    """Only the dominant kernel's timing (for counter runs), then a plain 512 MiB copy (torch elementwise multiply
-    by 1.0) whose FETCH_SIZE / WRITE_SIZE give the counters' scale."""
+    """Only the dominant kernel's timing (for counter runs: 51 launches of the persistent kernel at 1100 cached
+    positions, window 1024), then a plain 512 MiB copy (torch elementwise multiply by 1.0) whose FETCH_SIZE /
+    WRITE_SIZE give the counters' scale."""
     import torch
     from seedplane_amd.presets import preset
     from seedplane_amd.qwen_engine import Qwen2Engine
-    from seedplane_amd.synth import make_weights
+    from seedplane_amd.synth import make_weights, random_prompt
     cfg, w = make_weights(preset('qwen2-1.5b'), 'q8', seed=0)
     eng = Qwen2Engine(config=cfg, tensors=w, max_tokens=64)
-    out['roofline'] = gemv_roofline(eng)
+    cache = eng.new_cache(4096, window=args.window)
+    eng.prefill([random_prompt(1100, cfg['vocab_size'], seed=1)], [cache])
+    out['roofline'] = step_roofline(eng, cache)
     src = torch.ones(128 << 20, dtype=torch.float32, device='cuda')
     dst = torch.empty_like(src)
     for _ in range(3):
         torch.mul(src, 1.0, out=dst)
     sync()
-    out.update({'value': out['roofline']['achieved'], 'unit': 'GB/s', 'metric': 'gate_up GEMV HBM GB/s',
+    out.update({'value': out['roofline']['achieved'], 'unit': 'GB/s', 'metric': 'persistent step kernel HBM GB/s',
                 'copy_bytes_each_way': src.numel() * 4})
 
 
@@ -310,7 +317,7 @@ def workload_c3(args, out):
     latency, dispatches = token_latency(eng, cache, toks[0])
     log(f'latency: {latency}, {dispatches} kernels per step')
 
-    roofline = gemv_roofline(eng)
+    roofline = step_roofline(eng, cache)
 
     bs16 = None
     if not args.no_bs16:

@@ -207,6 +207,14 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
 int sp_engine_time_attention(sp_engine *e, int32_t n, const sp_token *toks, int32_t iters, float *avg_us,
                              uint64_t *bytes);
 
+/* Measurement hook (no counterpart in the reference): launch the persistent one-column step's kernel (every layer of
+ * one decode column; no head GEMV, no argmax) for column *tok `iters` times on the engine's stream, timed with HIP
+ * events.  Returns the average launch duration in microseconds and the algorithmic bytes one launch reads: every
+ * layer's packed weights and scales, norm weights and qkv bias, the visible keys' K and V, the embedding row.  The
+ * column must be a plain decode column where the step applies (SP_ESTATE otherwise); its K/V slot is rewritten with
+ * the same values each time.  Clobbers the activation buffers; call between forward passes only. */
+int sp_engine_time_persistent(sp_engine *e, const sp_token *tok, int32_t iters, float *avg_us, uint64_t *bytes);
+
 /* Benchmark utility (no counterpart in the reference): fill slots [first_slot, first_slot + n) of sequence `seq`
  * in every layer's K and V with seeded pseudo-random fp16 values in [-scale, scale], standing in for a long prefill
  * when only the decode step is measured (the step reads the same bytes whatever the values). */

@@ -60,6 +60,8 @@ SIGNATURES = {
     'sp_engine_persistent_status': (c_int, [c_void_p, c_char_p, c_int32]),
     'sp_persistent_geometry': (c_int, [ctypes.POINTER(ModelDesc), c_int32, c_int32, ctypes.POINTER(c_int32)]),
     'sp_engine_last_dispatches': (c_int, [c_void_p]),
+    'sp_engine_time_persistent': (c_int, [c_void_p, ctypes.POINTER(Token), c_int32, ctypes.POINTER(c_float),
+                                          ctypes.POINTER(c_uint64)]),
     'sp_engine_time_attention': (c_int, [c_void_p, c_int32, ctypes.POINTER(Token), c_int32, ctypes.POINTER(c_float),
                                          ctypes.POINTER(c_uint64)]),
     'sp_engine_bytes': (c_int, [c_void_p, ctypes.POINTER(c_uint64), ctypes.POINTER(c_uint64)]),

@@ -568,7 +568,8 @@ struct sp_engine {
     unsigned d1_seq = 0;
     bool d1_plain = false;       // the runtime refused a cooperative launch once: plain launches from then on
     bool prepare_d1();
-    bool run_d1(const sp_token &t, int flags);
+    bool launch_d1(const sp_token &t, int flags);     // the persistent kernel alone
+    bool run_d1(const sp_token &t, int flags);        // + the error word copy, the head GEMV and the argmax
     void check_d1_error();
 
     // attention plan of one forward call: same-sequence column groups (multi-query kernel) or one block row per column
@@ -999,7 +1000,7 @@ bool sp_engine::prepare_d1() {
 // also places one block per CU.  Either way every wait in the kernel is bounded: a grid that is not all resident
 // ends with the error word set, never a hang.  Returns false, with nothing enqueued, if both launches fail (the step
 // is then marked as not applying and the caller runs the chain).
-bool sp_engine::run_d1(const sp_token &t, int flags) {
+bool sp_engine::launch_d1(const sp_token &t, int flags) {
     d1::Step a{};
     a.tok = t;
     a.feed = (flags & SP_F_FEED) ? am_out : nullptr;
@@ -1021,6 +1022,10 @@ bool sp_engine::run_d1(const sp_token &t, int flags) {
         d1_why = std::string("launch refused: ") + hipGetErrorString(le);
         return false;
     }
+    return true;
+}
+bool sp_engine::run_d1(const sp_token &t, int flags) {
+    if (!launch_d1(t, flags)) return false;
     HIPCHK(hipMemcpyAsync(h_d1err, d1_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream));
     const DevMat &hm = d.tied_head ? embed : head;
     launch_gemv(hm, EPI_STORE, xn, d.hidden, 1, logits, nullptr, d.vocab, nullptr, stream);
@@ -1540,6 +1545,47 @@ int sp_engine_time_gemv(sp_engine *e, int32_t kind, int32_t layer, int32_t n_col
         HIPCHK(hipGetLastError());
         *avg_us = ms * 1000.f / iters;
         *bytes = m->bytes;
+    });
+}
+
+int sp_engine_time_persistent(sp_engine *e, const sp_token *tok, int32_t iters, float *avg_us, uint64_t *bytes) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        const sp_model_desc &d = e->d;
+        require(avg_us && bytes && tok, SP_EINVAL, "NULL argument");
+        require(iters >= 1, SP_EINVAL, "iters must be >= 1");
+        require(e->n_seq > 0, SP_ESTATE, "KV cache not reserved");
+        e->check_columns(1, tok, false);
+        const sp_token &t = *tok;
+        require(t.tree_count == 0 && t.ctx_hi >= t.ctx_lo && t.slot == t.ctx_hi % e->n_slots, SP_EINVAL,
+                "not a plain decode column");
+        require(e->prepare_d1(), SP_ESTATE, "the persistent step does not apply: " + e->d1_why);
+        hipEvent_t a, b;
+        HIPCHK(hipEventCreate(&a));
+        HIPCHK(hipEventCreate(&b));
+        require(e->launch_d1(t, 0), SP_ESTATE, "persistent launch refused: " + e->d1_why);      // warm-up
+        HIPCHK(hipEventRecord(a, e->stream));
+        for (int i = 0; i < iters; ++i) require(e->launch_d1(t, 0), SP_ESTATE, "persistent launch refused: " + e->d1_why);
+        HIPCHK(hipEventRecord(b, e->stream));
+        HIPCHK(hipEventSynchronize(b));
+        float ms = 0.f;
+        HIPCHK(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        HIPCHK(hipMemcpy(e->h_d1err, e->d1_err, sizeof(unsigned), hipMemcpyDeviceToHost));
+        e->check_d1_error();
+        *avg_us = ms * 1000.f / iters;
+        // algorithmic bytes: every layer's packed weights (codes + scales), norms and qkv bias, the visible K / V
+        // of each kv head (the new key and value are written, the others read), and the embedding row
+        uint64_t nb = 0;
+        const int vis = t.ctx_hi - t.ctx_lo + 1;
+        for (const auto &ly : e->layers) {
+            nb += ly.qkv.bytes + ly.o.bytes + ly.gate_up.bytes + ly.down.bytes;
+            nb += (uint64_t)(2 * d.hidden + e->Nqkv) * sizeof(float);
+            nb += (uint64_t)2 * d.n_kv_heads * vis * d.head_dim * sizeof(f16);
+        }
+        nb += (uint64_t)d.hidden * (e->embed.bytes / ((uint64_t)d.vocab * d.hidden) + 1);
+        *bytes = nb;
     });
 }
 

@@ -201,6 +201,16 @@ class Qwen2Engine:
                    self.h)
         return us.value, nb.value
 
+    def time_persistent(self, cache, iters=50):
+        """Average duration (us) and algorithmic bytes of one launch of the persistent one-column step's kernel for a
+        decode column of `cache` at its current length (every layer; no head, no argmax), timed with HIP events on
+        the engine's stream.  Clobbers activation buffers; the column's K/V slot is rewritten with the same values."""
+        col = _lib.Token(*self._column(0, cache, cache.length, cache.length))
+        us, nb = ctypes.c_float(), ctypes.c_uint64()
+        _lib.check(self.lib.sp_engine_time_persistent(self.h, ctypes.byref(col), iters, ctypes.byref(us),
+                                                      ctypes.byref(nb)), self.h)
+        return us.value, nb.value
+
     def time_attention(self, caches, iters=100):
         """Average duration (us) and K/V bytes of one launch of the attention kernel a decode step of `caches` (one
         column each, at their current lengths) runs, timed with HIP events on the engine's stream.  Clobbers
