@@ -266,7 +266,8 @@ int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_d
 
 /* Replaces the T > 0 branch of Qwen2Engine.sample (qwen_engine.py:149-156, torch.multinomial) and the native
  * Sampler::draw inverse CDF (native/vulkan_decode/sampler.hpp:93-97) with seeded uniforms: out_dev[s] = the first
- * index whose cumulative softmax mass of row row_dev[s] exceeds u_dev[s] * total.  All pointers are device memory. */
+ * index whose cumulative softmax mass of row row_dev[s] exceeds u_dev[s] * total.  All pointers are device memory.
+ * Each draw runs on many blocks through a per-device scratch area: calls on one device must not overlap. */
 int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32_t *row_dev, const double *u_dev,
                  int32_t n, double temperature, int32_t *out_dev, void *hip_stream);
 

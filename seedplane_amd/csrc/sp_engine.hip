@@ -1815,9 +1815,34 @@ int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32
         require(logits_dev && row_dev && u_dev && out_dev, SP_EINVAL, "NULL pointer");
         require(vocab >= 1 && ld >= vocab && n >= 1 && n <= 65535, SP_EINVAL, "bad sizes");
         require(temperature > 0.0, SP_EINVAL, "temperature must be positive");
-        hipLaunchKernelGGL(k_sample, dim3(n), dim3(SMP_THREADS), 0, (hipStream_t)stream, logits_dev, vocab, ld, row_dev,
-                           u_dev, 1.0 / temperature, out_dev);
-        HIPCHK(hipGetLastError());
+        hipStream_t st = (hipStream_t)stream;
+        // partial maxima and chunk sums of SMP_BATCH draws, one set per device (calls on one device must not overlap)
+        constexpr int SMP_BATCH = 512;
+        struct SmpScratch { float *pmax; double *csum; };
+        static std::map<int, SmpScratch> scratch_of;
+        static std::mutex mu;
+        int dev = 0;
+        HIPCHK(hipGetDevice(&dev));
+        SmpScratch sc;
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            auto it = scratch_of.find(dev);
+            if (it == scratch_of.end())
+                it = scratch_of.emplace(dev, SmpScratch{dev_alloc<float>((size_t)SMP_BATCH * SMX_BLOCKS),
+                                                        dev_alloc<double>((size_t)SMP_BATCH * SMP_THREADS)}).first;
+            sc = it->second;
+        }
+        const double invT = 1.0 / temperature;
+        for (int r0 = 0; r0 < n; r0 += SMP_BATCH) {
+            const int nr = std::min(SMP_BATCH, n - r0);
+            hipLaunchKernelGGL(k_smp_max, dim3(SMX_BLOCKS, nr), dim3(SMS_T), 0, st, logits_dev, vocab, ld, row_dev + r0,
+                               sc.pmax);
+            hipLaunchKernelGGL(k_smp_sum, dim3(SMP_THREADS / SMS_CPB, nr), dim3(SMS_T), 0, st, logits_dev, vocab, ld,
+                               row_dev + r0, invT, (const float *)sc.pmax, sc.csum);
+            hipLaunchKernelGGL(k_smp_draw, dim3(nr), dim3(SMS_T), 0, st, logits_dev, vocab, ld, row_dev + r0, u_dev + r0,
+                               invT, (const float *)sc.pmax, (const double *)sc.csum, out_dev + r0);
+            HIPCHK(hipGetLastError());
+        }
     });
 }
 

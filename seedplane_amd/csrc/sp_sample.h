@@ -16,129 +16,143 @@
 #pragma once
 #include "sp_device.h"
 
-constexpr int SMP_THREADS = 1024;
+constexpr int SMP_THREADS = 1024;      // chunks per row
 
-__device__ __forceinline__ double block_sum_d(double v, double *red) {
-    // fixed-order: lanes -> waves (butterfly, deterministic for a fixed input) -> sequential over waves
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SP_WAVE);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    double t = 0.0;
-    for (int j = 0; j < (int)(blockDim.x >> 6); ++j) t += red[j];
-    return t;
+// Seeded draws on many blocks per row, three launches, in the summation order stated at the top of this file:
+//   k_smp_max   SMX_BLOCKS blocks per draw: partial maxima of the row (a maximum is exact in any order);
+//   k_smp_sum   SMP_THREADS / SMS_CPB blocks per draw: the row maximum m from the partial maxima, then the sums of
+//               SMS_CPB chunks: the block's threads compute the weights exp((l_i - m) / T) of a window of entries into
+//               LDS, and one thread per chunk adds its chunk's entries of the window in index order, carrying the
+//               chunk's running sum from window to window (the same additions as one thread summing its chunk);
+//   k_smp_draw  one block per draw: thread 0 adds the chunk sums in chunk order (the total and the exclusive
+//               prefixes), the chunk holding target = u * total is found, and its entries are scanned in index order
+//               (weights computed by the block a window at a time, running sum by thread 0).
+// Every total, prefix and comparison is that order's, so a sequential evaluation reproduces every draw bit for bit;
+// the fallbacks: a chunk with no running sum above the target gives its last positive-weight index, no positive
+// weight where the target fell gives the last positive-weight index of the row (0 if none).
+// Scratch per draw: SMX_BLOCKS floats and SMP_THREADS doubles.
+constexpr int SMX_BLOCKS = 16, SMS_CPB = 8, SMS_T = 256, SMS_WIN = 2048;
+
+__device__ __forceinline__ double smp_weight(const float *l, int i, float m, double invT) {
+    return exp(((double)l[i] - (double)m) * invT);
 }
 
-__device__ __forceinline__ float block_max_f(float v, float *red) {
-    v = wave_max(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = red[0];
-    for (int j = 1; j < (int)(blockDim.x >> 6); ++j) t = fmaxf(t, red[j]);
-    return t;
+__device__ __forceinline__ float smp_row_max(const float *pmax) {
+    float m = pmax[0];
+    for (int j = 1; j < SMX_BLOCKS; ++j) m = fmaxf(m, pmax[j]);
+    return m;
 }
 
-// Per-block scratch for the chunked sums.
-struct SmpShared {
-    double chunk[SMP_THREADS];   // chunk sums, then exclusive prefixes
-    double red[16];
-    float redf[16];
-    double total;
-    int found;
-};
-
-// Weight of entry i for the distribution being scanned.
-//   mode 0: exp((l[i] - m) * invT)                         (unnormalised softmax of `l`)
-//   mode 1: r[i]                                           (explicit fp64 weights, the residual)
-struct Dist {
-    int mode;
-    const float *l;
-    float m;
-    double invT;
-    const double *r;
-    __device__ __forceinline__ double w(int i) const {
-        return mode == 0 ? exp(((double)l[i] - (double)m) * invT) : r[i];
-    }
-};
-
-// Z = sum of weights in the fixed chunk order; leaves the chunk sums in sh.chunk.
-__device__ double dist_total(const Dist &d, int V, SmpShared &sh) {
-    const int C = (V + SMP_THREADS - 1) / SMP_THREADS;
-    const int lo = threadIdx.x * C, hi = min(V, lo + C);
-    double s = 0.0;
-    for (int i = lo; i < hi; ++i) s += d.w(i);
-    sh.chunk[threadIdx.x] = s;
+__global__ void __launch_bounds__(SMS_T) k_smp_max(const float *logits, int V, int ld, const int *rows, float *pmax) {
+    __shared__ float red[SMS_T / 64];
+    const int s = blockIdx.y, bk = blockIdx.x;
+    const float *l = logits + (size_t)rows[s] * ld;
+    const int per = (V + SMX_BLOCKS - 1) / SMX_BLOCKS;
+    const int lo = bk * per, hi = min(V, lo + per);
+    float m = -INFINITY;
+    for (int i = lo + (int)threadIdx.x; i < hi; i += SMS_T) m = fmaxf(m, l[i]);
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     if (threadIdx.x == 0) {
-        double t = 0.0;
-        for (int j = 0; j < SMP_THREADS; ++j) t += sh.chunk[j];
-        sh.total = t;
+        float t = red[0];
+        for (int j = 1; j < SMS_T / 64; ++j) t = fmaxf(t, red[j]);
+        pmax[s * SMX_BLOCKS + bk] = t;
     }
-    __syncthreads();
-    return sh.total;
 }
 
-// Inverse-CDF draw with target = u * Z (call right after dist_total with the same distribution): the chunk t with
-// P_t <= target < P_{t+1} (exclusive prefixes P, the last chunk open above) is scanned from zero against
-// target - P_t; the first index whose running sum exceeds it is drawn.  If rounding leaves no such index, the last
-// positive-weight index of that chunk is drawn, or else the last positive-weight index of the row.
-__device__ int dist_draw(const Dist &d, int V, double u, SmpShared &sh) {
+__global__ void __launch_bounds__(SMS_T) k_smp_sum(const float *logits, int V, int ld, const int *rows, double invT,
+                                                    const float *pmax, double *csum) {
+    __shared__ double w[SMS_WIN];
+    const int s = blockIdx.y;
+    const float *l = logits + (size_t)rows[s] * ld;
+    const float m = smp_row_max(pmax + s * SMX_BLOCKS);
     const int C = (V + SMP_THREADS - 1) / SMP_THREADS;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double p = 0.0;
-        for (int j = 0; j < SMP_THREADS; ++j) { const double s = sh.chunk[j]; sh.chunk[j] = p; p += s; }
-        sh.found = 0x7fffffff;
-    }
-    __syncthreads();
-    const double target = u * sh.total;
+    const int c0 = blockIdx.x * SMS_CPB;
+    const int lo = min(V, c0 * C), hi = min(V, (c0 + SMS_CPB) * C);
     const int t = threadIdx.x;
-    const int lo = t * C, hi = min(V, lo + C);
-    const double start = sh.chunk[t];
-    const bool last = t + 1 == SMP_THREADS;
-    if (target >= start && (last || target < sh.chunk[t + 1])) {
-        const double tl = target - start;
+    // thread t < SMS_CPB owns chunk c0 + t: entries [clo, chi)
+    const int clo = min(V, (c0 + t) * C), chi = min(V, (c0 + t + 1) * C);
+    double acc = 0.0;
+    for (int wlo = lo; wlo < hi; wlo += SMS_WIN) {
+        const int whi = min(hi, wlo + SMS_WIN);
+        for (int i = wlo + t; i < whi; i += SMS_T) w[i - wlo] = smp_weight(l, i, m, invT);
+        __syncthreads();
+        if (t < SMS_CPB) {
+            const int a = max(clo, wlo), e = min(chi, whi);
+            for (int i = a; i < e; ++i) acc += w[i - wlo];
+        }
+        __syncthreads();
+    }
+    if (t < SMS_CPB) csum[(size_t)s * SMP_THREADS + c0 + t] = acc;
+}
+
+__global__ void __launch_bounds__(SMS_T) k_smp_draw(const float *logits, int V, int ld, const int *rows,
+                                                     const double *u, double invT, const float *pmax,
+                                                     const double *csum, int *out) {
+    __shared__ double pre[SMP_THREADS + 1];
+    __shared__ double w[SMS_WIN];
+    __shared__ int sel, found;
+    __shared__ int last[SMS_T / 64];
+    const int s = blockIdx.x, t = threadIdx.x;
+    const float *l = logits + (size_t)rows[s] * ld;
+    const float m = smp_row_max(pmax + s * SMX_BLOCKS);
+    const int C = (V + SMP_THREADS - 1) / SMP_THREADS;
+    for (int j = t; j < SMP_THREADS; j += SMS_T) pre[j] = csum[(size_t)s * SMP_THREADS + j];
+    if (t == 0) { sel = -1; found = -1; }
+    __syncthreads();
+    if (t == 0) {
+        double p = 0.0;
+        for (int j = 0; j < SMP_THREADS; ++j) { const double c = pre[j]; pre[j] = p; p += c; }
+        pre[SMP_THREADS] = p;
+    }
+    __syncthreads();
+    const double target = u[s] * pre[SMP_THREADS];
+    for (int j = t; j < SMP_THREADS; j += SMS_T)
+        if (target >= pre[j] && (j + 1 == SMP_THREADS || target < pre[j + 1])) sel = j;
+    __syncthreads();
+    if (sel >= 0) {
+        // scan chunk sel from zero against target - prefix: the first index whose running sum exceeds it, else the
+        // chunk's last positive-weight index
+        const int clo = min(V, sel * C), chi = min(V, sel * C + C);
+        const double tl = target - pre[sel];
         double acc = 0.0;
         int pick = -1, lastpos = -1;
-        for (int i = lo; i < hi; ++i) {
-            const double wi = d.w(i);
-            if (wi > 0.0) lastpos = i;
-            acc += wi;
-            if (acc > tl) { pick = i; break; }
+        for (int wlo = clo; wlo < chi; wlo += SMS_WIN) {
+            const int whi = min(chi, wlo + SMS_WIN);
+            for (int i = wlo + t; i < whi; i += SMS_T) w[i - wlo] = smp_weight(l, i, m, invT);
+            __syncthreads();
+            if (t == 0 && pick < 0) {
+                for (int i = wlo; i < whi; ++i) {
+                    const double wi = w[i - wlo];
+                    if (wi > 0.0) lastpos = i;
+                    acc += wi;
+                    if (acc > tl) { pick = i; break; }
+                }
+                found = pick;
+            }
+            __syncthreads();
+            if (found >= 0) break;
         }
-        if (pick < 0) pick = lastpos;
-        if (pick >= 0) atomicMin(&sh.found, pick);
-    }
-    __syncthreads();
-    if (sh.found == 0x7fffffff) {
+        if (t == 0 && pick < 0) found = lastpos;
         __syncthreads();
-        if (threadIdx.x == 0) {
-            int tok = V - 1;
-            while (tok > 0 && !(d.w(tok) > 0.0)) --tok;
-            sh.found = tok;
+    }
+    if (found < 0) {
+        // no positive weight where the target fell: the last positive-weight index of the row (0 if none)
+        int best = 0;
+        for (int i = t; i < V; i += SMS_T)
+            if (smp_weight(l, i, m, invT) > 0.0) best = max(best, i);
+        for (int o = 32; o > 0; o >>= 1) best = max(best, __shfl_xor(best, o, SP_WAVE));
+        if ((t & 63) == 0) last[t >> 6] = best;
+        __syncthreads();
+        if (t == 0) {
+            int b = last[0];
+            for (int j = 1; j < SMS_T / 64; ++j) b = max(b, last[j]);
+            found = b;
         }
         __syncthreads();
     }
-    return sh.found;
-}
-
-__device__ float row_max(const float *l, int V, SmpShared &sh) {
-    float m = -INFINITY;
-    for (int i = threadIdx.x; i < V; i += blockDim.x) m = fmaxf(m, l[i]);
-    return block_max_f(m, sh.redf);
-}
-
-// One block per sample s: out[s] = inverse-CDF draw from softmax(logits[rows[s]] / T) with uniform u[s].
-__global__ void __launch_bounds__(SMP_THREADS) k_sample(const float *logits, int V, int ld, const int *rows,
-                                                         const double *u, double invT, int *out) {
-    __shared__ SmpShared sh;
-    const int s = blockIdx.x;
-    const float *l = logits + (size_t)rows[s] * ld;
-    Dist d{0, l, row_max(l, V, sh), invT, nullptr};
-    dist_total(d, V, sh);
-    const int tok = dist_draw(d, V, u[s], sh);
-    if (threadIdx.x == 0) out[s] = tok;
+    if (t == 0) out[s] = found;
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -42,6 +42,39 @@ def test_sample_matches_oracle(gpu_device, V, T):
         assert got[s] == tok, (s, r)
 
 
+@pytest.mark.parametrize('V,n,T', [(300000, 600, 0.7), (2200000, 3, 1.0)])
+def test_sample_windows_and_batches(gpu_device, V, n, T):
+    """More draws than one launch sequence takes (512), chunks longer than a sum block's LDS window (V = 300000: 8
+    chunks of 293 entries per block), a chunk longer than the draw's scan window (V = 2200000: 2149 entries)."""
+    print(f'sample V={V} n={n} T={T}', flush=True)
+    g = torch.Generator().manual_seed(V + n)
+    logits = torch.randn(4, V, generator=g) * 2
+    rows = [int(r) for r in torch.randint(0, 4, (n,), generator=g)]
+    u = sref.uniforms(7, V, n)
+    got = sample_rows(_lib.load(), logits.to(gpu_device), rows, u, T)
+    w = [sref.softmax_weights(logits[r].numpy(), T) for r in range(4)]
+    for s, r in enumerate(rows):
+        tok, margin = sref.draw(w[r], u[s])
+        assert margin > MARGIN
+        assert got[s] == tok, (s, r)
+
+
+def test_sample_zero_weight_chunks(gpu_device):
+    """A row whose weights underflow to zero everywhere but one spike (every chunk before it sums to zero, every
+    prefix after it is the total), and a row of equal logits (every entry drawable)."""
+    V = 151936
+    logits = torch.zeros(2, V)
+    logits[0, 123457] = 50.0
+    u = [0.0, 0.25, 0.999999, 0.5, 0.0, 0.3, 0.7, 0.999]
+    rows = [0, 0, 0, 0, 1, 1, 1, 1]
+    got = sample_rows(_lib.load(), logits.to(gpu_device), rows, u, 0.05)
+    assert got[:4] == [123457] * 4
+    w1 = sref.softmax_weights(logits[1].numpy(), 0.05)
+    for s in range(4, 8):
+        assert got[s] == sref.draw(w1, u[s])[0]
+    assert got[4] == 0
+
+
 def _random_case(rng, V, n_branches=8, depth=4, noise=0.3):
     branches = [[int(rng.integers(0, min(V, 6))) if rng.random() < 0.5 else int(rng.integers(0, V))
                  for _ in range(depth)] for _ in range(n_branches)]
