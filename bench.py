@@ -448,25 +448,72 @@ def run_c5(steps=128):
 
 def run_spec(target, cfg, drafter_engine, steps=32):
     """The full speculative loop: target 1.5B int8, drafter 0.5B fp16, 8 branches x 4 tokens, T = 0.8, seeded
-    uniforms, over a 2048-token prompt (prefill outside the timing).  Random-init models are unrelated, so few
-    drafts are accepted; the figure is the cost of a step, not a speedup."""
+    uniforms, over a 2048-token prompt; both models' prefills run before the timed steps.  Random-init models are
+    unrelated, so few drafts are accepted; the figure is the cost of a step, not a speedup.
+    budget: the parts of a step timed alone, each call followed by a synchronisation -- the drafter's root pass (one
+    column), one drafter level (8 tree columns over the 24-node draft tree), the target's verify step (the 33-node
+    pass + the acceptance walk) -- and budget_ms = root + 3 levels + verify step + 0.3 ms, against ms_per_step."""
+    import numpy as np
+    import torch
     from seedplane_amd import _lib
-    from seedplane_amd.speculative import SpecStats, TreeDrafter, speculative_generate
+    from seedplane_amd.speculative import SpecStats, SpeculativeLoop, TreeDrafter, TreeVerifier, flatten, uniforms
     from seedplane_amd.synth import random_prompt
     drafter = TreeDrafter(drafter_engine)
     prompt = random_prompt(2048, cfg['vocab_size'], seed=9)
+    warm = SpeculativeLoop(target, drafter, prompt, seed=0, capacity=len(prompt) + 64)
+    for _ in range(2):
+        warm.step()
+    del warm
     stats = SpecStats()
-    speculative_generate(target, drafter, prompt, steps=2, seed=0)
+    loop = SpeculativeLoop(target, drafter, prompt, seed=1, stats=stats, capacity=len(prompt) + 5 * steps + 128)
     sync()
     t0 = time.perf_counter()
-    toks = speculative_generate(target, drafter, prompt, steps=steps, seed=1, stats=stats)
+    toks = []
+    for _ in range(steps):
+        toks += loop.step()
     sync()
     dt = time.perf_counter() - t0
+
+    def alone(fn, reps=20):
+        fn()
+        sync()
+        t = time.perf_counter()
+        for _ in range(reps):
+            fn()
+            sync()
+        return (time.perf_counter() - t) / reps * 1e3
+    dc, tc, tok = loop.dcache, loop.tcache, loop.committed[-1]
+
+    def root():
+        drafter_engine.forward([tok], dc)
+        dc.length -= 1
+    L, S = dc.length, drafter_engine._pool_slots
+    cols = [(5 + b, dc.seq, L + 2, (L + 16 + b) % S, 0, L - 1, L % S, 24,       # level 3 of the draft tree
+             (1 << b) | (1 << (8 + b)) | (1 << (16 + b))) for b in range(8)]
+    lout = torch.empty((8, drafter_engine.vocab), dtype=torch.float32, device=drafter_engine.device)
+    rng = np.random.default_rng(0)
+    tree = flatten(tok, [list(rng.integers(0, cfg['vocab_size'], 4)) for _ in range(8)])
+    verifier = TreeVerifier(target)
+    p = verifier.forward(tc, tree, ids=False)
+    g = torch.Generator(device=p.device).manual_seed(0)
+    q = p + 0.3 * torch.randn(p.shape, generator=g, device=p.device)
+    u = uniforms(3, 0, 64)
+
+    def verify_step():
+        pp = verifier.forward(tc, tree, ids=False)
+        verifier.accept(pp, q, tree, u, 0.8)
+    root_ms = alone(root)
+    level_ms = alone(lambda: drafter_engine.run(cols, _lib.SP_F_LOGITS, logits_out=lout))
+    verify_ms = alone(verify_step)
+    budget = root_ms + 3 * level_ms + verify_ms + 0.3
     us, nb = target.time_gemv(_lib.SP_T_GATE_UP, layer=-1, n_cols=33, iters=140)
     return {'workload': 'target Qwen2-1.5B int8, drafter Qwen2-0.5B fp16, 8 branches x 4, T 0.8, 2048-token prompt',
             'tok_s': round(len(toks) / dt, 2), 'ms_per_step': round(dt / steps * 1e3, 3), 'steps': steps,
             'accepted_per_step': round(stats.accepted / stats.steps, 3),
             'emitted_per_step': round(stats.emitted / stats.steps, 3),
+            'budget': {'drafter_root_ms': round(root_ms, 3), 'drafter_level_ms': round(level_ms, 3),
+                       'verify_step_ms': round(verify_ms, 3), 'budget_ms': round(budget, 3),
+                       'step_within_budget': dt / steps * 1e3 <= budget},
             'dominant_kernel': kernel_frac('k_gemv<Q8, 3 m-tiles, gate+up pair> 33 columns (tree pass)', us, nb)}
 
 
@@ -503,7 +550,8 @@ def workload_spec(args, out):
                 'steps': 64, 'warmup': 2, 'ms_per_step': r['ms_per_step'], 'higher_is_better': True,
                 'dtype': 'target int8 / drafter fp16, fp32 logits, fp64 acceptance',
                 'data': 'synthetic random-init target and drafter (acceptance is near zero for unrelated models)',
-                'config': {'workload': r['workload']}, **{k: r[k] for k in ('accepted_per_step', 'emitted_per_step')}})
+                'config': {'workload': r['workload']},
+                **{k: r[k] for k in ('accepted_per_step', 'emitted_per_step', 'budget')}})
 
 
 def workload_sampling(args, out):

@@ -69,7 +69,9 @@ enum {
     SP_F_FEED = 32,       /* column b's token is the argmax id of column b of the last SP_F_ARGMAX   */
                           /* call (on the device; the token field is ignored), so a greedy loop     */
                           /* needs no host round trip per step                                       */
-    SP_F_CHAIN = 64       /* run the kernel chain even where the persistent one-column step applies  */
+    SP_F_CHAIN = 64,      /* run the kernel chain even where the persistent one-column step applies  */
+    SP_F_DEVCOLS = 128    /* column b's token (and tree mask) come from the device arrays set by      */
+                          /* sp_engine_set_device_columns, read when the step runs (always the chain) */
 };
 
 typedef struct sp_model_desc {
@@ -143,6 +145,15 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
  * 0 = the kernel chain, 1 = the persistent one-column step (one kernel launch for every layer, then the head
  * GEMV and the argmax), -1 = none yet. */
 int sp_engine_last_path(const sp_engine *e);
+
+/* Device-side columns (no counterpart in the reference, whose speculative forest is built from host token lists,
+ * seedplane/speculative.py:19-38; the drafter uses it to run its levels without reading tokens back).  For calls
+ * with SP_F_DEVCOLS: tokens_dev[b]
+ * replaces column b's token (clamped to [0, vocab)) and, when masks_dev is not NULL, masks_dev[b] its tree_mask; the
+ * arrays are read on the engine's stream when the step runs, so a kernel queued before the call may write them.
+ * The host records still give every other field (positions, slots, ranges, tree block).  Pointers stay set until the
+ * next call of this function; tokens_dev NULL clears them. */
+int sp_engine_set_device_columns(sp_engine *e, const int32_t *tokens_dev, const uint64_t *masks_dev);
 
 /* Introspection (no counterpart in the reference; the reference records its whole one-token step once and submits
  * it once per token, native/vulkan_decode/qwen_vk.cpp:372-412): 1 when a plain decode column (one column, no tree
@@ -314,6 +325,34 @@ int sp_op_accept_tree_host(const float *p_logits_dev, const float *q_logits_dev,
                            int32_t n_nodes, const int32_t *token, const int32_t *trial_start, const int32_t *n_trials,
                            const int32_t *trials, int32_t n_trials_total, const double *u, int32_t n_u,
                            double temperature, int32_t max_depth, int32_t *out_dev, void *hip_stream, int32_t *out_host);
+
+/* sp_op_accept_tree_host with the drafter's rows given by index (no counterpart in the reference; it replaces a
+ * gather of the drafter rows into node order): node i's drafter logits are row q_row[i] (host array [n_nodes], each
+ * < n_q_rows for a node with trials; leaves' entries are not read) of q_logits_dev [n_q_rows][ld].  Same decision
+ * rule, limits, outputs and errors. */
+int sp_op_accept_tree_rows(const float *p_logits_dev, const float *q_logits_dev, int32_t n_q_rows, int32_t vocab,
+                           int32_t ld, int32_t n_nodes, const int32_t *token, const int32_t *trial_start,
+                           const int32_t *n_trials, const int32_t *trials, int32_t n_trials_total,
+                           const int32_t *q_row, const double *u, int32_t n_u, double temperature, int32_t max_depth,
+                           int32_t *out_dev, void *hip_stream, int32_t *out_host);
+
+/* Library teardown (no counterpart in the reference): frees what the sampling and acceptance entry points keep per
+ * device (draw and histogram scratch, the walk's exchange words, its pinned result and staging blocks and their
+ * event) after waiting for each such device's work; a later call of those entry points creates them again.  Engines
+ * are not touched (sp_engine_destroy frees an engine).  The Python layer calls it at interpreter exit, after the
+ * engines' own finalizers, so no HIP object of the library is left for the HIP runtime's own teardown.  Must not
+ * overlap a call of the entry points it serves. */
+int sp_library_release(void);
+
+/* One level of a drafter's proposal on the device (no counterpart in the reference; with SP_F_DEVCOLS it lets a
+ * drafter run its levels without reading tokens back).  tokens_dev [levels][n_branches]: the tokens drawn so far,
+ * level-major.  For `level`, canon_dev[level][b] = the first branch whose tokens at levels 0..level equal branch b's
+ * (the branch whose row every branch through that tree node draws from); masks_dev[b] = the tree mask of column b of
+ * that level (bit l' * n_branches + canon_dev[l'][b] for every earlier level l', and bit level * n_branches + b);
+ * rows_dev[b] = canon_dev[level][b].  canon_dev rows of earlier levels must hold this function's earlier results.
+ * Requires n_branches * (level + 1) <= 64.  All pointers are device memory; one small launch on hip_stream. */
+int sp_op_draft_link(const int32_t *tokens_dev, int32_t n_branches, int32_t level, int32_t *canon_dev,
+                     uint64_t *masks_dev, int32_t *rows_dev, void *hip_stream);
 
 #ifdef __cplusplus
 }

@@ -3,6 +3,7 @@
 The shared library is built in-tree (seedplane_amd/build.py) and loaded from this package directory only.  There is
 no fallback: if the library is missing or a call fails, an exception is raised.
 """
+import atexit
 import ctypes
 
 import numpy as np
@@ -17,6 +18,7 @@ SP_FMT_F32, SP_FMT_F16, SP_FMT_Q8, SP_FMT_Q4 = range(4)
 (SP_T_EMBED, SP_T_HEAD, SP_T_FINAL_NORM, SP_T_IN_NORM, SP_T_POST_NORM, SP_T_QKV, SP_T_QKV_BIAS, SP_T_O,
  SP_T_GATE_UP, SP_T_DOWN) = range(10)
 SP_F_LOGITS, SP_F_ARGMAX, SP_F_GRAPH, SP_F_PERSISTENT, SP_F_UNFUSED, SP_F_FEED, SP_F_CHAIN = 1, 2, 4, 8, 16, 32, 64
+SP_F_DEVCOLS = 128
 
 # Every function the header declares, with its ctypes signature.
 c_int, c_int32, c_size_t, c_uint64, c_float = ctypes.c_int, ctypes.c_int32, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float
@@ -89,6 +91,12 @@ SIGNATURES = {
     'sp_op_accept_tree_host': (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int32, c_void_p, c_int32, ctypes.c_double, c_int32, c_void_p,
                                        c_void_p, c_void_p]),
+    'sp_op_accept_tree_rows': (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int32, ctypes.c_double,
+                                       c_int32, c_void_p, c_void_p, c_void_p]),
+    'sp_op_draft_link': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
+    'sp_engine_set_device_columns': (c_int, [c_void_p, c_void_p, c_void_p]),
+    'sp_library_release': (c_int, []),
 }
 
 _lib = None
@@ -108,7 +116,15 @@ def load():
         fn.restype = res
         fn.argtypes = args
     _lib = lib
+    atexit.register(_release_at_exit)
     return lib
+
+
+def _release_at_exit():
+    """Free the library's per-device scratch (sp_library_release) at interpreter exit, while the HIP runtime is
+    still whole: its own teardown runs later, in the C exit handlers.  Engines are freed by their finalizers."""
+    if _lib is not None:
+        _lib.sp_library_release()
 
 
 class SeedPlaneError(RuntimeError):

@@ -12,6 +12,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <set>
 #include <mutex>
 #include <tuple>
 #include <type_traits>
@@ -463,6 +464,15 @@ void launch_attn_dec(int HD, int kpb, dim3 grid, hipStream_t st, const AttnArgs 
     else launch_attn_dec_hd<128>(kpb, grid, st, aa, out, ldo, direct, mtp);
 }
 
+// SP_F_DEVCOLS: the uploaded column records take their tokens (clamped to the vocabulary, as a fed token is) and,
+// when given, their tree masks from device arrays, on the stream ahead of the step.
+__global__ void k_patch_columns(sp_token *t, int n, const int32_t *tokens, const uint64_t *masks, int vocab) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    t[i].token = min(max(tokens[i], 0), vocab - 1);
+    if (masks) t[i].tree_mask = masks[i];
+}
+
 template <int FMT>
 void launch_embed(const DevMat &m, const sp_token *toks, int n, int H, float *x, hipStream_t st, const int *feed,
                   int vocab, const float *inv_freq, int half, float2 *rtab) {
@@ -538,6 +548,9 @@ struct sp_engine {
     size_t upload_bytes = 0;
     hipEvent_t upload_done = nullptr;
     int *h_ids = nullptr;        // pinned landing buffer of the greedy ids a call returns to the host
+    // SP_F_DEVCOLS: device arrays the columns' tokens and tree masks are read from (sp_engine_set_device_columns)
+    const int32_t *dev_tokens = nullptr;
+    const uint64_t *dev_masks = nullptr;
 
     // KV ring
     int n_seq = 0, n_slots = 0;
@@ -1294,16 +1307,18 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
                     "a layer's weights are not loaded");
         require(!(argmax_host && !(flags & SP_F_ARGMAX)), SP_EINVAL, "argmax_host needs SP_F_ARGMAX");
         require(!((flags & SP_F_ARGMAX) && !(flags & SP_F_LOGITS)), SP_EINVAL, "SP_F_ARGMAX needs SP_F_LOGITS");
-        const bool feed = flags & SP_F_FEED;
+        const bool feed = flags & SP_F_FEED, devcols = flags & SP_F_DEVCOLS;
+        require(!(devcols && feed), SP_EINVAL, "SP_F_DEVCOLS and SP_F_FEED both name the tokens");
+        require(!devcols || e->dev_tokens, SP_ESTATE, "SP_F_DEVCOLS needs sp_engine_set_device_columns");
         require(!feed || n <= e->argmax_cols, SP_ESTATE,
                 "SP_F_FEED needs a previous SP_F_ARGMAX call over at least as many columns");
-        e->check_columns(n, toks, feed);
+        e->check_columns(n, toks, feed || devcols);
         e->check_d1_error();
         const bool use_graph = flags & SP_F_GRAPH;
         const int sflags = flags & (SP_F_LOGITS | SP_F_ARGMAX | SP_F_UNFUSED | SP_F_FEED);
         // one plain decode column: the persistent step, where the shape and the pool allow it
         const sp_token &t0 = toks[0];
-        if (n == 1 && (flags & SP_F_LOGITS) && !(flags & (SP_F_UNFUSED | SP_F_CHAIN)) && t0.tree_count == 0 &&
+        if (n == 1 && (flags & SP_F_LOGITS) && !(flags & (SP_F_UNFUSED | SP_F_CHAIN | SP_F_DEVCOLS)) && t0.tree_count == 0 &&
             t0.ctx_hi >= t0.ctx_lo && t0.slot == t0.ctx_hi % e->n_slots && e->prepare_d1() && e->run_d1(t0, sflags)) {
             e->last_path = 1;
             e->last_dispatches = (sflags & SP_F_ARGMAX) ? 4 : 2;
@@ -1321,6 +1336,11 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
         e->last_path = 0;
         const sp_engine::AttnPlan ap = e->plan_attention(n, toks, use_graph);
         e->upload(n, toks, ap);
+        if (devcols) {
+            hipLaunchKernelGGL(k_patch_columns, dim3((n + 63) / 64), dim3(64), 0, e->stream, e->dtoks, n, e->dev_tokens,
+                               e->dev_masks, d.vocab);
+            HIPCHK(hipGetLastError());
+        }
         if (use_graph) {
             // The step's three parts (the embedding and layer 0, layers 1-4, the rest) are recorded as graphs once per
             // (columns, flags, attention plan); their kernel nodes are the reported dispatch count.  The first part
@@ -1401,6 +1421,15 @@ int sp_engine_forward(sp_engine *e, int32_t n, const sp_token *toks, int32_t fla
 }
 
 int sp_engine_last_path(const sp_engine *e) { return e ? e->last_path : -1; }
+
+int sp_engine_set_device_columns(sp_engine *e, const int32_t *tokens_dev, const uint64_t *masks_dev) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        require(tokens_dev || !masks_dev, SP_EINVAL, "masks need tokens");
+        e->dev_tokens = tokens_dev;
+        e->dev_masks = masks_dev;
+    });
+}
 
 int sp_engine_last_dispatches(const sp_engine *e) { return e ? e->last_dispatches : -1; }
 
@@ -1807,6 +1836,20 @@ int sp_op_gemv(const sp_weight *w, const void *x_dev, int32_t m_cols, float *y_d
 
 }  // extern "C"
 
+// Per-device scratch of the sampling and acceptance entry points: created on a device's first call, kept until
+// sp_library_release (or the process end); each map is guarded by its mutex.
+namespace lib_scratch {
+struct Smp { float *pmax; double *csum; };
+struct Fm { FmHist *hist; FmState *st; };
+struct Acc { unsigned long long *xbuf; unsigned *err; int32_t *host; };
+struct Stage { unsigned char *buf = nullptr; size_t cap = 0; hipEvent_t done = nullptr; bool used = false; };
+std::map<int, Smp> smp;
+std::map<int, Fm> fm;
+std::map<int, Acc> acc;
+std::map<int, Stage> stage;
+std::mutex smp_mu, fm_mu, acc_mu, stage_mu;
+}  // namespace lib_scratch
+
 extern "C" {
 
 int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32_t *row_dev, const double *u_dev,
@@ -1818,18 +1861,16 @@ int sp_op_sample(const float *logits_dev, int32_t vocab, int32_t ld, const int32
         hipStream_t st = (hipStream_t)stream;
         // partial maxima and chunk sums of SMP_BATCH draws, one set per device (calls on one device must not overlap)
         constexpr int SMP_BATCH = 512;
-        struct SmpScratch { float *pmax; double *csum; };
-        static std::map<int, SmpScratch> scratch_of;
-        static std::mutex mu;
         int dev = 0;
         HIPCHK(hipGetDevice(&dev));
-        SmpScratch sc;
+        lib_scratch::Smp sc;
         {
-            std::lock_guard<std::mutex> lock(mu);
-            auto it = scratch_of.find(dev);
-            if (it == scratch_of.end())
-                it = scratch_of.emplace(dev, SmpScratch{dev_alloc<float>((size_t)SMP_BATCH * SMX_BLOCKS),
-                                                        dev_alloc<double>((size_t)SMP_BATCH * SMP_THREADS)}).first;
+            std::lock_guard<std::mutex> lock(lib_scratch::smp_mu);
+            auto it = lib_scratch::smp.find(dev);
+            if (it == lib_scratch::smp.end())
+                it = lib_scratch::smp.emplace(dev, lib_scratch::Smp{dev_alloc<float>((size_t)SMP_BATCH * SMX_BLOCKS),
+                                                                    dev_alloc<double>((size_t)SMP_BATCH * SMP_THREADS)})
+                         .first;
             sc = it->second;
         }
         const double invT = 1.0 / temperature;
@@ -1856,18 +1897,15 @@ int sp_op_sample_filtered(const float *logits_dev, int32_t vocab, int32_t ld, co
         require(top_p > 0.0, SP_EINVAL, "top_p must be positive");
         hipStream_t st = (hipStream_t)stream;
         // histograms and per-row state for FM_ROWS draws, one set per device (calls on one device must not overlap)
-        struct FmScratch { FmHist *hist; FmState *st; };
-        static std::map<int, FmScratch> scratch_of;
-        static std::mutex mu;
         int dev = 0;
         HIPCHK(hipGetDevice(&dev));
-        FmScratch sc;
+        lib_scratch::Fm sc;
         {
-            std::lock_guard<std::mutex> lock(mu);
-            auto it = scratch_of.find(dev);
-            if (it == scratch_of.end())
-                it = scratch_of.emplace(dev, FmScratch{dev_alloc<FmHist>((size_t)FM_ROWS * FM_NLEV),
-                                                       dev_alloc<FmState>(FM_ROWS)}).first;
+            std::lock_guard<std::mutex> lock(lib_scratch::fm_mu);
+            auto it = lib_scratch::fm.find(dev);
+            if (it == lib_scratch::fm.end())
+                it = lib_scratch::fm.emplace(dev, lib_scratch::Fm{dev_alloc<FmHist>((size_t)FM_ROWS * FM_NLEV),
+                                                                  dev_alloc<FmState>(FM_ROWS)}).first;
             sc = it->second;
         }
         const int nb = (vocab + FM_SPAN - 1) / FM_SPAN;
@@ -1900,7 +1938,7 @@ static void accept_tree_run(const float *p_logits_dev, const float *q_logits_dev
                             int32_t n_nodes, const int32_t *token, const int32_t *trial_start, const int32_t *n_trials,
                             const int32_t *trials, int32_t n_trials_total, const double *u, int32_t n_u,
                             double temperature, int32_t max_depth, int32_t *out_dev, hipStream_t st, int32_t *out_host,
-                            hipEvent_t staged) {
+                            hipEvent_t staged, const int32_t *q_row = nullptr, int32_t n_q_rows = 0) {
     {
         require(p_logits_dev && q_logits_dev && token && trial_start && n_trials && trials && u && out_dev, SP_EINVAL,
                 "NULL pointer");
@@ -1916,15 +1954,12 @@ static void accept_tree_run(const float *p_logits_dev, const float *q_logits_dev
         // clearing between launches (the kernel writes every entry of out_dev itself).  The host polls the tags
         // (block 0's, then the drawing block's) instead of synchronising the stream; a poll that runs out (about
         // 1 s) falls back to the synchronisation, which reports any error of the kernel.
-        struct AccScratch { unsigned long long *xbuf; unsigned *err; int32_t *host; };
-        static std::map<int, AccScratch> scratch_of;
-        static unsigned launches = 0;
-        static std::mutex mu;        // the map and the tag counter are shared by every host thread
+        static unsigned launches = 0;   // guarded by acc_mu like the map (shared by every host thread)
         int dev = 0;
         HIPCHK(hipGetDevice(&dev));
-        std::unique_lock<std::mutex> lock(mu);
-        auto it = scratch_of.find(dev);
-        if (it == scratch_of.end()) {
+        std::unique_lock<std::mutex> lock(lib_scratch::acc_mu);
+        auto it = lib_scratch::acc.find(dev);
+        if (it == lib_scratch::acc.end()) {
             unsigned long long *xb = dev_alloc<unsigned long long>(4 * ACC_NB * ACC_XW);
             unsigned *err = dev_alloc<unsigned>(1);
             HIPCHK(hipMemset(xb, 0, 4 * ACC_NB * ACC_XW * sizeof(unsigned long long)));
@@ -1932,14 +1967,15 @@ static void accept_tree_run(const float *p_logits_dev, const float *q_logits_dev
             int32_t *host = nullptr;
             HIPCHK(hipHostMalloc((void **)&host, (ACC_HOST_OUT + 64 + 4) * sizeof(int32_t), hipHostMallocCoherent));
             std::memset(host, 0, (ACC_HOST_OUT + 64 + 4) * sizeof(int32_t));
-            it = scratch_of.emplace(dev, AccScratch{xb, err, host}).first;
+            it = lib_scratch::acc.emplace(dev, lib_scratch::Acc{xb, err, host}).first;
         }
-        const AccScratch sc = it->second;
+        const lib_scratch::Acc sc = it->second;
         launches = launches % 0xFFFFFu + 1;
         const unsigned tag = launches << 12;
         lock.unlock();
         AcceptArgs a{p_logits_dev, q_logits_dev, vocab, ld, token, trial_start, n_trials, trials, u,
-                     n_u, 1.0 / temperature, sc.xbuf, sc.err, tag, n_nodes, n_trials_total, out_dev, max_depth, sc.host};
+                     n_u, 1.0 / temperature, sc.xbuf, sc.err, tag, n_nodes, n_trials_total, out_dev, max_depth, sc.host,
+                     q_row, n_q_rows};
         volatile int32_t *hb = sc.host;
         // entries per thread as a compile-time count (151936 entries: 10)
         const int C = (vocab + ACC_NB * ACC_T - 1) / (ACC_NB * ACC_T);
@@ -1983,29 +2019,31 @@ int sp_op_accept_tree(const float *p_logits_dev, const float *q_logits_dev, int3
     });
 }
 
-int sp_op_accept_tree_host(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld,
-                           int32_t n_nodes, const int32_t *token, const int32_t *trial_start, const int32_t *n_trials,
-                           const int32_t *trials, int32_t n_trials_total, const double *u, int32_t n_u,
-                           double temperature, int32_t max_depth, int32_t *out_dev, void *stream, int32_t *out_host) {
-    return guarded(nullptr, [&] {
+}  // extern "C"
+
+static void accept_tree_host(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld,
+                             int32_t n_nodes, const int32_t *token, const int32_t *trial_start, const int32_t *n_trials,
+                             const int32_t *trials, int32_t n_trials_total, const int32_t *q_row, int32_t n_q_rows,
+                             const double *u, int32_t n_u, double temperature, int32_t max_depth, int32_t *out_dev,
+                             void *stream, int32_t *out_host) {
+    {
         require(token && trial_start && n_trials && trials && u, SP_EINVAL, "NULL pointer");
+        require(!q_row || n_q_rows >= 1, SP_EINVAL, "n_q_rows must be positive");
         require(n_nodes >= 1 && n_nodes <= ACC_MAX_NODES, SP_EINVAL, "n_nodes must be in [1, 64]");
         require(n_trials_total >= 0 && n_trials_total <= ACC_MAX_TRIALS, SP_EINVAL, "n_trials_total must be in [0, 1024]");
         require(n_u >= 1 && n_u <= (1 << 20), SP_EINVAL, "n_u must be in [1, 2^20]");
         // per device: a pinned staging block the kernel reads the tree and the uniforms from (no copy on the stream),
         // and an event after the last walk that read it (waited on before the block is refilled)
-        struct Stage { unsigned char *buf; size_t cap; hipEvent_t done; bool used; };
-        static std::map<int, Stage> stage_of;
-        static std::mutex mu;        // guards the map; calls that overlap on one device race as documented
         int dev = 0;
         HIPCHK(hipGetDevice(&dev));
-        Stage *sgp;
+        lib_scratch::Stage *sgp;
         {
-            std::lock_guard<std::mutex> lock(mu);
-            sgp = &stage_of[dev];    // std::map references stay valid across inserts
+            // guards the map; calls that overlap on one device race as documented
+            std::lock_guard<std::mutex> lock(lib_scratch::stage_mu);
+            sgp = &lib_scratch::stage[dev];    // std::map references stay valid across inserts
         }
-        Stage &sg = *sgp;
-        const size_t ints = (size_t)3 * n_nodes + std::max(n_trials_total, 1);
+        lib_scratch::Stage &sg = *sgp;
+        const size_t ints = (size_t)4 * n_nodes + std::max(n_trials_total, 1);
         const size_t need = (size_t)n_u * sizeof(double) + ints * sizeof(int32_t);
         if (!sg.done) HIPCHK(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
         if (sg.used) HIPCHK(hipEventSynchronize(sg.done));
@@ -2023,12 +2061,92 @@ int sp_op_accept_tree_host(const float *p_logits_dev, const float *q_logits_dev,
         std::memcpy(si, token, (size_t)n_nodes * sizeof(int32_t));
         std::memcpy(si + n_nodes, trial_start, (size_t)n_nodes * sizeof(int32_t));
         std::memcpy(si + 2 * n_nodes, n_trials, (size_t)n_nodes * sizeof(int32_t));
-        if (n_trials_total > 0) std::memcpy(si + 3 * n_nodes, trials, (size_t)n_trials_total * sizeof(int32_t));
-        else si[3 * n_nodes] = 0;
+        if (q_row) std::memcpy(si + 3 * n_nodes, q_row, (size_t)n_nodes * sizeof(int32_t));
+        int32_t *st = si + 4 * n_nodes;
+        if (n_trials_total > 0) std::memcpy(st, trials, (size_t)n_trials_total * sizeof(int32_t));
+        else st[0] = 0;
         sg.used = true;
-        accept_tree_run(p_logits_dev, q_logits_dev, vocab, ld, n_nodes, si, si + n_nodes, si + 2 * n_nodes,
-                        si + 3 * n_nodes, n_trials_total, su, n_u, temperature, max_depth, out_dev, (hipStream_t)stream,
-                        out_host, sg.done);
+        accept_tree_run(p_logits_dev, q_logits_dev, vocab, ld, n_nodes, si, si + n_nodes, si + 2 * n_nodes, st,
+                        n_trials_total, su, n_u, temperature, max_depth, out_dev, (hipStream_t)stream, out_host, sg.done,
+                        q_row ? si + 3 * n_nodes : nullptr, n_q_rows);
+    }
+}
+
+extern "C" {
+
+int sp_op_accept_tree_host(const float *p_logits_dev, const float *q_logits_dev, int32_t vocab, int32_t ld,
+                           int32_t n_nodes, const int32_t *token, const int32_t *trial_start, const int32_t *n_trials,
+                           const int32_t *trials, int32_t n_trials_total, const double *u, int32_t n_u,
+                           double temperature, int32_t max_depth, int32_t *out_dev, void *stream, int32_t *out_host) {
+    return guarded(nullptr, [&] {
+        accept_tree_host(p_logits_dev, q_logits_dev, vocab, ld, n_nodes, token, trial_start, n_trials, trials,
+                         n_trials_total, nullptr, 0, u, n_u, temperature, max_depth, out_dev, stream, out_host);
+    });
+}
+
+int sp_op_accept_tree_rows(const float *p_logits_dev, const float *q_logits_dev, int32_t n_q_rows, int32_t vocab,
+                           int32_t ld, int32_t n_nodes, const int32_t *token, const int32_t *trial_start,
+                           const int32_t *n_trials, const int32_t *trials, int32_t n_trials_total,
+                           const int32_t *q_row, const double *u, int32_t n_u, double temperature, int32_t max_depth,
+                           int32_t *out_dev, void *stream, int32_t *out_host) {
+    return guarded(nullptr, [&] {
+        require(q_row != nullptr, SP_EINVAL, "NULL pointer");
+        accept_tree_host(p_logits_dev, q_logits_dev, vocab, ld, n_nodes, token, trial_start, n_trials, trials,
+                         n_trials_total, q_row, n_q_rows, u, n_u, temperature, max_depth, out_dev, stream, out_host);
+    });
+}
+
+int sp_library_release(void) {
+    return guarded(nullptr, [&] {
+        std::lock_guard<std::mutex> a(lib_scratch::smp_mu), b(lib_scratch::fm_mu), c(lib_scratch::acc_mu),
+            d(lib_scratch::stage_mu);
+        if (lib_scratch::smp.empty() && lib_scratch::fm.empty() && lib_scratch::acc.empty() &&
+            lib_scratch::stage.empty())
+            return;                  // nothing held: no HIP call (a process that never used a GPU stays so)
+        int cur = 0;
+        HIPCHK(hipGetDevice(&cur));
+        // every device that holds scratch: wait for its work (a kernel may still read the scratch), then free it
+        std::set<int> devs;
+        {
+            for (auto &kv : lib_scratch::smp) devs.insert(kv.first);
+            for (auto &kv : lib_scratch::fm) devs.insert(kv.first);
+            for (auto &kv : lib_scratch::acc) devs.insert(kv.first);
+            for (auto &kv : lib_scratch::stage) devs.insert(kv.first);
+            for (int dev : devs) {
+                HIPCHK(hipSetDevice(dev));
+                HIPCHK(hipDeviceSynchronize());
+            }
+            for (auto &kv : lib_scratch::smp) { HIPCHK(hipSetDevice(kv.first)); dev_free(kv.second.pmax); dev_free(kv.second.csum); }
+            for (auto &kv : lib_scratch::fm) { HIPCHK(hipSetDevice(kv.first)); dev_free(kv.second.hist); dev_free(kv.second.st); }
+            for (auto &kv : lib_scratch::acc) {
+                HIPCHK(hipSetDevice(kv.first));
+                dev_free(kv.second.xbuf);
+                dev_free(kv.second.err);
+                if (kv.second.host) HIPCHK(hipHostFree(kv.second.host));
+            }
+            for (auto &kv : lib_scratch::stage) {
+                HIPCHK(hipSetDevice(kv.first));
+                if (kv.second.buf) HIPCHK(hipHostFree(kv.second.buf));
+                if (kv.second.done) HIPCHK(hipEventDestroy(kv.second.done));
+            }
+            lib_scratch::smp.clear();
+            lib_scratch::fm.clear();
+            lib_scratch::acc.clear();
+            lib_scratch::stage.clear();
+        }
+        HIPCHK(hipSetDevice(cur));
+    });
+}
+
+int sp_op_draft_link(const int32_t *tokens_dev, int32_t n_branches, int32_t level, int32_t *canon_dev,
+                     uint64_t *masks_dev, int32_t *rows_dev, void *stream) {
+    return guarded(nullptr, [&] {
+        require(tokens_dev && canon_dev && masks_dev && rows_dev, SP_EINVAL, "NULL pointer");
+        require(n_branches >= 1 && n_branches <= 64 && level >= 0 && n_branches * (level + 1) <= 64, SP_EINVAL,
+                "the drafted nodes (branches x levels) must fit one 64-bit tree mask");
+        hipLaunchKernelGGL(k_draft_link, dim3(1), dim3(64), 0, (hipStream_t)stream, tokens_dev, n_branches, level,
+                           canon_dev, (unsigned long long *)masks_dev, rows_dev);
+        HIPCHK(hipGetLastError());
     });
 }
 

@@ -155,6 +155,27 @@ __global__ void __launch_bounds__(SMS_T) k_smp_draw(const float *logits, int V, 
     if (t == 0) out[s] = found;
 }
 
+// One level of a drafter's proposal on the device (one block, thread b = branch b < nb; tokens [levels][nb]): the
+// branch's canonical branch at `level` -- the first branch whose tokens at levels 0..level equal its own, so every
+// branch through a tree node draws from that node's one row -- then, for the level's columns, column b's tree mask
+// (the canonical node of its branch at every earlier level, node index level' * nb + canonical, and the column
+// itself) and the row its next token is drawn from (its canonical column).
+__global__ void k_draft_link(const int *tokens, int nb, int level, int *canon, unsigned long long *masks, int *rows) {
+    const int b = threadIdx.x;
+    if (b >= nb) return;
+    int c = b;
+    for (int o = 0; o < b; ++o) {
+        bool same = true;
+        for (int lv = 0; lv <= level; ++lv) same = same && tokens[lv * nb + o] == tokens[lv * nb + b];
+        if (same) { c = o; break; }
+    }
+    canon[level * nb + b] = c;
+    unsigned long long m = 1ull << (level * nb + b);
+    for (int lv = 0; lv < level; ++lv) m |= 1ull << (lv * nb + canon[lv * nb + b]);
+    masks[b] = m;
+    rows[b] = c;
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Tree acceptance on ACC_NB co-resident blocks (a plain launch: 64 blocks of 256 threads are all resident on the
 // 256-CU chip once the stream's previous kernel has finished, and every exchange wait is bounded, so a block that
@@ -204,6 +225,8 @@ struct AcceptArgs {
     int max_depth;
     int *host;               // may be NULL: pinned host block written directly: [0] the err word, [1] block 0's
                              // completion tag, [2] the drawing block's tag, [ACC_HOST_OUT ..] a copy of out
+    const int *q_row;        // may be NULL: node i's drafter row is q_row[i] (< n_q_rows) instead of i
+    int n_q_rows;
 };
 constexpr int ACC_HOST_OUT = 16;
 
@@ -408,6 +431,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
 #pragma clang fp contract(off)
     __shared__ AccShared sh;
     __shared__ int s_token[ACC_MAX_NODES], s_tstart[ACC_MAX_NODES], s_ntr[ACC_MAX_NODES], s_trials[ACC_MAX_TRIALS];
+    __shared__ int s_qrow[ACC_MAX_NODES];
     __shared__ double s_u[ACC_U_LDS];
     const int C = (a.V + ACC_NB * ACC_T - 1) / (ACC_NB * ACC_T);
     const int lo = (blockIdx.x * ACC_T + threadIdx.x) * C;
@@ -417,6 +441,7 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
         s_token[i] = a.token[i];
         s_tstart[i] = a.trial_start[i];
         s_ntr[i] = a.n_trials[i];
+        s_qrow[i] = a.q_row ? a.q_row[i] : i;
     }
     for (int i = threadIdx.x; i < a.n_trials_total; i += ACC_T) s_trials[i] = a.trials[i];
     for (int i = threadIdx.x; i < min(a.n_u, ACC_U_LDS); i += ACC_T) s_u[i] = a.u[i];
@@ -435,9 +460,11 @@ __global__ void __launch_bounds__(ACC_T) k_accept_tree(AcceptArgs a) {
             const int child = s_trials[j];
             if (child <= 0 || child >= a.n_nodes || s_token[child] < 0 || s_token[child] >= a.V) alive = acc_bad(a);
         }
+        const int qr = s_qrow[cur];
+        if (nt > 0 && a.q_row && (qr < 0 || qr >= a.n_q_rows)) alive = acc_bad(a);
         if (!alive) break;
         const bool draw_bonus = nt == 0 || k >= a.max_depth;
-        const float *ql = a.q_logits + (size_t)cur * a.ld;
+        const float *ql = a.q_logits + (size_t)(nt > 0 ? qr : 0) * a.ld;
         // the first trial's logits, loaded with the rows (the tree was validated above)
         const int x0 = nt > 0 ? s_token[s_trials[t0]] : 0;
         const float lpx0 = pl[x0], lqx0 = ql[x0];

@@ -349,9 +349,10 @@ class TreeVerifier:
         self.commit(cache, tree, kept)
         return v
 
-    def accept(self, p_logits, q_logits, tree: FlatTree, u, temperature):
+    def accept(self, p_logits, q_logits, tree: FlatTree, u, temperature, q_index=None):
         """GPU acceptance walk (sp_op_accept_tree_host: the tree arrays and uniforms go from host memory straight to
-        the kernel, no copy on the stream).  p_logits / q_logits: device tensors [nodes, vocab].
+        the kernel, no copy on the stream).  p_logits: device tensor [nodes, vocab]; q_logits: [nodes, vocab], or any
+        [rows, vocab] with `q_index` giving node i's row (sp_op_accept_tree_rows; TreeDrafter.q_index).
         Returns (accepted node ids, final token, uniforms used, bonus)."""
         torch = self.torch
         dev = p_logits.device
@@ -374,10 +375,22 @@ class TreeVerifier:
         at = lambda o: ctypes.c_void_p(base + 4 * o)
         ptr = lambda t: ctypes.c_void_p(t.data_ptr())
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        self._lib.check(self.engine.lib.sp_op_accept_tree_host(
-            ptr(p_logits), ptr(q_logits), V, p_logits.stride(0), tree.size, at(rel[0]), at(rel[1]), at(rel[2]),
-            at(rel[3]), len(tree.trials), ctypes.c_void_p(uu.ctypes.data), len(uu), float(temperature), md, ptr(out),
-            stream, res.ctypes.data_as(ctypes.c_void_p)))
+        if q_logits.stride(0) != p_logits.stride(0):
+            raise ValueError('p and q logits rows must have the same stride')
+        if q_index is None:
+            self._lib.check(self.engine.lib.sp_op_accept_tree_host(
+                ptr(p_logits), ptr(q_logits), V, p_logits.stride(0), tree.size, at(rel[0]), at(rel[1]), at(rel[2]),
+                at(rel[3]), len(tree.trials), ctypes.c_void_p(uu.ctypes.data), len(uu), float(temperature), md,
+                ptr(out), stream, res.ctypes.data_as(ctypes.c_void_p)))
+        else:
+            qi = np.ascontiguousarray(q_index, dtype=np.int32)
+            if len(qi) != tree.size:
+                raise ValueError('q_index needs one row per tree node')
+            self._lib.check(self.engine.lib.sp_op_accept_tree_rows(
+                ptr(p_logits), ptr(q_logits), q_logits.shape[0], V, p_logits.stride(0), tree.size, at(rel[0]),
+                at(rel[1]), at(rel[2]), at(rel[3]), len(tree.trials), ctypes.c_void_p(qi.ctypes.data),
+                ctypes.c_void_p(uu.ctypes.data), len(uu), float(temperature), md, ptr(out), stream,
+                res.ctypes.data_as(ctypes.c_void_p)))
         o = res.tolist()
         k = o[0]
         return o[1:1 + k], o[md + 1], o[md + 2], bool(o[md + 3])
@@ -398,74 +411,107 @@ def sample_rows(lib_engine, logits, rows, u, temperature):
 
 
 class TreeDrafter:
-    """Proposes `branches` draft continuations of `depth` tokens by seeded sampling from a drafter engine.
+    """Proposes `branches` draft continuations of `depth` tokens by seeded sampling from a drafter engine, with every
+    level on the device.
 
     The drafter's cache holds the committed tokens it has processed; `propose` first runs the pending committed
-    tokens (ending with the root), samples every branch's first token from the root distribution, then runs one
-    tree-masked pass per level over the new nodes and samples each branch's next token from its node's distribution.
-    Branches sharing a node draw independently from the same distribution (what the multi-branch acceptance rule
-    assumes)."""
+    tokens (ending with the root) and draws every branch's first token from the root's row.  Level l = 1 .. depth-1
+    then runs one column per branch: branch b's level-l token as drafted node (l - 1) * B + b, in the slots after the
+    root, seeing the committed range and, through its tree mask, the canonical node of its branch at every earlier
+    level and itself.  A branch's canonical node is the first branch with the same prefix (sp_op_draft_link), and
+    every branch draws its next token from its canonical column's row, so the branches through one tree node draw
+    independently from that node's one distribution (what the multi-branch acceptance rule assumes).  Tokens,
+    canonical indices and masks stay on the device (the columns read them through SP_F_DEVCOLS); the host reads the
+    drafted tokens and canonical indices once, after the last level."""
 
     def __init__(self, engine):
         self.engine = engine
-        self.verifier = TreeVerifier(engine)
-        self._tok, self._par, self._lvl = [], [], []
+        self._bufs = {}
+        self._node_of, self._index, self._L = {}, {}, -1
+        self.q_rows = None
 
-    def _mask(self, j):
-        m = 0
-        while j >= 0:
-            m |= 1 << j
-            j = self._par[j]
-        return m
+    def _buffers(self, B, depth):
+        b = self._bufs.get((B, depth))
+        if b is None:
+            import torch
+            e = self.engine
+            i32 = dict(dtype=torch.int32, device=e.device)
+            b = self._bufs[(B, depth)] = dict(
+                q=torch.empty((1 + B * (depth - 1), e.vocab), dtype=torch.float32, device=e.device),
+                toks=torch.zeros((depth, B), **i32), canon=torch.zeros((depth, B), **i32),
+                masks=torch.zeros(B, dtype=torch.int64, device=e.device), rows=torch.zeros(B, **i32),
+                zero=torch.zeros(B, **i32), u=torch.zeros(B * depth, dtype=torch.float64, device=e.device),
+                u_host=torch.zeros(B * depth, dtype=torch.float64).pin_memory())
+        return b
 
     def propose(self, cache, pending, n_branches, depth, temperature, u, graph=False):
-        """Returns (branches, rows, used): `rows` maps a drafted prefix (tuple of tokens after the root) to the
-        drafter logits row (device tensor) there; `used` = uniforms consumed (one per branch per level)."""
+        """Returns (branches, rows, used): `rows` maps a drafted prefix (tuple of tokens after the root, shorter than
+        `depth`) to the drafter logits row there, a view of `self.q_rows` (overwritten by the next proposal);
+        `q_index(tree)` gives the same rows by index; `used` = uniforms consumed (one per branch per level)."""
         import torch
         from . import _lib
         e = self.engine
+        B = n_branches
+        if B < 1 or depth < 1 or B * max(depth - 1, 1) > 64:
+            raise ValueError('n_branches x (depth - 1) drafted nodes must be in [1, 64]')
+        if len(u) < B * depth:
+            raise ValueError('need n_branches x depth uniforms')
+        bf = self._buffers(B, depth)
+        q, toks, canon, masks, rows = bf['q'], bf['toks'], bf['canon'], bf['masks'], bf['rows']
+        L = cache.length + len(pending) - 1          # position of the root
+        if cache.window is None and L + 1 + B * (depth - 1) > cache.capacity:
+            raise ValueError('drafter cache too small for the draft tree')
+        # the uniforms go up from pinned memory without waiting (the last proposal's copy ended at its read-back)
+        bf['u_host'].numpy()[:] = np.asarray(u[:B * depth], dtype=np.float64)
+        ud = bf['u']
+        ud.copy_(bf['u_host'], non_blocking=True)
         logits, cache = e.forward(pending, cache)
-        L = cache.length - 1                         # position of the root
-        rows = {(): logits[0]}
-        ui = 0
-        first = sample_rows(e.lib, logits, [0] * n_branches, u[ui:ui + n_branches], temperature)
-        ui += n_branches
-        branches = [[t] for t in first]
-        self._tok, self._par, self._lvl = [], [], []
-        node_of = {}                                 # prefix -> drafter node index
-        S = e._pool_slots
-        V = e.vocab
-        for level in range(1, depth):
-            new_nodes = []
-            for b in branches:
-                pref = tuple(b)
-                if pref not in node_of:
-                    node_of[pref] = len(self._tok)
-                    self._tok.append(pref[-1])
-                    self._par.append(node_of.get(pref[:-1], -1))
-                    self._lvl.append(level)
-                    new_nodes.append(node_of[pref])
-            n_tree = len(self._tok)
-            if L + 1 + n_tree > cache.capacity and cache.window is None:
-                raise ValueError('drafter cache too small for the draft tree')
-            cols = []
-            for j in new_nodes:
-                pos = L + self._lvl[j]
+        q[0].copy_(logits[0])
+        lib, V, S = e.lib, e.vocab, e._pool_slots
+        ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+        stream = ctypes.c_void_p(torch.cuda.current_stream(e.device).cuda_stream)
+        T = float(temperature)
+        _lib.check(lib.sp_op_sample(ptr(q), V, V, ptr(bf['zero']), ptr(ud), B, T, ptr(toks[0]), stream))
+        base = (L + 1) % S
+        try:
+            for lv in range(depth - 1):
+                _lib.check(lib.sp_op_draft_link(ptr(toks), B, lv, ptr(canon), ptr(masks), ptr(rows), stream))
+                pos = L + 1 + lv
                 lo = 0 if cache.window is None else max(0, pos - cache.window + 1)
-                cols.append((self._tok[j], cache.seq, pos, (L + 1 + j) % S, lo, L, (L + 1) % S, n_tree, self._mask(j)))
-            out = torch.empty((len(cols), V), dtype=torch.float32, device=e.device)
-            e.run(cols, _lib.SP_F_LOGITS, logits_out=out)
-            for r, j in enumerate(new_nodes):
-                pref = next(p for p, n in node_of.items() if n == j)
-                rows[pref] = out[r]
-            row_of_branch = [new_nodes.index(node_of[tuple(b)]) for b in branches]
-            nxt = sample_rows(e.lib, out, row_of_branch, u[ui:ui + n_branches], temperature)
-            ui += n_branches
-            for b, t in zip(branches, nxt):
-                b.append(t)
-        self._node_of = node_of
+                cols = [(0, cache.seq, pos, (L + 1 + lv * B + b) % S, lo, L, base, B * (lv + 1), 0) for b in range(B)]
+                _lib.check(lib.sp_engine_set_device_columns(e.h, ptr(toks[lv]), ptr(masks)), e.h)
+                out = q[1 + lv * B:1 + (lv + 1) * B]
+                e.run(cols, _lib.SP_F_LOGITS | _lib.SP_F_DEVCOLS, logits_out=out)
+                _lib.check(lib.sp_op_sample(ptr(out), V, V, ptr(rows), ptr(ud[B * (lv + 1):]), B, T,
+                                            ptr(toks[lv + 1]), stream))
+        finally:
+            _lib.check(lib.sp_engine_set_device_columns(e.h, None, None), e.h)
+        host = torch.cat([toks.flatten(), canon.flatten()]).cpu().numpy()   # the proposal's one read-back
+        tk, cn = host[:depth * B].reshape(depth, B), host[depth * B:].reshape(depth, B)
+        branches = [[int(tk[lv, b]) for lv in range(depth)] for b in range(B)]
+        self._node_of, self._index = {}, {(): 0}
+        out_rows = {(): q[0]}
+        for lv in range(depth - 1):
+            for b in range(B):
+                pref = tuple(branches[b][:lv + 1])
+                j = lv * B + int(cn[lv, b])          # the same for every branch with this prefix
+                self._node_of[pref] = j
+                self._index[pref] = 1 + j
+                out_rows[pref] = q[1 + j]
         self._L = L
-        return branches, rows, ui
+        self.q_rows = q
+        return branches, out_rows, B * depth
+
+    def q_index(self, tree: FlatTree):
+        """Row of `self.q_rows` holding the drafter's distribution at each node of `tree` (the flattened last
+        proposal); leaves (never read by the acceptance walk) get row 0."""
+        out, prefixes = [0] * tree.size, [()]
+        for i in range(1, tree.size):
+            prefixes.append(prefixes[tree.parent[i]] + (tree.token[i],))
+        for i, pref in enumerate(prefixes):
+            if tree.n_children[i]:
+                out[i] = self._index[pref]
+        return out
 
     def commit(self, cache, accepted_tokens):
         """Keep the drafted nodes on the accepted path (those the drafter processed) after the root."""
@@ -512,37 +558,58 @@ class SpecStats:
     nodes: int = 0
 
 
-def speculative_generate(target, drafter, prompt, steps, n_branches=8, depth=4, temperature=0.8, seed=0,
-                         window=None, stats=None):
-    """Tree speculative sampling: each step the drafter proposes n_branches x depth tokens, the target verifies all
-    nodes in one pass, the acceptance kernel keeps a prefix of one branch plus one corrected or bonus token.
-    Returns the generated tokens (after the prompt)."""
-    import torch
-    if len(prompt) < 1:
-        raise ValueError('prompt cannot be empty')
-    cap = len(prompt) + steps * (depth + 1) + 2 * 64
-    tcache = target.new_cache(cap, window=window)
-    dcache = drafter.engine.new_cache(cap, window=window)
-    verifier = TreeVerifier(target)
-    committed = [int(t) for t in prompt]
-    if len(committed) > 1:
-        target.forward(committed[:-1], tcache)
-    out = []
-    st = stats if stats is not None else SpecStats()
-    for step in range(steps):
-        u = uniforms(seed, step, n_branches * depth + 64)
-        pending = committed[dcache.length:]
-        branches, rows, used = drafter.propose(dcache, pending, n_branches, depth, temperature, u)
-        tree = flatten(committed[-1], branches)
-        p = verifier.forward(tcache, tree, ids=False)          # the target engine's own logits rows, no copy
-        q = q_rows_for_tree(tree, rows, target.vocab, target.device)
-        path, final, _, bonus = verifier.accept(p, q, tree, u[used:], temperature)
+class SpeculativeLoop:
+    """Tree speculative sampling, one step at a time: each step the drafter proposes n_branches x depth tokens, the
+    target verifies all nodes in one pass, the acceptance kernel keeps a prefix of one branch plus one corrected or
+    bonus token.  The constructor prefills both caches with the prompt (all but its last token, the first step's
+    root), so `step()` does only a step's work.  `capacity`: cache positions (default: the prompt + 4096)."""
+
+    def __init__(self, target, drafter, prompt, n_branches=8, depth=4, temperature=0.8, seed=0, window=None,
+                 capacity=None, stats=None):
+        if len(prompt) < 1:
+            raise ValueError('prompt cannot be empty')
+        cap = capacity if capacity is not None else len(prompt) + 4096
+        self.target, self.drafter = target, drafter
+        self.n_branches, self.depth, self.temperature, self.seed = n_branches, depth, temperature, seed
+        self.tcache = target.new_cache(cap, window=window)
+        self.dcache = drafter.engine.new_cache(cap, window=window)
+        self.verifier = TreeVerifier(target)
+        self.committed = [int(t) for t in prompt]
+        self.stats = stats if stats is not None else SpecStats()
+        self._step = 0
+        if len(self.committed) > 1:
+            target.forward(self.committed[:-1], self.tcache)
+            drafter.engine.forward(self.committed[:-1], self.dcache)
+
+    def step(self):
+        """One speculative step; returns the emitted tokens (accepted drafts + the corrected or bonus token)."""
+        B, depth, T = self.n_branches, self.depth, self.temperature
+        u = uniforms(self.seed, self._step, B * depth + 64)
+        self._step += 1
+        pending = self.committed[self.dcache.length:]
+        branches, rows, used = self.drafter.propose(self.dcache, pending, B, depth, T, u)
+        tree = flatten(self.committed[-1], branches)
+        p = self.verifier.forward(self.tcache, tree, ids=False)    # the target engine's own logits rows, no copy
+        path, final, _, bonus = self.verifier.accept(p, self.drafter.q_rows, tree, u[used:], T,
+                                                     q_index=self.drafter.q_index(tree))
         acc_tokens = [tree.token[n] for n in path]
-        verifier.commit(tcache, tree, path)
-        drafter.commit(dcache, acc_tokens)
+        self.verifier.commit(self.tcache, tree, path)
+        self.drafter.commit(self.dcache, acc_tokens)
         emitted = acc_tokens + [int(final)]
-        committed += emitted
-        out += emitted
+        self.committed += emitted
+        st = self.stats
         st.steps += 1; st.emitted += len(emitted); st.accepted += len(path); st.bonus += int(bonus)
         st.nodes += tree.size - 1
+        return emitted
+
+
+def speculative_generate(target, drafter, prompt, steps, n_branches=8, depth=4, temperature=0.8, seed=0,
+                         window=None, stats=None):
+    """`steps` steps of SpeculativeLoop over a fresh pair of caches.  Returns the generated tokens (after the
+    prompt)."""
+    loop = SpeculativeLoop(target, drafter, prompt, n_branches, depth, temperature, seed, window,
+                           capacity=len(prompt) + steps * (depth + 1) + 2 * 64, stats=stats)
+    out = []
+    for _ in range(steps):
+        out += loop.step()
     return out

@@ -55,6 +55,22 @@ def test_workspace_queries_are_pure_host_functions():
     assert lib.sp_op_gemv_workspace(None, 1) == 0
 
 
+def test_library_release_without_scratch_is_a_host_no_op():
+    # nothing was created on a device in this process: the release makes no HIP call and succeeds
+    assert _lib.load().sp_library_release() == _lib.SP_OK
+
+
+def test_new_entry_points_reject_bad_arguments_before_any_gpu_call():
+    lib = _lib.load()
+    assert lib.sp_op_draft_link(None, 8, 0, None, None, None, None) == _lib.SP_EINVAL
+    d = ctypes.c_void_p(16)             # never dereferenced: the size check fails first
+    assert lib.sp_op_draft_link(d, 16, 4, d, d, d, None) == _lib.SP_EINVAL       # 80 drafted nodes > 64
+    assert b'64-bit' in lib.sp_last_error()
+    assert lib.sp_engine_set_device_columns(None, None, None) == _lib.SP_EINVAL
+    assert lib.sp_op_accept_tree_rows(None, None, 1, 10, 10, 1, None, None, None, None, 0, None, None, 1, 0.8, 1,
+                                      None, None, None) == _lib.SP_EINVAL
+
+
 def test_null_arguments_are_rejected_with_einval():
     lib = _lib.load()
     assert lib.sp_engine_create(None, None) == _lib.SP_EINVAL

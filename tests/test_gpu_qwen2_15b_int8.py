@@ -130,7 +130,8 @@ def test_tree_verify_8x4_over_2048_prefix_vs_oracle(m15, drafter):
     eng.forward(ctx, cache)
     dcache = drafter.new_cache(P + 64)
     u = uniforms(7, 0, 8 * 4 + 64)
-    branches, drows, used = TreeDrafter(drafter).propose(dcache, ctx + [root], 8, 4, 0.8, u)
+    td = TreeDrafter(drafter)
+    branches, drows, used = td.propose(dcache, ctx + [root], 8, 4, 0.8, u)
     tree = flatten(root, branches)
     assert tree.size > 8 and tree.max_depth == 4
     verifier = TreeVerifier(eng)
@@ -146,8 +147,8 @@ def test_tree_verify_8x4_over_2048_prefix_vs_oracle(m15, drafter):
     same = check_greedy([int(t) for t in ids], ref_rows, what='tree')
     print(f'1.5b tree: worst max-rel {worst:.2e}, {same}/{tree.size} node ids equal the oracle argmax', flush=True)
     assert same >= 0.75 * tree.size
-    q = q_rows_for_tree(tree, drows, V, eng.device)
-    got = verifier.accept(p, q, tree, u[used:], 0.8)
+    q = q_rows_for_tree(tree, drows, V, eng.device)          # node order, for the oracle
+    got = verifier.accept(p, td.q_rows, tree, u[used:], 0.8, q_index=td.q_index(tree))
     t = dict(token=tree.token, trial_start=tree.trial_start, n_trials=tree.n_trials, trials=tree.trials)
     path, final, n_u, bonus, margin = sref.accept_tree(p.cpu().numpy(), q.cpu().numpy(), t, np.asarray(u[used:]), 0.8,
                                                        tree.max_depth)

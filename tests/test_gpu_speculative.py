@@ -160,6 +160,108 @@ def test_accept_tree_entries_agree(model, V):
         if case == 3:
             assert path == [] and used == 301
 
+def test_accept_tree_rows_by_index(model):
+    """sp_op_accept_tree_rows with the drafter rows scattered over a larger buffer takes the decisions of the
+    host-array entry over the same rows gathered in node order, and refuses an index past the buffer."""
+    cfg, w, eng, _ = model
+    verifier = TreeVerifier(eng)
+    rng = np.random.default_rng(5)
+    dev = eng.device
+    for case in range(4):
+        tree, p, q = _random_case(rng, 151936 if case == 0 else 64)
+        V = p.shape[1]
+        nr = tree.size + 7
+        perm = rng.permutation(nr)[:tree.size]               # node i's row in the scattered buffer
+        big = rng.normal(size=(nr, V)).astype(np.float32)
+        big[perm] = q
+        u = sref.uniforms(13, case, 64)
+        pd = torch.from_numpy(p).to(dev)
+        got_rows = verifier.accept(pd, torch.from_numpy(big).to(dev), tree, u, 0.8, q_index=perm.tolist())
+        got_host = verifier.accept(pd, torch.from_numpy(q).to(dev), tree, u, 0.8)
+        assert tuple(got_rows) == tuple(got_host), case
+    bad = perm.copy()
+    bad[0] = nr                                               # the root has trials: its row is read
+    with pytest.raises(ValueError, match='malformed tree'):
+        verifier.accept(pd, torch.from_numpy(big).to(dev), tree, u, 0.8, q_index=bad.tolist())
+
+
+def _link_ref(toks, nb, level, canon):
+    """Host restatement of one sp_op_draft_link level (first branch with the same prefix; canonical ancestors)."""
+    c = []
+    for b in range(nb):
+        cb = next(o for o in range(b + 1) if all(toks[lv][o] == toks[lv][b] for lv in range(level + 1)))
+        c.append(cb)
+    canon[level] = c
+    masks = [(1 << (level * nb + b)) | sum(1 << (lv * nb + canon[lv][b]) for lv in range(level)) for b in range(nb)]
+    return c, masks
+
+
+def test_draft_link_matches_host_rule(gpu_device):
+    lib = _lib.load()
+    rng = np.random.default_rng(3)
+    for nb, depth in [(8, 4), (5, 3), (1, 5), (16, 4)]:
+        toks = rng.integers(0, 3, size=(depth, nb)).astype(np.int32)     # few values: many shared prefixes
+        td = torch.from_numpy(toks).to(gpu_device)
+        canon = torch.full((depth, nb), -1, dtype=torch.int32, device=gpu_device)
+        masks = torch.zeros(nb, dtype=torch.int64, device=gpu_device)
+        rows = torch.zeros(nb, dtype=torch.int32, device=gpu_device)
+        ref_canon = [[0] * nb for _ in range(depth)]
+        ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+        for level in range(depth - 1):
+            _lib.check(lib.sp_op_draft_link(ptr(td), nb, level, ptr(canon), ptr(masks), ptr(rows), None))
+            c, m = _link_ref(toks.tolist(), nb, level, ref_canon)
+            assert canon[level].tolist() == c and rows.tolist() == c
+            assert [int(x) & (2 ** 64 - 1) for x in masks.tolist()] == m, (nb, level)
+    assert lib.sp_op_draft_link(ptr(td), 16, 4, ptr(canon), ptr(masks), ptr(rows), None) == _lib.SP_EINVAL
+
+
+def test_device_drafter_rows_and_draws(model, gpu_device):
+    """The device-side proposal: every drafted prefix's row equals the drafter run linearly over that prefix
+    (fp16 bar), branches sharing a prefix share its row, and each branch's token at every level is the oracle's draw
+    from its prefix's row with the level's uniform (bit-exact)."""
+    cfg, w, eng, _ = model
+    drafter = TreeDrafter(eng)
+    prefix = random_prompt(11, cfg['vocab_size'], seed=12)
+    B, depth, T = 8, 4, 1.5
+    u = sref.uniforms(21, 0, B * depth + 8)
+    cache = eng.new_cache(128)
+    eng.forward(prefix[:-1], cache)
+    branches, rows, used = drafter.propose(cache, [prefix[-1]], B, depth, T, u)
+    assert used == B * depth and len(branches) == B and all(len(b) == depth for b in branches)
+    assert cache.length == len(prefix)
+    for b in range(B):
+        for lv in range(depth):
+            pref = tuple(branches[b][:lv])
+            row = rows[pref].cpu()
+            tok, margin = sref.draw(sref.softmax_weights(row.numpy(), T), u[lv * B + b])
+            assert margin > MARGIN and branches[b][lv] == tok, (b, lv)
+    for pref, row in rows.items():
+        lin, _ = eng.forward(prefix + list(pref), eng.new_cache(64), all_logits=True)
+        assert max_rel(row, lin[-1]) < TOL, pref
+    tree = flatten(prefix[-1], branches)
+    idx = drafter.q_index(tree)
+    prefixes = [()]
+    for i in range(1, tree.size):
+        prefixes.append(prefixes[tree.parent[i]] + (tree.token[i],))
+    for i, pref in enumerate(prefixes):
+        if tree.n_children[i]:
+            assert torch.equal(drafter.q_rows[idx[i]], rows[pref])
+
+
+def test_devcols_flag_errors(model):
+    cfg, w, eng, _ = model
+    cache = eng.new_cache(16)
+    col = eng._column(1, cache, 0, 0)
+    _lib.check(eng.lib.sp_engine_set_device_columns(eng.h, None, None), eng.h)
+    with pytest.raises(RuntimeError, match='sp_engine_set_device_columns'):
+        eng.run([col], _lib.SP_F_LOGITS | _lib.SP_F_DEVCOLS)
+    t = torch.zeros(1, dtype=torch.int32, device=eng.device)
+    _lib.check(eng.lib.sp_engine_set_device_columns(eng.h, ctypes.c_void_p(t.data_ptr()), None), eng.h)
+    with pytest.raises(ValueError, match='both name the tokens'):
+        eng.run([col], _lib.SP_F_LOGITS | _lib.SP_F_DEVCOLS | _lib.SP_F_FEED)
+    _lib.check(eng.lib.sp_engine_set_device_columns(eng.h, None, None), eng.h)
+
+
 def test_tree_pass_equals_linear_paths(model):
     cfg, w, eng, _ = model
     prefix = random_prompt(12, cfg['vocab_size'], seed=4)
@@ -272,3 +374,23 @@ def test_logits_only_pass_returns_the_engine_rows_without_a_copy(model):
     _lib.check(eng.lib.sp_engine_logits(eng.h, ctypes.byref(ptr)), eng.h)
     assert view.data_ptr() == ptr.value
     assert torch.equal(view, copied)
+
+
+def test_library_release_then_reuse(model, gpu_device):
+    """sp_library_release frees the sampling and acceptance scratch; the next calls create it again and give the
+    same draws and decisions."""
+    cfg, w, eng, _ = model
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(1)
+    logits = (torch.randn(3, 5000, generator=g) * 2).to(gpu_device)
+    u = sref.uniforms(2, 0, 6)
+    first = sample_rows(lib, logits, [0, 1, 2, 0, 1, 2], u, 0.9)
+    tree, p, q = _random_case(np.random.default_rng(8), 64)
+    pd, qd = torch.from_numpy(p).to(gpu_device), torch.from_numpy(q).to(gpu_device)
+    verifier = TreeVerifier(eng)
+    ua = sref.uniforms(4, 0, 64)
+    a1 = verifier.accept(pd, qd, tree, ua, 0.8)
+    assert lib.sp_library_release() == _lib.SP_OK
+    assert lib.sp_library_release() == _lib.SP_OK          # nothing held: no-op
+    assert sample_rows(lib, logits, [0, 1, 2, 0, 1, 2], u, 0.9) == first
+    assert verifier.accept(pd, qd, tree, ua, 0.8) == a1
