@@ -31,7 +31,7 @@ constexpr int SMP_THREADS = 1024;      // chunks per row
 // the fallbacks: a chunk with no running sum above the target gives its last positive-weight index, no positive
 // weight where the target fell gives the last positive-weight index of the row (0 if none).
 // Scratch per draw: SMX_BLOCKS floats and SMP_THREADS doubles.
-constexpr int SMX_BLOCKS = 16, SMS_CPB = 8, SMS_T = 256, SMS_WIN = 2048;
+constexpr int SMX_BLOCKS = 64, SMS_CPB = 8, SMS_T = 256, SMS_WIN = 2048;
 
 __device__ __forceinline__ double smp_weight(const float *l, int i, float m, double invT) {
     return exp(((double)l[i] - (double)m) * invT);
@@ -91,7 +91,7 @@ __global__ void __launch_bounds__(SMS_T) k_smp_draw(const float *logits, int V, 
                                                      const double *u, double invT, const float *pmax,
                                                      const double *csum, int *out) {
     __shared__ double pre[SMP_THREADS + 1];
-    __shared__ double w[SMS_WIN];
+    __shared__ double w[SMS_WIN + 16];
     __shared__ int sel, found;
     __shared__ int last[SMS_T / 64];
     const int s = blockIdx.x, t = threadIdx.x;
@@ -102,8 +102,19 @@ __global__ void __launch_bounds__(SMS_T) k_smp_draw(const float *logits, int V, 
     if (t == 0) { sel = -1; found = -1; }
     __syncthreads();
     if (t == 0) {
+        // the sums in chunk order; each batch of 32 is read into registers first, so the reads do not wait on the
+        // prefixes written before them
         double p = 0.0;
-        for (int j = 0; j < SMP_THREADS; ++j) { const double c = pre[j]; pre[j] = p; p += c; }
+        for (int j0 = 0; j0 < SMP_THREADS; j0 += 32) {
+            double c[32];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) c[k] = pre[j0 + k];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                pre[j0 + k] = p;
+                p += c[k];
+            }
+        }
         pre[SMP_THREADS] = p;
     }
     __syncthreads();
@@ -123,11 +134,21 @@ __global__ void __launch_bounds__(SMS_T) k_smp_draw(const float *logits, int V, 
             for (int i = wlo + t; i < whi; i += SMS_T) w[i - wlo] = smp_weight(l, i, m, invT);
             __syncthreads();
             if (t == 0 && pick < 0) {
-                for (int i = wlo; i < whi; ++i) {
-                    const double wi = w[i - wlo];
-                    if (wi > 0.0) lastpos = i;
-                    acc += wi;
-                    if (acc > tl) { pick = i; break; }
+                // in index order, 16 weights read ahead at a time (entries past the window read a zero pad and are
+                // not visited)
+                for (int i0 = wlo; i0 < whi && pick < 0; i0 += 16) {
+                    double c[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) c[k] = w[i0 - wlo + k];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) {
+                        const int i = i0 + k;
+                        if (pick < 0 && i < whi) {
+                            if (c[k] > 0.0) lastpos = i;
+                            acc += c[k];
+                            if (acc > tl) pick = i;
+                        }
+                    }
                 }
                 found = pick;
             }
