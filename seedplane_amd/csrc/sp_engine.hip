@@ -105,12 +105,6 @@ struct GemvPlan {
     bool shallow;      // several column tiles: one k-tile per load batch (k_gemv<..., SHALLOW>)
 };
 
-#ifdef SP_GEMV_TUNE
-// plan override for launch-shape sweeps (row groups per wave, waves per block, slices); 0 keeps the heuristic
-int g_tune[3] = {0, 0, 0};
-// single-column step plans: qkv slices, qkv waves, down slices, down waves, gate_up waves (0 keeps the defaults)
-int g_tune_one[5] = {0, 0, 0, 0, 0};
-#endif
 
 // Launch shape of one GEMV, from launch-shape sweeps (row groups per wave x waves x slices) of the Qwen2-0.5B fp16,
 // 1.5B int8 and 7B int4 matrices at 1, 16 and 32-33 columns.  Small-batch GEMVs are latency-bound: what counts is
@@ -138,10 +132,6 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
         s = std::min(s, mt == 1 || m.fmt == 3 ? GEMV_MAX_SLICES : 4);
         if (slices > 0) s = std::min(slices, std::max(1, m.nkt / 2));
     }
-#ifdef SP_GEMV_TUNE
-    if (g_tune[0] > 0 && p.units % g_tune[0] == 0) p.r = g_tune[0];
-    if (g_tune[2] > 0) s = (split_ok && !m.paired) ? std::min(g_tune[2], GEMV_MAX_SLICES) : 1;
-#endif
     p.s = s;
     p.kslice = (m.nkt + s - 1) / s;
     // several column tiles: 8 waves for the split layer matrices and long k-ranges, 4 for the gate_up pair and the
@@ -155,9 +145,6 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
     // with int4 codes shallow batches are slower (head at 32 columns 58 -> 64 us, int4 matrices 10-35 %).
     p.shallow = mt == 3 && m.fmt == 2 && !(s > 1 && p.kslice >= 32);
     if (p.shallow && p.r == 4 && waves == 0) nw = std::min(nw, 2);
-#ifdef SP_GEMV_TUNE
-    if (g_tune[1] > 0) nw = std::min(g_tune[1], mt == 1 ? 16 : 8);
-#endif
     if (mt == 1 && p.r > 1) nw = std::min(nw, 4);
     while (nw > 1 && (size_t)nw * p.r * p.rg * mt * 1024 > GEMV_MAX_LDS) --nw;
     p.nw = std::max(1, nw);
@@ -297,10 +284,6 @@ int launch_gemv(const DevMat &m, int epi, const f16 *x, int ldx, int mcols, floa
         // the SwiGLU pair: 8 waves of <= 3 k-tiles each keep the most loads in flight (launch-shape sweep)
         if (m.paired && waves == 0) {
             nw = std::min(p.kslice, 8);
-#ifdef SP_GEMV_TUNE
-            if (g_tune_one[4] > 0) nw = std::min(p.kslice, g_tune_one[4]);
-            if (g_tune[1] > 0) nw = std::min(g_tune[1], 16);
-#endif
         }
         const int T = (p.kslice + nw - 1) / nw;
         const int kt = m.fmt == 1 ? 32 : (m.fmt == 2 ? 64 : 128);
@@ -373,8 +356,7 @@ void launch_attn_rope_hd(int G, dim3 grid, hipStream_t st, const AttnArgs &a, co
 
 // Keys per multi-query block (one partial record per block and row): 128 for tree groups (verify pass: 33 x 12
 // query rows, fewer and larger blocks, half the records to merge; -1 % per pass), 64 otherwise (the plain batches
-// and prefill chunks got slower with 128: bs16 +16 %, prefill +3 %).  g_mq_ch != 0 forces one size (sweeps).
-int g_mq_ch = 0;
+// and prefill chunks got slower with 128: bs16 +16 %, prefill +3 %).
 template <int HD, int CH>
 void launch_attn_mq_ch(int G, dim3 grid, hipStream_t st, const AttnMqArgs &a) {
     switch (G) {
@@ -423,17 +405,11 @@ void launch_rope(int n, const RopeArgs &ra, int np, hipStream_t st) {
 }
 
 // decode attention split: waves per block x 32-key sub-chunks per wave
-#ifdef SP_GEMV_TUNE
-int g_tune_attn[2] = {0, 0};
-#endif
 struct DecShape { int nwv, sub; };
 // Keys per decode-attention block: 1024 (2 waves streaming 16 sub-chunks of 32 keys, two sub-chunks of loads in
 // flight per wave) when the ranges give the chip at least two such blocks per CU, else 256 (4 waves x 2 sub-chunks).
 // 32 columns of 8260 keys, 4 kv heads: 126 -> 111 us per launch.
 DecShape dec_shape(int kpb) {
-#ifdef SP_GEMV_TUNE
-    if (g_tune_attn[0] > 0) return DecShape{g_tune_attn[0], g_tune_attn[1]};
-#endif
     return kpb >= 1024 ? DecShape{2, 16} : DecShape{4, 2};
 }
 int dec_keys(const DecShape &d) { return d.nwv * d.sub * DEC_KC; }
@@ -444,17 +420,6 @@ constexpr int DEC_ROUTE_KEYS = 256;
 template <int HD>
 void launch_attn_dec_hd(int kpb, dim3 grid, hipStream_t st, const AttnArgs &aa, f16 *out, int ldo, int direct, int mtp) {
     const DecShape d = dec_shape(kpb);
-#ifdef SP_GEMV_TUNE
-    if (d.nwv == 1 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 1>), grid, dim3(64), 0, st, aa, out, ldo, direct, mtp); return; }
-    if (d.nwv == 2 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 1>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp); return; }
-    if (d.nwv == 4 && d.sub == 1) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 1>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
-    if (d.nwv == 2 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 2>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp); return; }
-    if (d.nwv == 1 && d.sub == 2) { hipLaunchKernelGGL((k_attn_dec<HD, 1, 2>), grid, dim3(64), 0, st, aa, out, ldo, direct, mtp); return; }
-    if (d.nwv == 4 && d.sub == 4) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 4>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
-    if (d.nwv == 4 && d.sub == 8) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 8>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
-    if (d.nwv == 4 && d.sub == 16) { hipLaunchKernelGGL((k_attn_dec<HD, 4, 16>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp); return; }
-    if (d.nwv == 2 && d.sub == 8) { hipLaunchKernelGGL((k_attn_dec<HD, 2, 8>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp); return; }
-#endif
     if (d.nwv == 2 && d.sub == 16) hipLaunchKernelGGL((k_attn_dec<HD, 2, 16>), grid, dim3(128), 0, st, aa, out, ldo, direct, mtp);
     else hipLaunchKernelGGL((k_attn_dec<HD, 4, 2>), grid, dim3(256), 0, st, aa, out, ldo, direct, mtp);
 }
@@ -710,14 +675,9 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
     int maxcols = 1;
     for (auto &g : p.groups) { p.mq = p.mq || g.ncols > 1; maxcols = std::max(maxcols, g.ncols); }
     const int G = d.n_heads / d.n_kv_heads;
-    bool dec_ok = true, force = false;
-#ifdef SP_GEMV_TUNE
-    dec_ok = g_tune_attn[0] >= 0;
-    force = g_tune_attn[0] > 0;
-#endif
     // blocks per kv head and column: decode key splits of DEC_ROUTE_KEYS keys, chunk-kernel blocks of ATT_CH
     long dec_work = 0, chunk_work = 0;
-    bool dec_cols = G <= 8 && dec_ok;
+    bool dec_cols = G <= 8;
     for (int c = 0; c < n; ++c) {
         dec_cols = dec_cols && t[c].tree_count == 0 && nlin_of(t[c]) >= 1;
         dec_work += (long)(nlin_of(t[c]) + DEC_ROUTE_KEYS - 1) / DEC_ROUTE_KEYS * d.n_kv_heads;
@@ -728,14 +688,14 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
     // step: 16 x 1024 keys, 2 kv heads (512 chunks, 128 splits) multi-query 2.3% faster than the chunk kernel;
     // 32 x 8192 keys, 4 kv heads (4096 splits) the decode kernel 2.8% faster; 16 ragged prompts of 16-128 keys
     // (about 64 chunks) the chunk kernel with the rotation fused 7% faster.
-    if (n > 1 && dec_cols && chunk_work >= 256 && dec_work < 1024 && !force) p.mq = true;
+    if (n > 1 && dec_cols && chunk_work >= 256 && dec_work < 1024) p.mq = true;
     p.splits = (maxcols * G + 63) / 64;
     p.colnc.assign(n, 0);
     int mx = 1;
     if (p.mq) {
         bool trees = true;
         for (auto &g : p.groups) trees = trees && g.tree_count > 0;
-        p.mq_ch = g_mq_ch ? g_mq_ch : (trees ? 128 : ATT_CH);
+        p.mq_ch = trees ? 128 : ATT_CH;
         for (auto &g : p.groups) {
             const int nc = (g.nlin + g.tree_count + p.mq_ch - 1) / p.mq_ch;
             for (int c = 0; c < g.ncols; ++c) p.colnc[g.first_col + c] = nc;
@@ -752,7 +712,7 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
     if (!p.mq && dec_cols) {
         // the MFMA decode kernel pays off once its key splits fill the chip (long contexts, large batches); short
         // ranges stay on the 64-key chunk kernel, which spreads them over more CUs
-        p.dec = dec_work >= 256 || force;
+        p.dec = dec_work >= 256;
     }
     if (!p.mq && !p.dec) {
         // every column a plain ring range of its own sequence: no column sees another column's new key, so each
@@ -865,12 +825,6 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
     // in gpart.  SP_F_UNFUSED keeps the plans and runs the norm and the combine as kernels of their own.
     // launch-shape sweep of whole bs1 steps (1.5B int8): qkv in 2 slices of 8 waves, down in 8 slices of 8 waves
     int one_qs = 2, one_qw = 8, one_ds = 8, one_dw = 8;
-#ifdef SP_GEMV_TUNE
-    if (g_tune_one[0] > 0) one_qs = g_tune_one[0];
-    if (g_tune_one[1] > 0) one_qw = g_tune_one[1];
-    if (g_tune_one[2] > 0) one_ds = g_tune_one[2];
-    if (g_tune_one[3] > 0) one_dw = g_tune_one[3];
-#endif
     const bool one = n == 1 && !layers.empty() && gemv_pro_ok(layers[0].qkv, PRO_NORM, H, HD, one_qs, one_qw) &&
                      gemv_pro_ok(layers[0].o, PRO_COMB, H, HD);
     const bool fuse = one && !(flags & SP_F_UNFUSED);
@@ -1433,14 +1387,6 @@ int sp_engine_set_device_columns(sp_engine *e, const int32_t *tokens_dev, const 
 
 int sp_engine_last_dispatches(const sp_engine *e) { return e ? e->last_dispatches : -1; }
 
-#ifdef SP_GEMV_TUNE
-void sp_debug_gemv_plan(int r, int nw, int s) { g_tune[0] = r; g_tune[1] = nw; g_tune[2] = s; }
-void sp_debug_one_plan(int qs, int qw, int ds, int dw, int gw) {
-    g_tune_one[0] = qs; g_tune_one[1] = qw; g_tune_one[2] = ds; g_tune_one[3] = dw; g_tune_one[4] = gw;
-}
-void sp_debug_attn_plan(int nwv, int sub) { g_tune_attn[0] = nwv; g_tune_attn[1] = sub; }
-void sp_debug_mq_ch(int ch) { g_mq_ch = ch == 128 ? 128 : ch == 64 ? 64 : 0; }
-#endif
 
 int sp_engine_logits(sp_engine *e, float **logits_dev) {
     if (!e || !logits_dev) { g_err = "NULL argument"; return SP_EINVAL; }
