@@ -125,6 +125,12 @@ int sp_engine_load(sp_engine *e, int32_t kind, int32_t layer, int32_t fmt, int32
  * every layer (layout [layer][seq][kv_head][slot][head_dim]).  Re-reserving frees the previous cache. */
 int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots);
 
+/* Read access to the cache tensors (reference: KVCache.keys / KVCache.values, seedplane/qwen_engine.py:18-29, which
+ * are per-layer tensors).  k_dev / v_dev receive layer `layer`'s K and V pool: fp16 [n_seq][n_kv_heads][n_slots]
+ * [head_dim] (sp_engine_kv_reserve's sizes), position p of sequence s at slot p mod n_slots.  The pointers stay
+ * valid until the pool is reserved or grown again, or the engine is destroyed. */
+int sp_engine_kv_layer(sp_engine *e, int32_t layer, void **k_dev, void **v_dev);
+
 /* Replaces the independence of the reference's per-cache tensors (Qwen2Engine.new_cache allocates a fresh KVCache
  * per call and never touches the others, qwen_engine.py:82-85): grows the pool to n_seq x n_slots (neither smaller
  * than now) while keeping the live sequences.  For kept sequence keep_seq[i] of length keep_len[i], positions

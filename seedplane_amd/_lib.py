@@ -97,6 +97,7 @@ SIGNATURES = {
     'sp_op_draft_link': (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     'sp_engine_set_device_columns': (c_int, [c_void_p, c_void_p, c_void_p]),
     'sp_library_release': (c_int, []),
+    'sp_engine_kv_layer': (c_int, [c_void_p, c_int32, ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p)]),
 }
 
 _lib = None

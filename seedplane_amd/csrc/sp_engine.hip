@@ -1197,6 +1197,17 @@ int sp_engine_kv_reserve(sp_engine *e, int32_t n_seq, int32_t n_slots) {
     });
 }
 
+int sp_engine_kv_layer(sp_engine *e, int32_t layer, void **k_dev, void **v_dev) {
+    if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }
+    return guarded(e, [&] {
+        require(k_dev && v_dev, SP_EINVAL, "NULL pointer");
+        require(e->n_seq > 0, SP_ESTATE, "KV cache not reserved");
+        require(layer >= 0 && layer < (int)e->kc.size(), SP_EINVAL, "layer out of range");
+        *k_dev = e->kc[layer];
+        *v_dev = e->vc[layer];
+    });
+}
+
 int sp_engine_kv_grow(sp_engine *e, int32_t n_seq, int32_t n_slots, int32_t n_keep, const int32_t *keep_seq,
                       const int32_t *keep_len) {
     if (!e) { g_err = "engine is NULL"; return SP_EINVAL; }

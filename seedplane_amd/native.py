@@ -84,7 +84,7 @@ class NativeEngine:
     DEFAULT_SYSTEM = 'You are a helpful assistant.'
 
     def __init__(self, bundle, engine=None, mode=None, full=False, ctx=None, temperature=None, top_k=None, top_p=None,
-                 seed=None, max_new_tokens=None, system=None, extra_args=()):
+                 seed=None, max_new_tokens=None, system=None, extra_args=(), dump_at=None, dump_dir='.'):
         import torch
         from .qwen_engine import Qwen2Engine
         path = find_engine(engine)
@@ -142,6 +142,12 @@ class NativeEngine:
                      'window_slots': window}
         self.last = None
         self.last_tokens = []
+        # logits dumps (qwen_vk.cpp:891-894, --dump-at / --dump-dir): after the token at session position i is
+        # processed, its fp32 logits row goes to <dump_dir>/logits_<i>.f32 (raw little-endian floats, vocab of them)
+        self.dump_at = frozenset(int(i) for i in (dump_at or ()))
+        self.dump_dir = Path(dump_dir)
+        if self.dump_at and self._shard is not None:
+            raise ValueError('--dump-at is available with full attention only')
 
     # ---------------------------------------------------------------------------------------------- helpers
     def _stop_ids(self, cfg):
@@ -215,8 +221,17 @@ class NativeEngine:
                 raise RuntimeError('nothing to continue from: the session is empty')
             if len(self._seq) > self.positions:
                 raise _ContextFull()
+            start = len(self._seq) - len(pending)
+            dumps = [i for i in range(start, len(self._seq)) if i in self.dump_at]
             if sh is not None:
                 logits = sh.feed(pending)[None]
+                nxt = int(torch.argmax(logits[0])) if greedy else None
+            elif dumps:
+                # every row of the call, for the rows to dump (the K/V-only prefill computes no logits)
+                rows, _ = eng.forward(pending, cache, all_logits=True)
+                for i in dumps:
+                    self._dump(i, rows[i - start])
+                logits = rows[-1:]
                 nxt = int(torch.argmax(logits[0])) if greedy else None
             elif greedy:
                 nxt = int(eng.prefill([pending], [cache])[0])
@@ -242,13 +257,17 @@ class NativeEngine:
                     break
                 if len(self._seq) > self.positions:
                     raise _ContextFull()
+                pos = len(self._seq) - 1
                 if sh is not None:
                     logits = sh.step(int(t))[None]
                     nxt = int(torch.argmax(logits[0])) if greedy else None
-                elif greedy:
+                elif greedy and pos not in self.dump_at:
                     nxt = int(eng.decode([int(t)], [cache])[0])
                 else:
                     logits, _ = eng.forward([int(t)], cache)
+                    nxt = int(torch.argmax(logits[0])) if greedy else None
+                    if pos in self.dump_at:
+                        self._dump(pos, logits[0])
                 self._done = len(self._seq)
         except _ContextFull:
             res['reason'] = 'context'
@@ -301,6 +320,10 @@ class NativeEngine:
     def state(self):
         self._live()
         return {'position': len(self._seq), 'processed': self._done, 'tokens': list(self._seq)}
+
+    def _dump(self, pos, row):
+        self.dump_dir.mkdir(parents=True, exist_ok=True)
+        row.detach().float().cpu().numpy().astype('<f4').tofile(self.dump_dir / f'logits_{pos}.f32')
 
     def _draw(self, logits, sp):
         """One GPU draw from the last logits row (temperature, top-k, top-p) with the next seeded uniform."""

@@ -31,11 +31,38 @@ from . import native_bundle
 GROUP = 32
 
 
+class _KVLayers:
+    """`KVCache.keys` / `KVCache.values` of a cache bound to an engine: item `l` is a copy of layer l's cached keys
+    (values) in the reference's layout, fp16 [1, max(capacity, length), kv_heads, head_dim] on the GPU (reference:
+    qwen_engine.py:18-29), gathered from the engine's HBM ring (position p at slot p mod n_slots).  Positions the ring
+    no longer holds (older than length - n_slots, windowed caches only) and positions not yet written are zero.
+    A copy, not the storage: writing it does not change the cache."""
+
+    def __init__(self, engine, cache, which):
+        self._eng, self._cache, self._which = weakref.ref(engine), weakref.ref(cache), which
+
+    def __len__(self):
+        eng = self._eng()
+        return 0 if eng is None else eng.n_layers
+
+    def __iter__(self):
+        return (self[i] for i in range(len(self)))
+
+    def __getitem__(self, layer):
+        eng, cache = self._eng(), self._cache()
+        if eng is None or cache is None:
+            raise ValueError('the cache is no longer bound to a live engine')
+        if isinstance(layer, slice):
+            return [self[i] for i in range(len(self))[layer]]
+        return eng._kv_copy(cache, layer, self._which)
+
+
 @dataclass
 class KVCache:
     """Per-sequence KV state.  The keys/values live in the engine's HBM ring ([layer][seq][kv_head][slot][head_dim],
-    fp16), so `keys`/`values` are empty lists here; `length` is mutable exactly as in the reference (assigning a
-    smaller value rolls the cache back, experiments/hive_scaling/benchmark_speculative.py:119,127)."""
+    fp16); for a cache from `new_cache`, `keys[l]` / `values[l]` give copies of layer l's in the reference's layout
+    (_KVLayers).  `length` is mutable exactly as in the reference (assigning a smaller value rolls the cache back,
+    experiments/hive_scaling/benchmark_speculative.py:119,127)."""
     keys: list = field(default_factory=list)
     values: list = field(default_factory=list)
     length: int = 0
@@ -286,9 +313,34 @@ class Qwen2Engine:
         elif need > self._pool_slots or not self._free:
             self.grow(self._pool_n if self._free else 2 * self._pool_n, need)
         cache = KVCache([], [], 0, capacity, window, self._free.pop(), self._epoch)
+        cache.keys, cache.values = _KVLayers(self, cache, 'k'), _KVLayers(self, cache, 'v')
         self._live[cache.seq] = cache
         weakref.finalize(cache, self._release, cache.seq, cache.epoch)
         return cache
+
+    def _kv_copy(self, cache, layer, which):
+        """Layer `layer`'s keys ('k') or values ('v') of `cache`, copied out of the HBM ring (see _KVLayers)."""
+        self._check_cache(cache)
+        L = self.n_layers
+        if not -L <= layer < L:
+            raise IndexError('layer out of range')
+        layer %= L
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(self.lib.sp_engine_kv_layer(self.h, layer, ctypes.byref(k), ctypes.byref(v)), self.h)
+        N, S, NKV, HD = self._pool_n, self._pool_slots, self.n_kv_heads, self.head_dim
+
+        class _Pool:
+            __cuda_array_interface__ = {'shape': (N, NKV, S, HD), 'typestr': '<f2',
+                                        'data': ((k if which == 'k' else v).value, False), 'version': 3,
+                                        'strides': None}
+        pool = torch.as_tensor(_Pool(), device=self.device)
+        n = cache.length
+        out = torch.zeros((1, max(cache.capacity, n), NKV, HD), dtype=torch.float16, device=self.device)
+        first = max(0, n - S)
+        if n > first:
+            slots = torch.arange(first, n, device=self.device) % S
+            out[0, first:n] = pool[cache.seq][:, slots].permute(1, 0, 2)
+        return out
 
     def _release(self, seq, epoch):
         if epoch == self._epoch and seq not in self._free:

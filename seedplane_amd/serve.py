@@ -35,8 +35,10 @@ else:
     from .native import NativeEngine
 
 _FLAGS = {'--mode': 'mode', '--ctx': 'ctx', '--temperature': 'temperature', '--top-k': 'top_k', '--top-p': 'top_p',
-          '--seed': 'seed', '-n': 'max_new_tokens', '--system': 'system'}
-_CONVERT = {'ctx': int, 'temperature': float, 'top_k': int, 'top_p': float, 'seed': int, 'max_new_tokens': int}
+          '--seed': 'seed', '-n': 'max_new_tokens', '--system': 'system', '--dump-at': 'dump_at',
+          '--dump-dir': 'dump_dir'}
+_CONVERT = {'ctx': int, 'temperature': float, 'top_k': int, 'top_p': float, 'seed': int, 'max_new_tokens': int,
+            'dump_at': lambda v: [int(x) for x in v.split(',') if x]}
 _SAMPLING = ('temperature', 'top_k', 'top_p', 'seed')
 
 
@@ -44,7 +46,7 @@ def parse_args(argv):
     """(bundle, NativeEngine keyword arguments) from the reference engine's command line (qwen_vk.cpp:665-688)."""
     if not argv:
         raise ValueError('usage: serve <bundle> --serve [--mode M] [--full] [--ctx N] [--temperature T] [--top-k K] '
-                         '[--top-p P] [--seed S] [-n N] [--system TEXT]')
+                         '[--top-p P] [--seed S] [-n N] [--system TEXT] [--dump-at p1,p2 --dump-dir d]')
     bundle, kw, serve, i = argv[0], {}, False, 1
     while i < len(argv):
         a = argv[i]

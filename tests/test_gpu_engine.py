@@ -156,3 +156,41 @@ def test_new_cache_growth_keeps_live_caches(small):
     for c in more:                                            # the new caches work too
         out, _ = eng.forward(ids[:3], c)
         assert torch.isfinite(out).all()
+
+
+def test_cache_tensors_read_back_in_reference_layout(small):
+    """KVCache.keys[l] / values[l] (reference: per-layer [1, capacity, kv_heads, head_dim] tensors) read back the
+    engine's ring: the oracle's cached (rotated) keys and values at every written position, zeros after `length`;
+    a windowed cache holds its last n_slots positions.  Copies: writing one leaves the cache unchanged."""
+    fmt, cfg, eng, ref = small
+    ids = random_prompt(21, cfg['vocab_size'], seed=31)
+    cache = eng.new_cache(40)
+    eng.forward(ids[:13], cache)
+    for t in ids[13:]:
+        eng.decode([t], [cache])
+    rc = ref.new_cache(40)
+    ref.forward(ids, rc)
+    L, NKV, HD = cfg['num_hidden_layers'], cfg['num_key_value_heads'], cfg['hidden_size'] // cfg['num_attention_heads']
+    assert len(cache.keys) == len(cache.values) == L
+    n = len(ids)
+    for l in range(L):
+        k, v = cache.keys[l], cache.values[l]
+        assert k.shape == (1, 40, NKV, HD) and k.dtype == torch.float16
+        assert max_rel(k[0, :n].float().cpu(), rc.keys[l][0, :n]) < TOL, l
+        assert max_rel(v[0, :n].float().cpu(), rc.values[l][0, :n]) < TOL, l
+        assert not k[0, n:].any() and not v[0, n:].any()
+    k0 = cache.keys[-1].clone()
+    cache.keys[-1].zero_()
+    assert torch.equal(cache.keys[-1], k0)
+    W = 8
+    wc = eng.new_cache(4096, window=W)
+    eng.forward(ids, wc)
+    S = eng.slots_for(4096, W)
+    first = max(0, n - S)
+    for l in (0, L - 1):
+        k = wc.keys[l]
+        assert k.shape[1] == 4096
+        assert not k[0, :first].any()
+        # layer 0's keys depend only on each position's own token, so the ring holds the full cache's keys there
+        if l == 0:
+            assert max_rel(k[0, first:n].float().cpu(), rc.keys[0][0, first:n]) < TOL

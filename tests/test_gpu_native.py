@@ -127,3 +127,26 @@ def test_sharded_modes_follow_the_bundle_plan(gpu_device, tmp_path, mode):
         eng.reset()
         list(eng.generate(ids=prompt, stop=[]))
         assert eng.last_tokens == ref
+
+
+def test_dump_at_writes_the_logits_rows(gpu_device, tmp_path):
+    """--dump-at / --dump-dir (qwen_vk.cpp:891-894): after the token at position i is processed, logits_<i>.f32
+    holds that step's fp32 logits row; positions inside the prompt and generated ones, greedy ids unchanged."""
+    d, cfg, _ = _bundle(tmp_path)
+    V = cfg['vocab_size']
+    prompt = random_prompt(9, V - len(SPECIAL), seed=4)
+    out = tmp_path / 'dumps'
+    with NativeEngine(d, max_new_tokens=6, ctx=256, dump_at=[3, 8, 11], dump_dir=str(out)) as eng:
+        ''.join(eng.generate(ids=prompt, stop=[]))
+        gen = list(eng.last_tokens)
+    seq = prompt + gen
+    rows, _ = Qwen2Engine(d).forward(seq, all_logits=True)
+    for j, t in enumerate(gen):                      # greedy: each id is its row's argmax up to a near-tie
+        row = rows[len(prompt) - 1 + j].cpu()
+        if t != int(torch.argmax(row)):
+            assert top2_margin(row) <= TOL * float(row.abs().max()), j
+    for i in (3, 8, 11):
+        got = torch.from_numpy(__import__('numpy').fromfile(out / f'logits_{i}.f32', dtype='<f4'))
+        assert got.shape == (V,)
+        assert float((got - rows[i].cpu()).abs().max()) <= TOL * float(rows[i].abs().max()), i
+    assert sorted(p.name for p in out.iterdir()) == ['logits_11.f32', 'logits_3.f32', 'logits_8.f32']

@@ -42,3 +42,13 @@ def test_forest_through_the_reference_path():
         return out
     v = verify_greedy([7], forest, logits)
     assert v.emitted == (1, 2, 3)          # the whole path accepted; no correction token
+
+
+def test_kvcache_keeps_the_reference_dataclass_signature():
+    from seedplane.qwen_engine import KVCache
+    c = KVCache([], [], 0, 16)                       # qwen_engine.py:18-23 field order
+    assert (c.keys, c.values, c.length, c.capacity) == ([], [], 0, 16)
+    a = KVCache.allocate(2, 32, 2, 64, 'cpu', None)
+    assert a.capacity == 32 and a.length == 0
+    a.length = 5                                     # rollback by assignment, as the reference does
+    assert a.length == 5

@@ -105,6 +105,9 @@ def test_parse_args():
     assert kw == {'mode': 'shadow', 'ctx': 512, 'temperature': 0.7, 'top_k': 20, 'top_p': 0.9, 'seed': 3,
                   'max_new_tokens': 16, 'system': 'Be brief.'}
     assert serve.parse_args(['m.sp', '--full', '--serve'])[1] == {'full': True}
+    # the reference engine's logits dumps (qwen_vk.cpp:21,674): positions as a comma list, and their directory
+    assert serve.parse_args(['m.sp', '--serve', '--dump-at', '3,17', '--dump-dir', '/tmp/d'])[1] == {
+        'dump_at': [3, 17], 'dump_dir': '/tmp/d'}
     for bad in ([], ['m.sp'], ['m.sp', '--serve', '--bogus'], ['m.sp', '--serve', '--ctx']):
         with pytest.raises(ValueError):
             serve.parse_args(bad)
