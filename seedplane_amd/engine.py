@@ -15,9 +15,13 @@ window's slots [0, j].  What happens at a shard boundary is a host-side slot pol
                       starts with the sinks), as a second column of the same engine call; at the boundary that cache
                       simply becomes the current one -- no recomputation (the reference's ShadowBatch).
 
-The reference's approximate 'reuse' mode (halo K/V carried over from the previous window, computed under that
-window's context) is not provided: its results depend on K/V computed with a different visible set, which the
-exact modes above avoid at the cost of at most H + K extra token columns per boundary.
+  'reuse'    (approximate, as the reference calls it) the new window's sinks and halo are COPIES of the K/V the
+                      earlier windows computed (sinks saved from the first window, the halo from the current one;
+                      qwen_vk.cpp:537-542): no recomputation, but a halo token's K/V were computed under its own
+                      shard's visible set, not the new window's.  Every position's K/V is then computed exactly once,
+                      when it is processed, so the mode equals one causal pass in which token i attends to
+                      plan.visible(i) -- what the tests check it against.  Needs halo <= shard and sinks <= shard
+                      (the copied slots must lie in the current window), as the reference requires.
 """
 from dataclasses import dataclass
 
@@ -65,11 +69,13 @@ class ShardedSession:
     """Token-at-a-time processing under a ShardPlan on a Qwen2Engine (qwen_vk.cpp:505-565).  `step` returns the
     fp32 logits row of the token when asked for it (else None, and the token is only written to the K/V cache)."""
 
-    MODES = ('rebuild', 'shadow')
+    MODES = ('rebuild', 'shadow', 'reuse')
 
     def __init__(self, engine, plan, mode='rebuild'):
         if mode not in self.MODES:
             raise ValueError(f'bad mode {mode!r} (expected one of {self.MODES})')
+        if mode == 'reuse' and (plan.halo > plan.shard or plan.sinks > plan.shard):
+            raise ValueError('reuse needs halo <= shard and sinks <= shard')
         self.e, self.plan, self.mode = engine, plan, mode
         self.capacity = plan.sinks + plan.halo + plan.shard
         if self.capacity > engine.config['max_position_embeddings']:
@@ -84,6 +90,8 @@ class ShardedSession:
         self.boundaries = 0           # shard boundaries crossed
         self.extra = 0                # token columns recomputed at boundaries (rebuild)
         self.dual = 0                 # tokens written to two windows (shadow)
+        self.reused = 0               # K/V slots copied at boundaries (reuse)
+        self._sinks = None            # per layer (K, V) of the first min(sinks, shard) positions (reuse)
         self._row = torch.empty((2, engine.vocab), dtype=torch.float32, device=engine.device)
 
     @property
@@ -109,11 +117,43 @@ class ShardedSession:
         self._kv_only(cache, [(self.seq[j], j) for j in range(ns)])
         return cache
 
+    def _reuse_window(self, i):
+        """The window of the shard starting at i, filled by copies (qwen_vk.cpp:524,537-542): slots [0, ns) the
+        sinks saved from the first window, slots [ns, ns + i - h0) the halo [h0, i) from the current window, where
+        the current shard's tokens sit after its sinks and halo."""
+        S, e = self.plan.shard, self.e
+        ns, h0 = self.plan.sinks_of(i), max(0, i - self.plan.halo)
+        pre = self.cur.length - S                # the current window's slots before its shard's tokens
+        old = self.cur
+        nxt = e.new_cache(self.capacity)         # (may grow the pool: the views below are taken after it)
+        src = torch.arange(pre + h0 - (i - S), pre + S, device=e.device)
+        for l in range(e.n_layers):
+            kp, vp = e._kv_pool(l)
+            for pool, which in ((kp, 0), (vp, 1)):
+                if ns:
+                    pool[nxt.seq][:, :ns] = self._sinks[l][which][:, :ns]
+                pool[nxt.seq][:, ns:ns + i - h0] = pool[old.seq][:, src]
+        nxt.length = ns + i - h0
+        self.reused += nxt.length
+        return nxt
+
+    def _save_sinks(self):
+        """K/V of the first min(sinks, shard) positions, from the first window (whose slot j holds position j)."""
+        K = min(self.plan.sinks, self.plan.shard)
+        self._sinks = []
+        for l in range(self.e.n_layers):
+            kp, vp = self.e._kv_pool(l)
+            self._sinks.append((kp[self.cur.seq][:, :K].clone(), vp[self.cur.seq][:, :K].clone()))
+
     def step(self, token, need_logits=True):
         i, S, H = self.done, self.plan.shard, self.plan.halo
         if i > 0 and i % S == 0:
             self.boundaries += 1
-            if self.mode == 'shadow' and self.shadow is not None:
+            if self.mode == 'reuse':
+                if self._sinks is None:
+                    self._save_sinks()
+                self.cur = self._reuse_window(i)
+            elif self.mode == 'shadow' and self.shadow is not None:
                 self.cur, self.shadow = self.shadow, None
             else:                      # rebuild (or a shadow that never started: halo 0)
                 h0 = max(0, i - H)

@@ -19,8 +19,8 @@ file).  Without it, generation from token ids still works: tokens are recorded i
 yielded; tokenize / detokenize / chat raise RuntimeError.
 
 The attention is full over `ctx` positions unless a shard-window mode is asked for (qwen_vk.cpp:686-690): 'rebuild' /
-'rebuild-batch' and 'shadow' / 'shadow-batch' run the exact boundary policies of seedplane_amd.engine.ShardedSession
-with the bundle's plan (seedplane.json) or the default ShardPlan; the approximate 'reuse' mode raises ValueError.
+'rebuild-batch' and 'shadow' / 'shadow-batch' run the exact boundary policies of seedplane_amd.engine.ShardedSession,
+'reuse' its approximate copy policy, with the bundle's plan (seedplane.json) or the default ShardPlan.
 Sampling at temperature > 0 (top-k / top-p) draws on the GPU with counter-based uniforms u(seed, draw counter).
 """
 import ctypes.util
@@ -89,9 +89,6 @@ class NativeEngine:
         from .qwen_engine import Qwen2Engine
         path = find_engine(engine)
         if mode is not None and mode != 'full':
-            if mode == 'reuse':
-                raise ValueError("mode 'reuse' (approximate halo reuse) is not available in this engine: use "
-                                 "'rebuild' or 'shadow' (exact), or full attention")
             if mode not in _MODES:
                 raise ValueError(f'bad mode {mode!r}')
         sharded = mode not in (None, 'full') and not full
@@ -129,7 +126,8 @@ class NativeEngine:
             plan = (native_bundle.read_manifest(self.bundle)['plan'] if native_bundle.is_bundle(self.bundle)
                     else {'shard': 512, 'halo': 256, 'sinks': 4})
             self._plan = ShardPlan(int(plan['shard']), int(plan['halo']), int(plan['sinks']))
-            self._shard_mode = 'rebuild' if mode.startswith('rebuild') else 'shadow'
+            self._shard_mode = ('rebuild' if mode.startswith('rebuild') else 'reuse' if mode == 'reuse'
+                                else 'shadow')
             self._shard = ShardedSession(self.engine, self._plan, self._shard_mode)
             window = self._shard.capacity
             plan_info = {'shard': self._plan.shard, 'halo': self._plan.halo, 'sinks': self._plan.sinks}

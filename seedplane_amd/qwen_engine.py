@@ -318,22 +318,29 @@ class Qwen2Engine:
         weakref.finalize(cache, self._release, cache.seq, cache.epoch)
         return cache
 
+    def _kv_pool(self, layer):
+        """Layer `layer`'s K and V pools as fp16 [n_seq, kv_heads, n_slots, head_dim] tensors sharing the engine's
+        memory.  Internal: valid only until the pool is reserved or grown again, so callers drop them at once."""
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(self.lib.sp_engine_kv_layer(self.h, layer, ctypes.byref(k), ctypes.byref(v)), self.h)
+        shape = (self._pool_n, self.n_kv_heads, self._pool_slots, self.head_dim)
+
+        def view(ptr):
+            class _Pool:
+                __cuda_array_interface__ = {'shape': shape, 'typestr': '<f2', 'data': (ptr.value, False),
+                                            'version': 3, 'strides': None}
+            return torch.as_tensor(_Pool(), device=self.device)
+        return view(k), view(v)
+
     def _kv_copy(self, cache, layer, which):
         """Layer `layer`'s keys ('k') or values ('v') of `cache`, copied out of the HBM ring (see _KVLayers)."""
         self._check_cache(cache)
         L = self.n_layers
         if not -L <= layer < L:
             raise IndexError('layer out of range')
-        layer %= L
-        k, v = ctypes.c_void_p(), ctypes.c_void_p()
-        _lib.check(self.lib.sp_engine_kv_layer(self.h, layer, ctypes.byref(k), ctypes.byref(v)), self.h)
-        N, S, NKV, HD = self._pool_n, self._pool_slots, self.n_kv_heads, self.head_dim
-
-        class _Pool:
-            __cuda_array_interface__ = {'shape': (N, NKV, S, HD), 'typestr': '<f2',
-                                        'data': ((k if which == 'k' else v).value, False), 'version': 3,
-                                        'strides': None}
-        pool = torch.as_tensor(_Pool(), device=self.device)
+        kp, vp = self._kv_pool(layer % L)
+        pool = kp if which == 'k' else vp
+        S, NKV, HD = self._pool_slots, self.n_kv_heads, self.head_dim
         n = cache.length
         out = torch.zeros((1, max(cache.capacity, n), NKV, HD), dtype=torch.float16, device=self.device)
         first = max(0, n - S)

@@ -111,7 +111,7 @@ def test_tokenizer_chat_and_errors(gpu_device, tmp_path):
         eng.state()                                         # closed
 
 
-@pytest.mark.parametrize('mode', ['shadow-batch', 'rebuild'])
+@pytest.mark.parametrize('mode', ['shadow-batch', 'rebuild', 'reuse'])
 def test_sharded_modes_follow_the_bundle_plan(gpu_device, tmp_path, mode):
     from seedplane_amd import native_bundle
     from seedplane_amd.engine import ShardPlan, ShardedSession

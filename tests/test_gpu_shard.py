@@ -44,6 +44,38 @@ def test_session_matches_window_oracle(model, mode, shard, halo, sinks):
         assert s.dual > 0
 
 
+def _masked_rows(ref, ids, plan):
+    """The reuse mode's oracle: one causal pass in which token i attends to plan.visible(i), so every position's
+    K/V are computed once, under its own window (what copying them between windows keeps)."""
+    n = len(ids)
+    allowed = torch.zeros((n, n), dtype=torch.bool)
+    for i in range(n):
+        allowed[i, plan.visible(i)] = True
+    return ref.forward_masked(ids, ref.new_cache(n), list(range(n)), allowed)
+
+
+@pytest.mark.parametrize('shard,halo,sinks', [(8, 4, 2), (6, 6, 3), (5, 0, 1), (7, 3, 0)])
+def test_reuse_matches_masked_pass(model, shard, halo, sinks):
+    cfg, eng, ref = model
+    print(f'shard session reuse S={shard} H={halo} K={sinks}', flush=True)
+    plan = ShardPlan(shard, halo, sinks)
+    ids = random_prompt(30, cfg['vocab_size'], seed=3 * shard + halo)
+    s = ShardedSession(eng, plan, 'reuse')
+    rows = _masked_rows(ref, ids, plan)
+    for i, t in enumerate(ids):
+        row = s.step(t, need_logits=(i % 2 == 1 or i == len(ids) - 1))
+        if row is not None:
+            err = max_rel(row[None], rows[i][None])
+            assert err < 2e-2, (i, err)
+    assert s.boundaries == (len(ids) - 1) // shard and s.extra == 0
+    assert s.reused == sum(plan.sinks_of(c) + c - max(0, c - halo) for c in range(shard, len(ids), shard))
+    if halo > 0:
+        # two boundaries in, the reused halo K/V (computed under the previous window's visible set) differ from the
+        # exact policy's, which recomputes them under the new window's sinks: the mode is approximate
+        i = 2 * shard + 1
+        assert max_rel(rows[i][None], _window_row(ref, ids, plan, i)[None]) > 1e-3
+
+
 def test_one_shard_equals_plain_forward(model):
     cfg, eng, ref = model
     ids = random_prompt(20, cfg['vocab_size'], seed=9)

@@ -41,6 +41,4 @@ def test_chat_turn_template():
 
 def test_bad_mode_is_rejected_before_loading(tmp_path):
     with pytest.raises(ValueError):
-        native.NativeEngine(tmp_path, mode='reuse')          # the approximate boundary mode is not provided
-    with pytest.raises(ValueError):
         native.NativeEngine(tmp_path, mode='bogus')

@@ -39,6 +39,11 @@ def test_visible_is_the_window_prefix(shard, halo, sinks):
             assert len(plan.visible(i)) <= shard + halo + sinks
 
 
-def test_session_rejects_unknown_modes():
+def test_session_rejects_unknown_modes_and_reuse_plans_it_cannot_copy():
     with pytest.raises(ValueError):
-        ShardedSession(None, ShardPlan(), mode='reuse')
+        ShardedSession(None, ShardPlan(), mode='bogus')
+    # reuse copies the halo and the sinks out of one window: both must fit a shard (qwen_vk.cpp:297)
+    with pytest.raises(ValueError, match='halo <= shard'):
+        ShardedSession(None, ShardPlan(shard=4, halo=10, sinks=3), mode='reuse')
+    with pytest.raises(ValueError, match='sinks <= shard'):
+        ShardedSession(None, ShardPlan(shard=4, halo=2, sinks=6), mode='reuse')
