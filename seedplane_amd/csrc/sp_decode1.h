@@ -45,6 +45,7 @@
 // most two tiles (or one row group) of MFMA results in flight.
 #pragma once
 #include <algorithm>
+#include <cstddef>
 #include <type_traits>
 #include <vector>
 
@@ -498,13 +499,18 @@ __device__ __forceinline__ float tile_scale(const Tiles<FMT, T> &tl, int t, int 
 
 // A operand of step st of the wave's tile t of the staged input (xh / xl, k measured from the staged input's start =
 // tile kt0): row 0 the fp16 values, row 1 their remainders, rows 2..15 (and dead tiles) the zero line.
+// The three sources are picked by integer selects on one byte offset from xh, not by choosing among pointers: a
+// pointer choice compiled to divergent branches around every read, which kept the read from being issued ahead of
+// the MFMAs before it (each step then paid the full LDS latency).
 template <int FMT, int T>
 __device__ __forceinline__ f16x8 x_operand(const Smem &s, int t, int st, bool live, int wv, int lane, int kdep) {
     constexpr int KT = TileGeom<FMT>::KT;
+    constexpr int XL = (int)((offsetof(Smem, xl) - offsetof(Smem, xh)) / sizeof(f16));
     const int r = lane & 15, g = lane >> 4;
     const int xo = (wv * T + t) * KT + st * 32 + 8 * g + kdep;
-    const f16 *src = !live || r > 1 ? s.xh + MAX_K : (r == 0 ? s.xh + xo : s.xl + xo);
-    return *(const f16x8 *)src;
+    int o = r == 0 ? xo : XL + xo;
+    o = !live || r > 1 ? MAX_K : o;
+    return *(const f16x8 *)((const char *)&s + offsetof(Smem, xh) + 2 * o);
 }
 
 // One row group's partial dot product with the staged input over the wave's T tiles: lanes 0..15 return the sums of
@@ -517,25 +523,40 @@ __device__ __forceinline__ float stream_dot(const Smem &s, Tiles<FMT, T> &tl, in
     float acc = 0.f;
     f32x4 acc4 = (f32x4){0.f, 0.f, 0.f, 0.f};
     int kdep[2] = {0, 0};
+    // software-pipelined like the LDS-tile version below: tile t + 1's A operands are read before tile t's MFMAs
+    auto read = [&](int t, f16x8 (&xa)[ST]) {
+#pragma unroll
+        for (int st = 0; st < ST; ++st) xa[st] = x_operand<FMT, T>(s, t, st, t < tl.nvalid, wv, lane, kdep[t & 1]);
+    };
+    f16x8 xa_cur[ST], xa_nxt[ST];
+    read(0, xa_cur);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const bool live = t < tl.nvalid;
+        if (t + 1 < T) read(t + 1, xa_nxt);
+        if constexpr (FMT == 1) {
 #pragma unroll
-        for (int st = 0; st < ST; ++st) {
-            const f16x8 xa = x_operand<FMT, T>(s, t, st, live, wv, lane, kdep[t & 1]);
-            if constexpr (FMT == 1) {
-                acc4 = mfma16(xa, __builtin_bit_cast(f16x8, tl.wt[t]), acc4);
-            } else {
-                const f32x4 sx = mfma16(xa, ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
-                const f32x4 dd = mfma16(xa, biased_step<FMT>(tl.wt[t], st), (f32x4){0.f, 0.f, 0.f, 0.f});
+            for (int st = 0; st < ST; ++st) acc4 = mfma16(xa_cur[st], __builtin_bit_cast(f16x8, tl.wt[t]), acc4);
+        } else {
+            f32x4 sx[ST], dd[ST];
+#pragma unroll
+            for (int st = 0; st < ST; ++st) {
+                sx[st] = mfma16(xa_cur[st], ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                dd[st] = mfma16(xa_cur[st], biased_step<FMT>(tl.wt[t], st), (f32x4){0.f, 0.f, 0.f, 0.f});
+            }
+#pragma unroll
+            for (int st = 0; st < ST; ++st) {
                 float offs;
                 const float scale = tile_scale<FMT, T>(tl, t, st, offs);
-                acc = fmaf(scale, fmaf(-offs, sx[0], dd[0]) + fmaf(-offs, sx[1], dd[1]), acc);
+                acc = fmaf(scale, fmaf(-offs, sx[st][0], dd[st][0]) + fmaf(-offs, sx[st][1], dd[st][1]), acc);
             }
         }
         const float v = FMT == 1 ? acc4[0] : acc;
         asm volatile("" : "+v"(kdep[t & 1]) : "v"(v));
         if (t + 2 < T) tl.after(t + 2, v);
+        if (t + 1 < T) {
+#pragma unroll
+            for (int st = 0; st < ST; ++st) xa_cur[st] = xa_nxt[st];
+        }
     }
     return FMT == 1 ? acc4[0] + acc4[1] : acc;
 }
@@ -591,7 +612,11 @@ __device__ __forceinline__ float tile_scale(const LdsTiles<FMT, T> &tl, int t, i
         return (float)__builtin_bit_cast(f16, (uint16_t)(d & 0xffffu));
     }
 }
-// stream_dot over LDS tiles: tile t + 2's weights and activations are read after tile t's sum.
+// stream_dot over LDS tiles, software-pipelined: iteration t first reads tile t + 1's weights and A operands (their
+// reads wait for tile t - 1's sum, which bounds the operands in flight to two tiles), then issues tile t's MFMAs on
+// the operands read one iteration earlier, then adds their results.  The reads of one tile thus overlap the matrix
+// work of the tile before it (written step by step, the compiler kept every read behind the previous step's
+// results).  Same sums in the same order as the register-tile version.
 template <int FMT, int T>
 __device__ __forceinline__ float stream_dot(const Smem &s, const LdsTiles<FMT, T> &tl, int wv, int lane) {
     constexpr int ST = TileGeom<FMT>::STEPS;
@@ -600,25 +625,42 @@ __device__ __forceinline__ float stream_dot(const Smem &s, const LdsTiles<FMT, T
     f32x4 acc4 = (f32x4){0.f, 0.f, 0.f, 0.f};
     int kdep[2] = {0, 0};
     copy_wait();
+    auto read = [&](int t, u32x4 &wt, f16x8 (&xa)[ST]) {
+        const int kd = kdep[t & 1];
+        wt = *(const u32x4 *)(tl.lds + (wv * T + t) * TILE_BYTES + lane * 16 + 4 * kd);
+#pragma unroll
+        for (int st = 0; st < ST; ++st) xa[st] = x_operand<FMT, T>(s, t, st, t < tl.nvalid, wv, lane, kd);
+    };
+    u32x4 wt_cur, wt_nxt;
+    f16x8 xa_cur[ST], xa_nxt[ST];
+    read(0, wt_cur, xa_cur);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const bool live = t < tl.nvalid;
-        const u32x4 wt = *(const u32x4 *)(tl.lds + (wv * T + t) * TILE_BYTES + lane * 16 + 4 * kdep[t & 1]);
+        if (t + 1 < T) read(t + 1, wt_nxt, xa_nxt);
+        if constexpr (FMT == 1) {
 #pragma unroll
-        for (int st = 0; st < ST; ++st) {
-            const f16x8 xa = x_operand<FMT, T>(s, t, st, live, wv, lane, kdep[t & 1]);
-            if constexpr (FMT == 1) {
-                acc4 = mfma16(xa, __builtin_bit_cast(f16x8, wt), acc4);
-            } else {
-                const f32x4 sx = mfma16(xa, ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
-                const f32x4 dd = mfma16(xa, biased_step<FMT>(wt, st), (f32x4){0.f, 0.f, 0.f, 0.f});
+            for (int st = 0; st < ST; ++st) acc4 = mfma16(xa_cur[st], __builtin_bit_cast(f16x8, wt_cur), acc4);
+        } else {
+            f32x4 sx[ST], dd[ST];
+#pragma unroll
+            for (int st = 0; st < ST; ++st) {
+                sx[st] = mfma16(xa_cur[st], ones8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                dd[st] = mfma16(xa_cur[st], biased_step<FMT>(wt_cur, st), (f32x4){0.f, 0.f, 0.f, 0.f});
+            }
+#pragma unroll
+            for (int st = 0; st < ST; ++st) {
                 float offs;
                 const float scale = tile_scale<FMT, T>(tl, t, st, offs);
-                acc = fmaf(scale, fmaf(-offs, sx[0], dd[0]) + fmaf(-offs, sx[1], dd[1]), acc);
+                acc = fmaf(scale, fmaf(-offs, sx[st][0], dd[st][0]) + fmaf(-offs, sx[st][1], dd[st][1]), acc);
             }
         }
         const float v = FMT == 1 ? acc4[0] : acc;
         asm volatile("" : "+v"(kdep[t & 1]) : "v"(v));
+        if (t + 1 < T) {
+            wt_cur = wt_nxt;
+#pragma unroll
+            for (int st = 0; st < ST; ++st) xa_cur[st] = xa_nxt[st];
+        }
     }
     return FMT == 1 ? acc4[0] + acc4[1] : acc;
 }
@@ -651,19 +693,29 @@ __device__ __forceinline__ float group_dot(const XOps<FMT, T> &x, const Tiles<FM
     constexpr int ST = TileGeom<FMT>::STEPS;
     float acc = 0.f;
     f32x4 acc4 = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if constexpr (FMT == 1) {
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+        for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int st = 0; st < ST; ++st) {
-            if constexpr (FMT == 1) {
-                acc4 = mfma16(x.a[t][st], __builtin_bit_cast(f16x8, tl.wt[t]), acc4);
-            } else {
-                const f32x4 dd = mfma16(x.a[t][st], biased_step<FMT>(tl.wt[t], st), (f32x4){0.f, 0.f, 0.f, 0.f});
+            for (int st = 0; st < ST; ++st) acc4 = mfma16(x.a[t][st], __builtin_bit_cast(f16x8, tl.wt[t]), acc4);
+    } else {
+        // every MFMA of the group first, then the sums in the same order: the products overlap in the matrix core
+        // instead of each waiting for the one before it to be read
+        f32x4 dd[T][ST];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int st = 0; st < ST; ++st)
+                dd[t][st] = mfma16(x.a[t][st], biased_step<FMT>(tl.wt[t], st), (f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int st = 0; st < ST; ++st) {
                 float offs;
                 const float scale = tile_scale<FMT, T>(tl, t, st, offs);
-                acc = fmaf(scale, fmaf(-offs, x.s0[t][st], dd[0]) + fmaf(-offs, x.s1[t][st], dd[1]), acc);
+                acc = fmaf(scale, fmaf(-offs, x.s0[t][st], dd[t][st][0]) + fmaf(-offs, x.s1[t][st], dd[t][st][1]), acc);
             }
-        }
+    }
     return FMT == 1 ? acc4[0] + acc4[1] : acc;
 }
 
