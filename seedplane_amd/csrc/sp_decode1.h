@@ -940,20 +940,29 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                         const float lsum = wave_sum_dpp(ex);
                         s.es[h][lane] = ex;
                         __builtin_amdgcn_wave_barrier();
+                        // lane: dims DPL * lane .. DPL * lane + DPL - 1, read together (one 2- or 4-byte LDS read per
+                        // key: the loop is bound by LDS instructions, not by its FMAs); each dim's sum runs over the
+                        // keys in order
                         constexpr int DPL = HD / 64;
+                        typedef std::conditional_t<DPL == 2, f16x2, f16> VT;
                         float o[DPL];
 #pragma unroll
                         for (int i = 0; i < DPL; ++i) o[i] = 0.f;
                         for (int j = 0; j < cnt; ++j) {
                             const float p = s.es[h][j];
-#pragma unroll
-                            for (int i = 0; i < DPL; ++i) o[i] += p * (float)s.vs[j][lane + 64 * i];
+                            const VT vv = *(const VT *)&s.vs[j][DPL * lane];
+                            if constexpr (DPL == 2) {
+                                o[0] += p * (float)vv[0];
+                                o[1] += p * (float)vv[1];
+                            } else {
+                                o[0] += p * (float)vv;
+                            }
                         }
                         const float il = lsum > 0.f ? 1.f / lsum : 0.f;
                         const unsigned tp = tag_of(seq, l, PH_PART);
                         const int qh = kvh * G + h;
 #pragma unroll
-                        for (int i = 0; i < DPL; ++i) st_word(ll + w_part(g, qh, c, 2 + lane + 64 * i), o[i] * il, tp);
+                        for (int i = 0; i < DPL; ++i) st_word(ll + w_part(g, qh, c, 2 + DPL * lane + i), o[i] * il, tp);
                         if (lane == 0) {
                             st_word(ll + w_part(g, qh, c, 0), m, tp);
                             st_word(ll + w_part(g, qh, c, 1), lsum, tp);
