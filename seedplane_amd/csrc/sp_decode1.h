@@ -763,6 +763,8 @@ __device__ __forceinline__ bool gate_up(Smem &s, CStatic *S, const Geom &g, CLay
     float xm[1][NPT];
     if (!gather_r<NPT, 1>(S->err, rg, xm, tid)) return false;
     prenorm_pairs(s, xm[0], g.H, nw, tid);
+    // the norm's scale is final once prenorm_pairs' barrier has passed: taken now, it is off the epilogue's path
+    const float rs = norm_scale(s, g.H, S->eps);
     XOps<FMT, TH> xo;
     xo.load(s, tg[0].nvalid, wv, lane);
     // one row group at a time: group j + 1's products start after group j's sum (absent units are skipped by
@@ -784,7 +786,6 @@ __device__ __forceinline__ bool gate_up(Smem &s, CStatic *S, const Geom &g, CLay
     if (tid < 16 * NG) {
         // lane 16 i + r: row r of unit i; rows r (even) and r + 1 go out as one word of two 24-bit values
         const int i = tid >> 4;
-        const float rs = norm_scale(s, g.H, S->eps);
         const float gt = rs * wave_total(s, 2 * MAXU, 2 * i, r), up = rs * wave_total(s, 2 * MAXU, 2 * i + 1, r);
         const uint32_t a = f24_of(silu_f(gt) * up);
         const uint32_t an = (uint32_t)__shfl_xor((int)a, 1);
