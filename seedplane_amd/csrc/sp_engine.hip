@@ -118,7 +118,9 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
     GemvPlan p;
     p.rg = m.paired ? 2 : 1;
     p.units = m.rows_pad / 16 / p.rg;
-    if (mt == 1) p.r = p.units >= 2048 && p.units % 2 == 0 ? 2 : 1;
+    // one column tile: two units per wave for the LM head and for the fp16 SwiGLU pair (whose 8-k-tile batches they
+    // share; see GemvBatch)
+    if (mt == 1) p.r = (p.units >= 2048 || (m.paired && m.fmt == 1)) && p.units % 2 == 0 ? 2 : 1;
     // the head at 2-3 column tiles: 4 units per wave (each activation fragment feeds 4 weight tiles); the int4 and
     // 4-tile variants would spill registers
     else if (!split_ok && !m.paired && p.units % 4 == 0 && mt <= 3 && m.fmt != 3) p.r = 4;
