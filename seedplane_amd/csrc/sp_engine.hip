@@ -141,7 +141,9 @@ GemvPlan plan_gemv(const DevMat &m, int mt, bool split_ok, int slices = 0, int w
     // One column tile of a split matrix whose slices hold >= 16 k-tiles (the down projection at 2-16 columns): 8
     // waves as well (sweep of single launches, 8 and 16 columns: 1.5B int8 down 6.04 -> 5.60 and 6.59 -> 6.10 us,
     // 0.5B fp16 down 4.42 -> 4.20 and 4.65 -> 4.42; int4 not swept, so it keeps 4).
-    const bool wide = mt > 1 ? m.fmt != 3 && (p.kslice >= 32 || s > 1) : m.fmt != 3 && s > 1 && p.kslice >= 16;
+    // The int4 SwiGLU pair at several column tiles: 8 waves (7B at 32 columns, one k-tile per batch: 34.3 -> 32.2 us).
+    const bool wide = mt > 1 ? (m.fmt != 3 && (p.kslice >= 32 || s > 1)) || (m.fmt == 3 && m.paired)
+                             : m.fmt != 3 && s > 1 && p.kslice >= 16;
     int nw = std::min(p.kslice, wide ? 8 : 4);
     if (waves > 0) nw = std::min(p.kslice, std::min(waves, mt == 1 ? 16 : 8));
     // int8 codes at 3 column tiles (33-48 columns, a tree pass): one k-tile per batch (98 instead of 132 VGPRs for

@@ -74,14 +74,15 @@ __device__ __forceinline__ f16x8 biased_step(const u32x4 &t, int s) {
 // TB = k-tiles per wave whose loads are in flight together.  The SwiGLU pair at one column tile (2-16 columns) by
 // format, from a sweep of batch depth x waves x units per wave at 8 and 16 columns: int8 2 (Qwen2-1.5B gate_up
 // 10.3 -> 9.7 us at 16 columns; deeper batches hold more registers than the loads they overlap pay for), fp16 8
-// with two units per wave (Qwen2-0.5B 6.75 -> 6.34 us), int4 2.
+// with two units per wave (Qwen2-0.5B 6.75 -> 6.34 us), int4 2.  Several column tiles of int4 codes: 1 (the
+// Qwen2-7B matrices at 32 columns, 71.4 -> 67.8 us per layer over qkv, o, gate_up and down).
 template <int MT, int RG, int R> struct GemvLimits {
     static constexpr int MAX_THREADS = MT == 1 ? (R == 1 ? 1024 : 256) : 512;
 };
 // SHALLOW (several column tiles): one k-tile per batch.  Fewer registers (e.g. 132 -> 98 VGPRs for the int8 gate_up
 // pair at 3 column tiles) and so more resident waves, which the int8 matrices with short per-wave k-ranges prefer.
 template <int FMT, int MT, int RG, bool SHALLOW = false> struct GemvBatch {
-    static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : (RG == 2 ? (FMT == 1 ? 8 : 2) : 4)) : (SHALLOW ? 1 : 2);
+    static constexpr int TB = MT == 1 ? (FMT == 3 ? 2 : (RG == 2 ? (FMT == 1 ? 8 : 2) : 4)) : (SHALLOW || FMT == 3 ? 1 : 2);
 };
 
 // Lane holds D[m = mt*16 + 4g + j][n = unit*16 + r], j < 4.  Operands the epilogue reads (bias, the residual) are
