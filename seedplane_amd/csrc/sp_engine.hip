@@ -836,9 +836,11 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
     const bool one = n == 1 && !layers.empty() && gemv_pro_ok(layers[0].qkv, PRO_NORM, H, HD, one_qs, one_qw) &&
                      gemv_pro_ok(layers[0].o, PRO_COMB, H, HD);
     const bool fuse = one && !(flags & SP_F_UNFUSED);
-    // batches of one column tile: qkv in 2 k-slices (whole steps, 16 columns: Qwen2-1.5B int8 1.422 -> 1.404 ms,
-    // Qwen2-0.5B fp16 -0.8 %; the RoPE kernel then adds 2 slices instead of 8)
+    // batches of one column tile: qkv and o_proj in 2 k-slices (whole steps, 16 columns: Qwen2-1.5B int8 1.422 ->
+    // 1.404 ms for qkv, then 1.406 -> 1.398 for o_proj, Qwen2-0.5B fp16 -0.8 %; the RoPE kernel and the norm then add
+    // 2 slices instead of 8); int4 o_proj at several column tiles in 4 (Qwen2-7B at 32 columns: -0.3 %)
     const int qkv_s = one ? one_qs : (n > 1 && n <= 16 ? 2 : 0), qkv_w = one ? one_qw : 0;
+    const int o_s = n > 1 && n <= 16 ? 2 : (n > 16 && !layers.empty() && layers[0].o.fmt == 3 ? 4 : 0);
     const int down_s = one ? one_ds : 0, down_w = one ? one_dw : 0;
     float *const qpart = fuse ? gpart2 : gpart;
     float *res = x;                             // residual at the start of the layer
@@ -886,7 +888,7 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
                 hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn,
                                    NH * HD, mtp);
             pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_NONE,
-                               nullptr, 0, 0, mtp);
+                               nullptr, o_s, 0, mtp);
         }
         // Remainders where they cost nothing (one column: MFMA row 1) or where the logits need them (the qkv input,
         // above: its rounding reaches the attention scores).  Several columns would pay a second MFMA and twice the
