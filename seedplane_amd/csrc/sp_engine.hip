@@ -1005,13 +1005,15 @@ bool sp_engine::launch_d1(const sp_token &t, int flags) {
 }
 bool sp_engine::run_d1(const sp_token &t, int flags) {
     if (!launch_d1(t, flags)) return false;
-    HIPCHK(hipMemcpyAsync(h_d1err, d1_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream));
     const DevMat &hm = d.tied_head ? embed : head;
     launch_gemv(hm, EPI_STORE, xn, d.hidden, 1, logits, nullptr, d.vocab, nullptr, stream);
     if (flags & SP_F_ARGMAX) {
         hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, 1), dim3(256), 0, stream, logits, d.vocab, d.vocab, am_v, am_i);
         hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(64), 0, stream, am_v, am_i, am_out);
     }
+    // the error word's read-back goes last: a copy between the kernel and the head would delay the head (the word
+    // is checked only after a synchronisation)
+    HIPCHK(hipMemcpyAsync(h_d1err, d1_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream));
     HIPCHK(hipGetLastError());
     return true;
 }
