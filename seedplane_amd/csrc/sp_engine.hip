@@ -840,7 +840,6 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
     // 1.404 ms for qkv, then 1.406 -> 1.398 for o_proj, Qwen2-0.5B fp16 -0.8 %; the RoPE kernel and the norm then add
     // 2 slices instead of 8); int4 o_proj at several column tiles in 4 (Qwen2-7B at 32 columns: -0.3 %)
     const int qkv_s = one ? one_qs : (n > 1 && n <= 16 ? 2 : 0), qkv_w = one ? one_qw : 0;
-    const int o_s = n > 1 && n <= 16 ? 2 : (n > 16 && !layers.empty() && layers[0].o.fmt == 3 ? 4 : 0);
     const int down_s = one ? one_ds : 0, down_w = one ? one_dw : 0;
     float *const qpart = fuse ? gpart2 : gpart;
     float *res = x;                             // residual at the start of the layer
@@ -887,6 +886,7 @@ void sp_engine::step(int n, int flags, const AttnPlan &ap, int l0, int l1) {
             if (!ap.dec_direct)
                 hipLaunchKernelGGL(k_attn_combine, dim3(NH, n), dim3(HD), 0, st, attn_part, dcolnc, NH, HD, nchunk, attn,
                                    NH * HD, mtp);
+            const int o_s = n > 1 && n <= 16 ? 2 : (n > 16 && ly.o.fmt == 3 ? 4 : 0);
             pend = launch_gemv(ly.o, EPI_RESID, attn, NH * HD, n, rmid, nullptr, H, nullptr, st, gpart, ps, PRO_NONE,
                                nullptr, o_s, 0, mtp);
         }
