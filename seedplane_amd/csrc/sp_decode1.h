@@ -942,8 +942,7 @@ __global__ void __launch_bounds__(NT, 1) k_decode1(const Static *sp, Step stp) {
                         s.es[h][lane] = ex;
                         __builtin_amdgcn_wave_barrier();
                         // lane: dims DPL * lane .. DPL * lane + DPL - 1, read together (one 2- or 4-byte LDS read per
-                        // key: the loop is bound by LDS instructions, not by its FMAs); each dim's sum runs over the
-                        // keys in order
+                        // key, measured faster than one read per dim); each dim's sum runs over the keys in order
                         constexpr int DPL = HD / 64;
                         typedef std::conditional_t<DPL == 2, f16x2, f16> VT;
                         float o[DPL];
