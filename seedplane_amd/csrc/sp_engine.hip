@@ -701,9 +701,15 @@ sp_engine::AttnPlan sp_engine::plan_attention(int n, const sp_token *t, bool gra
     p.colnc.assign(n, 0);
     int mx = 1;
     if (p.mq) {
+        // 128-key blocks for tree groups of many query rows (the 33-node target pass: 198 rows); a drafter level's
+        // 8 columns (56 rows, 4 row tiles) fill more CUs with 64-key blocks (speculative step -1.2 %)
         bool trees = true;
-        for (auto &g : p.groups) trees = trees && g.tree_count > 0;
-        p.mq_ch = trees ? 128 : ATT_CH;
+        int rows = 0;
+        for (auto &g : p.groups) {
+            trees = trees && g.tree_count > 0;
+            rows = std::max(rows, g.ncols * G);
+        }
+        p.mq_ch = trees && rows >= 128 ? 128 : ATT_CH;
         for (auto &g : p.groups) {
             const int nc = (g.nlin + g.tree_count + p.mq_ch - 1) / p.mq_ch;
             for (int c = 0; c < g.ncols; ++c) p.colnc[g.first_col + c] = nc;
