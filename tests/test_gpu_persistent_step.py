@@ -113,3 +113,38 @@ def test_chain_where_the_step_does_not_apply(gpu_device):
     lg, cache = eng.forward(random_prompt(5, cfg['vocab_size'], seed=8), cache)
     eng.decode([1], [cache])
     assert eng.last_path == 0
+
+
+def test_step_argmax_takes_the_first_of_equal_logits(gpu_device):
+    """The full 151936-entry vocabulary through the persistent step, its head GEMV and the two-pass argmax: the id
+    equals torch's first-index argmax of the step's logits, and with the winning head row copied to a row of another
+    16-row unit (another head block) the two logits are bit-equal and the lower row wins (torch.argmax and
+    sampler.hpp:98-99 keep the first maximal index)."""
+    print('persistent step: argmax ties, full vocabulary', flush=True)
+    cfg, w = make_weights(preset('qwen2-1.5b', num_hidden_layers=2), 'q8', seed=45)
+    V = cfg['vocab_size']
+    prompt = random_prompt(5, V, seed=3)
+
+    def one_step(tensors):
+        eng = Qwen2Engine(config=cfg, tensors=tensors, max_tokens=4)
+        eng.reserve(1, eng.slots_for(64, None))
+        cache = eng.new_cache(64)
+        eng.prefill([prompt], [cache])
+        buf = torch.empty((1, V), dtype=torch.float32, device=eng.device)
+        tid = _step(eng, cache, 7, 0, buf)
+        assert eng.last_path == 1
+        return tid, buf[0].cpu()
+
+    tid, row = one_step(w)
+    assert tid == int(torch.argmax(row))
+    head = 'lm_head' if 'lm_head.qweight' in w else 'model.embed_tokens'
+    # a row of another 16-row unit, below the winner when there is room (it must then win), else above (it must lose)
+    k = tid // 2 if tid >= 32 else tid + 1000
+    w2 = dict(w)
+    for part in ('qweight', 'scales'):
+        t = w[f'{head}.{part}'].clone()
+        t[k] = t[tid]
+        w2[f'{head}.{part}'] = t
+    tid2, row2 = one_step(w2)
+    assert float(row2[k]) == float(row2[tid])
+    assert tid2 == min(k, tid) == int(torch.argmax(row2))
